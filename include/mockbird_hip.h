@@ -1,0 +1,176 @@
+/*
+ * mockbird_hip.h -- C ABI of the MI355X (gfx950) decoder hot path for
+ * MOSS-TTS-Nano: KV ring append with RoPE on K, ring-aware single-query decode
+ * attention, causal prefill attention, and the QKV/O projections around them.
+ *
+ * This is the drop-in boundary.  The host engine (GpuTtsEngine / PrefillRunner /
+ * DecodeRunner in the reference, src/lib/tts/engine/gpu.ts:65-92,
+ * prefill.ts:114-674, decode.ts:201-1046) binds these entry points through a
+ * thin N-API addon; every signature uses plain pointers and sizes.
+ *
+ * Conventions
+ *  - Every call returns MB_OK (0) or an MB_ERR_* code; mb_last_error(ctx)
+ *    returns the message of the last failing call on that context.
+ *  - Host-pointer calls (no suffix) copy in, run on the context's stream and
+ *    synchronise before returning, like the reference's submit + mapAsync.
+ *  - `_dev` calls take device pointers, enqueue on the context's stream and
+ *    return without synchronising (for callers that keep data in HBM).
+ *  - Sequences ("voices") are addressed 0 .. max_seqs-1; a batched call with
+ *    B sequences works on sequences 0 .. B-1.
+ *  - Fused QKV rows are [2304] = q | k | v, each 768 wide, head-major
+ *    (head*64 + dim) as the exported graph lays them out (kernels-batch.ts:1-15).
+ *  - Ring semantics (kernels-decode.ts:679-714 and :590-667): a row at
+ *    absolute position pos is written to slot pos mod capacity, the slot
+ *    records pos, and a query at position cur sees exactly the slots whose
+ *    stored position p satisfies 0 <= cur - p < capacity.  With
+ *    mb_config.wrap == 0 the reference's non-wrapping global ring is kept
+ *    instead: slot == pos and pos >= capacity is MB_ERR_RANGE
+ *    (decode.ts:719-724).
+ *  - Attention scale is 0.125 (1/sqrt(64)); RoPE pairs (2i, 2i+1) at
+ *    frequency 10000^(-2i/64), out[2i] = x[2i] cos - x[2i+1] sin,
+ *    out[2i+1] = x[2i+1] cos + x[2i] sin (kernels-decode.ts:204-241).
+ *
+ * Not thread-safe per context: calls on one context must not overlap.
+ */
+#ifndef MOCKBIRD_HIP_H
+#define MOCKBIRD_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MB_ABI_VERSION 1
+
+enum {
+  MB_OK = 0,
+  MB_ERR_ARG = 1,       /* bad argument (null pointer, size out of range, unknown name) */
+  MB_ERR_RANGE = 2,     /* position does not fit a non-wrapping ring (decode.ts:719-724) */
+  MB_ERR_HIP = 3,       /* a HIP runtime call failed */
+  MB_ERR_STATE = 4,     /* call out of order (e.g. a weight is missing) */
+  MB_ERR_CANCELLED = 5, /* mb_cancel() was observed between layers */
+  MB_ERR_NOMEM = 6      /* device allocation failed */
+};
+
+enum { MB_KV_F32 = 0, MB_KV_BF16 = 1 };
+enum { MB_DT_F32 = 0, MB_DT_BF16 = 1 };
+
+typedef struct mb_config {
+  int32_t n_layers;   /* global transformer layers (12) */
+  int32_t vocab;      /* rows of the text embedding / columns of the text head */
+  int32_t capacity;   /* KV ring slots per sequence and layer (C) */
+  int32_t max_seqs;   /* sequences (voices) the context holds rings for */
+  int32_t max_rows;   /* most prompt rows one prefill call may carry per sequence */
+  int32_t kv_dtype;   /* MB_KV_F32 or MB_KV_BF16 (round-to-nearest-even on store) */
+  int32_t wrap;       /* 1: slot = pos mod C; 0: the reference's non-wrapping ring */
+  int32_t device;     /* HIP device ordinal */
+} mb_config;
+
+typedef struct mb_ctx mb_ctx;
+
+/* ---------------------------------------------------------------- context */
+
+int mb_abi_version(void);
+
+/* Create a context: allocates the rings (every slot empty) and activations.
+ * Replaces the device + buffer set-up of createGpuEngineFor (gpu.ts:316-388)
+ * and the PrefillRunner / DecodeRunner constructors (prefill.ts:128-167,
+ * decode.ts:255-290). */
+int mb_create(const mb_config* cfg, mb_ctx** out);
+/* Free everything (gpu.ts:283-291 dispose). */
+void mb_destroy(mb_ctx* ctx);
+const char* mb_last_error(const mb_ctx* ctx);
+/* Launch on `hip_stream` (a hipStream_t) instead of the context's own stream;
+ * NULL restores the context's own stream. */
+int mb_set_stream(mb_ctx* ctx, void* hip_stream);
+void* mb_get_stream(mb_ctx* ctx);
+int mb_synchronize(mb_ctx* ctx);
+/* Device bytes held by the context (rings + activations + weights). */
+int64_t mb_device_bytes(const mb_ctx* ctx);
+
+/* Copy one fp32 tensor in by name (uploadWeights, weights.ts:44-119).  Names
+ * follow the exported graph: core.model.transformer.h.{i}.{ln_1,ln_2}.{weight,
+ * bias}, .attn.c_attn.{weight,bias} [768,2304], .attn.c_proj.* [768,768],
+ * .mlp.fc_in.* [768,3072], .mlp.fc_out.* [3072,768],
+ * core.model.transformer.ln_f.*, core.model.transformer.wte.weight
+ * [vocab,768], core.model.audio_embeddings.{k}.weight [1024,768],
+ * model.local_transformer.h.0.* and model.local_transformer.ln_f.* (same
+ * shapes), model.text_lm_head.weight [768,vocab],
+ * model.audio_lm_heads.{k}.weight [768,1024].  Matrices are [K, N] row-major
+ * as in the graph (no transposition, doc section 9.1). */
+int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int64_t* dims,
+                     int ndims);
+
+/* Request cancellation: the next layer boundary of a running or later model
+ * call returns MB_ERR_CANCELLED (the reference polls isCancelled() per frame,
+ * runtime.ts:506, :541).  mb_cancel(ctx, 0) clears the request. */
+int mb_cancel(mb_ctx* ctx, int on);
+
+/* ------------------------------------------------------------------- ring */
+
+/* Empty the rings of `n` sequences (seq_ids; n < 0 means every sequence) on
+ * every layer: all slots forget their position (engine.reset, gpu.ts:237-242,
+ * codec.ts:279-282). */
+int mb_ring_reset(mb_ctx* ctx, int n, const int32_t* seq_ids);
+
+/* Fill K and V of slots [0, n_slots) of (layer, seq) with `sentinel` (rounded
+ * to bf16 for bf16 rings) without touching slot positions: the warm-up
+ * read-back probe of PrefillRunner.poisonKv (prefill.ts:610-620). */
+int mb_ring_poison(mb_ctx* ctx, int layer, int seq, int n_slots, float sentinel);
+
+/* Read slots [slot0, slot0+n) of (layer, seq) into the reference layout:
+ * k, v [n][768] fp32 (head*64 + dim; bf16 widened exactly) and slot_pos[n]
+ * (absolute position or -1).  Any output may be NULL.  Replaces
+ * PrefillRunner.readLayerCache (prefill.ts:661-673). */
+int mb_read_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, float* k, float* v,
+                 int32_t* slot_pos);
+
+/* Append one row per sequence b < B at absolute position pos[b]: q is roped
+ * into q_out[b][768], K = rope(k) and V = v are stored at slot pos mod C of
+ * `layer`, and the slot records pos.  qkv is [B][2304].
+ * Replaces ROPE_SPLIT_RING (kernels-decode.ts:216-241, dispatched at
+ * decode.ts:527-535) with the wrap rule of ROPE_SPLIT_CODEC (:679-714). */
+int mb_ring_append(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_t* pos,
+                   float* q_out);
+
+/* Write n_rows[b] consecutive rows per sequence, starting at pos0[b]:
+ * qkv [B][rows_max][2304] -> roped q_out [B][rows_max][768] plus K/V into the
+ * ring.  The prefill form of the append: ROPE_SPLIT_CACHE
+ * (kernels-batch.ts:194-234, prefill.ts:424-432) with pos0 = 0. */
+int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float* qkv,
+                       const int32_t* pos0, const int32_t* n_rows, float* q_out);
+
+/* Single-query decode attention for sequences b < B: q[b][768] (roped) at
+ * position pos[b] over the live slots of `layer`; out[b][768].
+ * Replaces ATTEND_RING (kernels-decode.ts:254-327, decode.ts:536-552) with the
+ * live-slot mask of ATTEND_RING_CODEC (kernels-decode.ts:590-667). */
+int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int32_t* pos,
+                        float* out);
+
+/* Causal prefill attention: q [B][rows_max][768] (roped) for rows r < n_rows[b]
+ * at positions pos0[b] + r, each attending the live slots of `layer` whose
+ * position is <= its own; out [B][rows_max][768].  Replaces ATTENTION_SCORES /
+ * _SOFTMAX / _APPLY (kernels-batch.ts:246-350, prefill.ts:434-462). */
+int mb_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const float* q,
+                         const int32_t* pos0, const int32_t* n_rows, float* out);
+
+/* ---- device-pointer forms (enqueue only; shapes and meaning as above) ----
+ * qkv_dtype / q_dtype select MB_DT_F32 or MB_DT_BF16 inputs; row strides are
+ * in elements.  max_pos bounds every pos (pass capacity - 1 or larger when
+ * unknown): it sizes the attention split without reading device memory. */
+int mb_ring_append_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
+                       int64_t qkv_stride, const int32_t* pos, float* q_out, int64_t q_stride);
+int mb_ring_write_rows_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* qkv,
+                           int qkv_dtype, const int32_t* pos0, const int32_t* n_rows, void* q_out,
+                           int q_dtype);
+int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
+                            const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride);
+int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
+                             int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOCKBIRD_HIP_H */

@@ -1,0 +1,240 @@
+"""mockbird_amd -- MI355X (gfx950) decoder hot path for MOSS-TTS-Nano.
+
+The product is the C-ABI library ``libmockbird_hip.so`` (include/mockbird_hip.h)
+built from ``csrc/``.  This module is the Python view of that ABI used by the
+tests and the benchmark: it loads the in-tree library with ctypes and fails
+loudly when it is missing -- there is no CPU fallback.  The JavaScript host
+(``engine/``) binds the same ABI through the N-API addon.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libmockbird_hip.so")
+
+MB_OK, MB_ERR_ARG, MB_ERR_RANGE, MB_ERR_HIP, MB_ERR_STATE, MB_ERR_CANCELLED, MB_ERR_NOMEM = range(7)
+MB_KV_F32, MB_KV_BF16 = 0, 1
+MB_DT_F32, MB_DT_BF16 = 0, 1
+D, H, HD, QKV, FFN, NVQ, ROW, PAD, CODES = 768, 12, 64, 2304, 3072, 16, 17, 1024, 1024
+
+#: every symbol include/mockbird_hip.h declares (checked by the CPU tests)
+EXPORTS = (
+    "mb_abi_version", "mb_create", "mb_destroy", "mb_last_error", "mb_set_stream",
+    "mb_get_stream", "mb_synchronize", "mb_device_bytes", "mb_upload_tensor", "mb_cancel",
+    "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_ring_append", "mb_ring_write_rows",
+    "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
+    "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
+)
+
+
+class MbError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[mb error {code}] {msg}")
+        self.code = code
+
+
+class Config(C.Structure):
+    _fields_ = [
+        ("n_layers", C.c_int32), ("vocab", C.c_int32), ("capacity", C.c_int32),
+        ("max_seqs", C.c_int32), ("max_rows", C.c_int32), ("kv_dtype", C.c_int32),
+        ("wrap", C.c_int32), ("device", C.c_int32),
+    ]
+
+
+_lib = None
+_vp, _i32, _i64, _f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_float
+
+
+def load():
+    """Load libmockbird_hip.so (built by mockbird_amd.build); raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m mockbird_amd.build` "
+            "(the HIP library is the only implementation; there is no fallback)")
+    L = C.CDLL(LIB_PATH)
+    sig = {
+        "mb_abi_version": ([], C.c_int),
+        "mb_create": ([C.POINTER(Config), C.POINTER(_vp)], C.c_int),
+        "mb_destroy": ([_vp], None),
+        "mb_last_error": ([_vp], C.c_char_p),
+        "mb_set_stream": ([_vp, _vp], C.c_int),
+        "mb_get_stream": ([_vp], _vp),
+        "mb_synchronize": ([_vp], C.c_int),
+        "mb_device_bytes": ([_vp], _i64),
+        "mb_upload_tensor": ([_vp, C.c_char_p, _vp, _vp, C.c_int], C.c_int),
+        "mb_cancel": ([_vp, C.c_int], C.c_int),
+        "mb_ring_reset": ([_vp, C.c_int, _vp], C.c_int),
+        "mb_ring_poison": ([_vp, C.c_int, C.c_int, C.c_int, _f32], C.c_int),
+        "mb_read_ring": ([_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_ring_append": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_ring_write_rows": ([_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+        "mb_decode_attention": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_prefill_attention": ([_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+        "mb_ring_append_dev": ([_vp, C.c_int, C.c_int, _vp, C.c_int, _i64, _vp, _vp, _i64], C.c_int),
+        "mb_ring_write_rows_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp,
+                                    C.c_int], C.c_int),
+        "mb_decode_attention_dev": ([_vp, C.c_int, C.c_int, _vp, _i64, _vp, _i32, _vp, _i64],
+                                    C.c_int),
+        "mb_prefill_attention_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp],
+                                     C.c_int),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _ptr(a: np.ndarray | None):
+    return None if a is None else a.ctypes.data
+
+
+def _f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i32c(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class Context:
+    """One mb_ctx: rings for `max_seqs` sequences on one GPU."""
+
+    def __init__(self, n_layers: int = 12, capacity: int = 1024, max_seqs: int = 1,
+                 max_rows: int = 512, kv_dtype: int = MB_KV_F32, wrap: bool = True,
+                 vocab: int = 32000, device: int = 0):
+        self.lib = load()
+        self.cfg = Config(n_layers, vocab, capacity, max_seqs, max_rows, kv_dtype, int(wrap), device)
+        h = _vp()
+        rc = self.lib.mb_create(C.byref(self.cfg), C.byref(h))
+        if rc != MB_OK:
+            raise MbError(rc, "mb_create failed (see stderr)")
+        self.h = h
+
+    # -- plumbing
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.mb_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def check(self, rc: int):
+        if rc != MB_OK:
+            raise MbError(rc, self.lib.mb_last_error(self.h).decode())
+
+    @property
+    def capacity(self):
+        return self.cfg.capacity
+
+    def set_stream(self, stream_handle: int | None):
+        self.check(self.lib.mb_set_stream(self.h, stream_handle))
+
+    def synchronize(self):
+        self.check(self.lib.mb_synchronize(self.h))
+
+    def device_bytes(self) -> int:
+        return self.lib.mb_device_bytes(self.h)
+
+    def upload(self, name: str, arr: np.ndarray):
+        a = _f32c(arr)
+        dims = (C.c_int64 * a.ndim)(*a.shape)
+        self.check(self.lib.mb_upload_tensor(self.h, name.encode(), a.ctypes.data, dims, a.ndim))
+
+    def upload_all(self, weights: dict):
+        for k, v in weights.items():
+            self.upload(k, v)
+
+    def cancel(self, on: bool = True):
+        self.check(self.lib.mb_cancel(self.h, int(on)))
+
+    # -- ring
+    def ring_reset(self, seq_ids=None):
+        if seq_ids is None:
+            self.check(self.lib.mb_ring_reset(self.h, -1, None))
+        else:
+            s = _i32c(seq_ids)
+            self.check(self.lib.mb_ring_reset(self.h, s.size, s.ctypes.data))
+
+    def ring_poison(self, layer: int, seq: int, n_slots: int, sentinel: float = -12345.5):
+        self.check(self.lib.mb_ring_poison(self.h, layer, seq, n_slots, sentinel))
+
+    def read_ring(self, layer: int, seq: int, slot0: int = 0, n: int | None = None):
+        n = self.capacity - slot0 if n is None else n
+        k = np.zeros((n, D), np.float32)
+        v = np.zeros((n, D), np.float32)
+        sp = np.zeros(n, np.int32)
+        self.check(self.lib.mb_read_ring(self.h, layer, seq, slot0, n, k.ctypes.data, v.ctypes.data,
+                                         sp.ctypes.data))
+        return k, v, sp
+
+    def ring_append(self, layer: int, qkv: np.ndarray, pos) -> np.ndarray:
+        qkv, pos = _f32c(qkv), _i32c(pos)
+        B = qkv.shape[0]
+        q = np.zeros((B, D), np.float32)
+        self.check(self.lib.mb_ring_append(self.h, layer, B, qkv.ctypes.data, pos.ctypes.data,
+                                           q.ctypes.data))
+        return q
+
+    def ring_write_rows(self, layer: int, qkv: np.ndarray, pos0, n_rows) -> np.ndarray:
+        qkv, pos0, n_rows = _f32c(qkv), _i32c(pos0), _i32c(n_rows)
+        B, R = qkv.shape[0], qkv.shape[1]
+        q = np.zeros((B, R, D), np.float32)
+        self.check(self.lib.mb_ring_write_rows(self.h, layer, B, R, qkv.ctypes.data,
+                                               pos0.ctypes.data, n_rows.ctypes.data, q.ctypes.data))
+        return q
+
+    def decode_attention(self, layer: int, q: np.ndarray, pos) -> np.ndarray:
+        q, pos = _f32c(q), _i32c(pos)
+        out = np.zeros((q.shape[0], D), np.float32)
+        self.check(self.lib.mb_decode_attention(self.h, layer, q.shape[0], q.ctypes.data,
+                                                pos.ctypes.data, out.ctypes.data))
+        return out
+
+    def prefill_attention(self, layer: int, q: np.ndarray, pos0, n_rows) -> np.ndarray:
+        q, pos0, n_rows = _f32c(q), _i32c(pos0), _i32c(n_rows)
+        B, R = q.shape[0], q.shape[1]
+        out = np.zeros((B, R, D), np.float32)
+        self.check(self.lib.mb_prefill_attention(self.h, layer, B, R, q.ctypes.data,
+                                                 pos0.ctypes.data, n_rows.ctypes.data,
+                                                 out.ctypes.data))
+        return out
+
+    # -- device-pointer forms (integer device addresses, e.g. torch tensor.data_ptr())
+    def ring_append_dev(self, layer, B, qkv_ptr, pos_ptr, q_ptr, qkv_dtype=MB_DT_F32,
+                        qkv_stride=QKV, q_stride=D):
+        self.check(self.lib.mb_ring_append_dev(self.h, layer, B, qkv_ptr, qkv_dtype, qkv_stride,
+                                               pos_ptr, q_ptr, q_stride))
+
+    def ring_write_rows_dev(self, layer, B, rows_max, qkv_ptr, pos0_ptr, n_ptr, q_ptr,
+                            qkv_dtype=MB_DT_F32, q_dtype=MB_DT_F32):
+        self.check(self.lib.mb_ring_write_rows_dev(self.h, layer, B, rows_max, qkv_ptr, qkv_dtype,
+                                                   pos0_ptr, n_ptr, q_ptr, q_dtype))
+
+    def decode_attention_dev(self, layer, B, q_ptr, pos_ptr, max_pos, out_ptr, q_stride=D,
+                             out_stride=D):
+        self.check(self.lib.mb_decode_attention_dev(self.h, layer, B, q_ptr, q_stride, pos_ptr,
+                                                    max_pos, out_ptr, out_stride))
+
+    def prefill_attention_dev(self, layer, B, rows_max, q_ptr, pos0_ptr, n_ptr, out_ptr,
+                              q_dtype=MB_DT_F32):
+        self.check(self.lib.mb_prefill_attention_dev(self.h, layer, B, rows_max, q_ptr, q_dtype,
+                                                     pos0_ptr, n_ptr, out_ptr))

@@ -1,0 +1,98 @@
+"""Build libmockbird_hip.so (gfx950) and the Node N-API addon in-tree.
+
+    python -m mockbird_amd.build            # library + addon
+    python -m mockbird_amd.build --lib-only
+
+hipcc compiles each csrc/*.hip file for gfx950 only; objects go to
+mockbird_amd/_build/ and the shared library to mockbird_amd/libmockbird_hip.so.
+Packed fp32 instructions are disabled on every HIP compile line.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+BUILD = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libmockbird_hip.so")
+ADDON = os.path.join(PKG, "engine", "mockbird_hip.node")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+
+HIP_FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function", "-Wno-unused-result",
+    "-I", os.path.join(ROOT, "include"),
+]
+
+
+def _run(cmd: list[str]) -> None:
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
+        raise RuntimeError(f"compile failed: {cmd[-1] if cmd else ''}")
+    if r.stderr.strip():
+        # keep warnings visible, minus hipcc's host-pass note about the packed-fp32 feature
+        lines = [ln for ln in r.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        if any(ln.strip() for ln in lines):
+            sys.stderr.write("\n".join(lines) + "\n")
+
+
+def build_lib(jobs: int = 8) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    objs = []
+    cmds = []
+    for src in sources:
+        obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(cmds))) as ex:
+        list(ex.map(_run, cmds))
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,
+          f"-Wl,-rpath,{ROCM}/lib"])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_addon() -> str | None:
+    """The N-API addon links libmockbird_hip.so by rpath $ORIGIN/.."""
+    src = os.path.join(CSRC, "napi", "mb_napi.cc")
+    if not os.path.exists(src):
+        return None
+    node_inc = "/usr/include/node"
+    if not os.path.exists(os.path.join(node_inc, "node_api.h")):
+        sys.stderr.write("node_api.h not found; skipping the N-API addon\n")
+        return None
+    tmp = ADDON + ".tmp"
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-I", node_inc,
+          "-I", os.path.join(ROOT, "include"), src, "-o", tmp, "-L", PKG, "-lmockbird_hip",
+          "-Wl,-rpath,$ORIGIN/..", "-Wl,--allow-shlib-undefined"])
+    os.replace(tmp, ADDON)
+    return ADDON
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--lib-only", action="store_true")
+    ap.add_argument("-j", type=int, default=8)
+    a = ap.parse_args(argv)
+    print(build_lib(a.j))
+    if not a.lib_only:
+        addon = build_addon()
+        if addon:
+            print(addon)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

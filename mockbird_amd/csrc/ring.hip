@@ -1,0 +1,422 @@
+// KV ring kernels for gfx950: RoPE + ring write (append / prefill rows) and
+// the split-softmax single-query attention over a wrapping ring.
+//
+// Ring layout in HBM (per layer, sequence and head, slots contiguous):
+//   K[(((layer * max_seqs + seq) * 12 + head) * C + slot) * 64 + dim]
+// so one (sequence, head) window is one contiguous run of C * 64 elements and
+// a wave streams it with 16-byte loads; the reference's [slot][head*64+dim]
+// order (prefill.ts:55-56) is produced only on read-back.
+#include "mb_internal.h"
+#include "kv_types.h"
+
+namespace mb {
+
+// fp32 inverse frequencies of the exported graph (torch's fp32 values of
+// 1 / 10000^(2i/64)); six entries sit one ulp away from the correctly rounded
+// value, and the reference's ORT K fixture fixes which.
+__constant__ uint32_t c_inv_freq_bits[32] = {
+    0x3f800000u, 0x3f3ff911u, 0x3f0ff59au, 0x3ed7e89bu, 0x3ea1e89bu, 0x3e72d423u,
+    0x3e361887u, 0x3e088d77u, 0x3dcccccdu, 0x3d99940du, 0x3d6655c2u, 0x3d2cba15u,
+    0x3d0186e3u, 0x3cc2434fu, 0x3c91ad39u, 0x3c5a7bf2u, 0x3c23d70au, 0x3bf5b9b0u,
+    0x3bb8449cu, 0x3b8a2e77u, 0x3b4f3e38u, 0x3b1b690du, 0x3ae91528u, 0x3aaec98eu,
+    0x3a83126fu, 0x3a44948cu, 0x3a136a16u, 0x39dd1725u, 0x39a5cb60u, 0x3978a815u,
+    0x393a7753u, 0x390bd472u};
+
+// ------------------------------------------------------------------ fills
+
+__global__ void k_fill_i32(int32_t* __restrict__ p, int64_t n, int32_t value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = value;
+}
+
+template <bool BF16>
+__global__ void k_fill_kv(void* __restrict__ p, int64_t n, float value) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    if (BF16)
+      ((uint16_t*)p)[i] = f32_to_bf16(value);
+    else
+      ((float*)p)[i] = value;
+  }
+}
+
+static int grid_for(int64_t n, int block) {
+  int64_t g = (n + block - 1) / block;
+  if (g > 65536) g = 65536;
+  return (int)(g < 1 ? 1 : g);
+}
+
+int launch_fill_i32(mb_ctx* ctx, int32_t* p, int64_t n, int32_t value) {
+  if (n <= 0) return MB_OK;
+  hipLaunchKernelGGL(k_fill_i32, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, p, n, value);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value) {
+  if (n <= 0) return MB_OK;
+  if (ctx->cfg.kv_dtype == MB_KV_BF16)
+    hipLaunchKernelGGL(k_fill_kv<true>, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, p, n,
+                       value);
+  else
+    hipLaunchKernelGGL(k_fill_kv<false>, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, p, n,
+                       value);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// ------------------------------------------------------------ RoPE + write
+
+// cos/sin of pair `i` at absolute position `pos`: the angle is the fp32
+// product float(pos) * inv_freq[i] (as the graph's fp32 Einsum forms it), and
+// cos/sin of that fp32 angle are evaluated in double and rounded to fp32.
+__device__ __forceinline__ void rope_cs(int32_t pos, int i, float& c, float& s) {
+  const float a = __fmul_rn((float)pos, __uint_as_float(c_inv_freq_bits[i]));
+  double sd, cd;
+  sincos((double)a, &sd, &cd);
+  c = (float)cd;
+  s = (float)sd;
+}
+
+// One rotated pair, evaluated as the graph does it: fp32 Mul, Mul, Add with
+// rotate_half(x) = (-x1, x0) -- never fused into an FMA.
+__device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& o0,
+                                          float& o1) {
+#pragma clang fp contract(off)
+  o0 = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
+  o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
+}
+
+// Each thread owns 8 consecutive dims (4 RoPE pairs) of one head of one row:
+// 96 threads per row.  It reads q, k, v (2 x 16 B each for fp32 input),
+// writes the roped q, the roped K and the raw V into the ring with 16-byte
+// stores (bf16: one 16-byte store each), and the head-0 / dims-0 thread
+// records the slot's position.  Rows with r >= n_rows[b], negative positions
+// or (non-wrapping ring) pos >= C are skipped; the host rejects them first.
+// With more than C rows in one call only the last C reach the ring.
+template <bool IN_BF16, bool KV_BF16, bool Q_BF16>
+__global__ __launch_bounds__(256) void k_ring_write(
+    const void* __restrict__ qkv, int64_t qkv_row_stride, int64_t qkv_seq_stride,
+    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows_max, int B,
+    void* __restrict__ q_out, int64_t q_row_stride, int64_t q_seq_stride,
+    void* __restrict__ ring_k, void* __restrict__ ring_v, int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, int wrap) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row_id = t / 96;
+  if (row_id >= (int64_t)B * rows_max) return;
+  const int part = (int)(t % 96), head = part >> 3, d0 = (part & 7) * 8;
+  const int b = (int)(row_id / rows_max), r = (int)(row_id % rows_max);
+  const int n = n_rows ? n_rows[b] : 1;
+  if (r >= n) return;
+  const int64_t p64 = (int64_t)pos0[b] + r;
+  if (p64 < 0 || p64 > INT32_MAX || (!wrap && p64 >= C)) return;
+  const int32_t pos = (int32_t)p64;
+  const int slot = wrap ? (int)(p64 % C) : (int)p64;
+
+  float q[8], k[8], v[8];
+  const int64_t roff = (int64_t)b * qkv_seq_stride + (int64_t)r * qkv_row_stride + head * HD + d0;
+  load8<IN_BF16>(qkv, roff, q);
+  load8<IN_BF16>(qkv, roff + D, k);
+  load8<IN_BF16>(qkv, roff + 2 * D, v);
+
+  float qo[8], ko[8];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    float c, s;
+    rope_cs(pos, (d0 >> 1) + j, c, s);
+    rope_pair(q[2 * j], q[2 * j + 1], c, s, qo[2 * j], qo[2 * j + 1]);
+    rope_pair(k[2 * j], k[2 * j + 1], c, s, ko[2 * j], ko[2 * j + 1]);
+  }
+  if (q_out) store8<Q_BF16>(q_out, (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + head * HD + d0, qo);
+  // a row that a later row of the same call overwrites is never stored, so
+  // every slot is written at most once per call (deterministic contents)
+  if (n > C && r < n - C) return;
+  const int64_t koff = (int64_t)b * ring_seq_stride + ((int64_t)head * C + slot) * HD + d0;
+  store8<KV_BF16>(ring_k, koff, ko);
+  store8<KV_BF16>(ring_v, koff, v);
+  if (part == 0) slot_pos[(int64_t)b * C + slot] = pos;
+}
+
+int launch_ring_write(mb_ctx* ctx, int layer, int B, int rows_max, const void* qkv, int qkv_dtype,
+                      int64_t qkv_row_stride, int64_t qkv_seq_stride, const int32_t* pos0,
+                      const int32_t* n_rows, void* q_out, int q_dtype, int64_t q_row_stride,
+                      int64_t q_seq_stride) {
+  const int64_t threads = (int64_t)B * rows_max * 96;
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many rows in one call");
+  const size_t e = kv_elem_bytes(ctx);
+  void* rk = (char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
+  void* rv = (char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
+  int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
+  const int64_t rs = (int64_t)H * ctx->cfg.capacity * HD;
+  const bool in_bf16 = qkv_dtype == MB_DT_BF16, kv_bf16 = ctx->cfg.kv_dtype == MB_KV_BF16,
+             q_bf16 = q_dtype == MB_DT_BF16;
+#define MB_RW(A, Bq, Cq)                                                                        \
+  hipLaunchKernelGGL((k_ring_write<A, Bq, Cq>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, \
+                     qkv, qkv_row_stride, qkv_seq_stride, pos0, n_rows, rows_max, B, q_out,      \
+                     q_row_stride, q_seq_stride, rk, rv, sp, rs, ctx->cfg.capacity, ctx->cfg.wrap)
+  if (in_bf16) {
+    if (kv_bf16) { if (q_bf16) MB_RW(true, true, true); else MB_RW(true, true, false); }
+    else { if (q_bf16) MB_RW(true, false, true); else MB_RW(true, false, false); }
+  } else {
+    if (kv_bf16) { if (q_bf16) MB_RW(false, true, true); else MB_RW(false, true, false); }
+    else { if (q_bf16) MB_RW(false, false, true); else MB_RW(false, false, false); }
+  }
+#undef MB_RW
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// ------------------------------------------------------- decode attention
+
+// Sum over aligned groups of LR lanes (8 or 16) with DPP row permutes:
+// quad swaps (xor 1, xor 2), then the half-row mirror (lane i <-> 7-i) and,
+// for 16, the row mirror (lane i <-> 15-i).  Every lane of the group ends
+// with the same sum (each step adds two values that are equal across pairs).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                              0xF, 0xF, false));
+}
+template <int LR>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  x += dpp<0x141>(x);  // row_half_mirror
+  if (LR == 16) x += dpp<0x140>(x);  // row_mirror
+  return x;
+}
+
+// Merge two online-softmax states (m, l, acc[]) in place.
+template <int VD>
+__device__ __forceinline__ void merge_state(float& m, float& l, float* acc, float mo, float lo,
+                                            const float* acco) {
+  const float mn = fmaxf(m, mo);
+  if (mn == -INFINITY) return;  // both empty
+  const float sa = __expf(m - mn), sb = __expf(mo - mn);
+  l = l * sa + lo * sb;
+#pragma unroll
+  for (int i = 0; i < VD; i++) acc[i] = acc[i] * sa + acco[i] * sb;
+  m = mn;
+}
+
+// One wave per (query, head, split).  A query is row r of sequence b at
+// position cur = pos0[b] + r; it attends the slots of its ring whose stored
+// position p satisfies 0 <= cur - p < C (kernels-decode.ts:608-611), which
+// are all inside physical slots [0, min(cur + 1, C)).  Split `s` covers
+// slots [s * split_len, (s + 1) * split_len) of that range.
+//
+// Lane layout: LR = 64 / VD lanes hold one 64-dim row (VD dims each, one
+// 16-byte load), so a wave covers G = VD slots per load; U loads of K and V
+// are issued before any is used.  Scores are reduced across the LR lanes with
+// DPP; each lane group keeps its own online-softmax state (max, sum, VD
+// accumulators) and the G groups are merged with cross-row shuffles at the
+// end.  One split writes its normalised row directly; several write partials
+// (acc[64], max, sum) that k_attn_combine folds.
+template <bool KV_BF16, int U>
+__global__ __launch_bounds__(256) void k_attn_split(
+    const float* __restrict__ q, int64_t q_row_stride, int64_t q_seq_stride,
+    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows,
+    const void* __restrict__ ring_k, const void* __restrict__ ring_v,
+    const int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, int split_len,
+    int nsplit, float* __restrict__ part, float* __restrict__ out, int64_t out_row_stride,
+    int64_t out_seq_stride) {
+  constexpr int VD = KV_BF16 ? 8 : 4;
+  constexpr int LR = 64 / VD;
+  constexpr int G = VD;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int head = blockIdx.y * 4 + wave;
+  const int qidx = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
+  const int b = qidx / rows, r = qidx % rows;
+  if (n_rows && r >= n_rows[b]) return;  // uniform per wave; no barriers in this kernel
+  const int g = lane / LR, sub = lane % LR;
+  const int64_t cur = (int64_t)pos0[b] + r;
+  const int nvalid = cur < 0 ? 0 : (int)(cur + 1 < C ? cur + 1 : C);
+  const int s0 = split * split_len;
+  const int s1 = min(s0 + split_len, nvalid);
+
+  float qv[VD];
+  {
+    const float* qp = q + (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + head * HD + sub * VD;
+#pragma unroll
+    for (int i = 0; i < VD; i += 4) {
+      const float4 t = *(const float4*)(qp + i);
+      // 0.125 = 2^-3: pre-scaling q is exact
+      qv[i] = t.x * 0.125f; qv[i + 1] = t.y * 0.125f; qv[i + 2] = t.z * 0.125f; qv[i + 3] = t.w * 0.125f;
+    }
+  }
+  const int64_t hoff = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
+  const int32_t* sp = slot_pos + (int64_t)b * C;
+
+  float m = -INFINITY, l = 0.f, acc[VD];
+#pragma unroll
+  for (int i = 0; i < VD; i++) acc[i] = 0.f;
+
+  for (int base = s0; base < s1; base += G * U) {
+    uint4 kr[U], vr[U];
+    int spv[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int slot = base + u * G + g;
+      ok[u] = slot < s1;
+      const int sl = ok[u] ? slot : s0;
+      kr[u] = *(const uint4*)((const char*)ring_k + (hoff + (int64_t)sl * HD) * (KV_BF16 ? 2 : 4));
+      vr[u] = *(const uint4*)((const char*)ring_v + (hoff + (int64_t)sl * HD) * (KV_BF16 ? 2 : 4));
+      spv[u] = sp[sl];
+    }
+    float sc[U];
+    float mx = m;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      float kf[VD];
+      unpack<KV_BF16>(kr[u], kf);
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
+      dot = group_sum<LR>(dot);
+      const int64_t dlt = cur - spv[u];
+      const bool live = ok[u] && spv[u] >= 0 && dlt >= 0 && dlt < C;
+      sc[u] = live ? dot : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
+    }
+    if (mx == -INFINITY) continue;  // nothing live yet in this lane group
+    const float scale = __expf(m - mx);
+    l *= scale;
+#pragma unroll
+    for (int i = 0; i < VD; i++) acc[i] *= scale;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float p = __expf(sc[u] - mx);
+      l += p;
+      float vf[VD];
+      unpack<KV_BF16>(vr[u], vf);
+#pragma unroll
+      for (int i = 0; i < VD; i++) acc[i] = fmaf(p, vf[i], acc[i]);
+    }
+    m = mx;
+  }
+
+  // fold the G lane groups: lanes sub, sub+LR, sub+2LR, ... hold the same dims
+#pragma unroll
+  for (int off = LR; off < 64; off <<= 1) {
+    const float mo = __shfl_xor(m, off);
+    const float lo = __shfl_xor(l, off);
+    float ao[VD];
+#pragma unroll
+    for (int i = 0; i < VD; i++) ao[i] = __shfl_xor(acc[i], off);
+    merge_state<VD>(m, l, acc, mo, lo, ao);
+  }
+  if (g != 0) return;
+  if (nsplit == 1) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float* op = out + (int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + head * HD + sub * VD;
+#pragma unroll
+    for (int i = 0; i < VD; i += 4)
+      *(float4*)(op + i) = make_float4(acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv, acc[i + 3] * inv);
+  } else {
+    float* pp = part + (((int64_t)qidx * H + head) * nsplit + split) * PART;
+#pragma unroll
+    for (int i = 0; i < VD; i += 4)
+      *(float4*)(pp + sub * VD + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+    if (sub == 0) {
+      pp[64] = m;
+      pp[65] = l;
+    }
+  }
+}
+
+// Fold the split partials of one (query, head): one wave, lane = dim.
+__global__ __launch_bounds__(256) void k_attn_combine(
+    const float* __restrict__ part, int nsplit, const int32_t* __restrict__ n_rows, int rows,
+    int nq, float* __restrict__ out, int64_t out_row_stride, int64_t out_seq_stride) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (query, head)
+  if (unit >= (int64_t)nq * H) return;
+  const int qidx = (int)(unit / H), head = (int)(unit % H);
+  const int b = qidx / rows, r = qidx % rows;
+  if (n_rows && r >= n_rows[b]) return;
+  const float* pp = part + unit * nsplit * PART;
+  float m = -INFINITY;
+  for (int s = 0; s < nsplit; s++) m = fmaxf(m, pp[s * PART + 64]);
+  float l = 0.f, acc = 0.f;
+  if (m != -INFINITY) {
+    for (int s = 0; s < nsplit; s++) {
+      const float ms = pp[s * PART + 64];
+      if (ms == -INFINITY) continue;
+      const float w = __expf(ms - m);
+      l += pp[s * PART + 65] * w;
+      acc += pp[s * PART + lane] * w;
+    }
+  }
+  out[(int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + head * HD + lane] =
+      l > 0.f ? acc / l : 0.f;
+}
+
+// Launch the split attention for nq = B * rows queries.  The split length is
+// chosen so that about kTargetWaves waves cover the chip (256 CUs) while each
+// split stays a whole number of U-deep load batches.
+static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
+                       int64_t q_row_stride, int64_t q_seq_stride, const int32_t* pos0,
+                       const int32_t* n_rows, int64_t max_valid, float* out,
+                       int64_t out_row_stride, int64_t out_seq_stride) {
+  constexpr int kU = 8;
+  constexpr int64_t kTargetWaves = 8192;
+  const bool bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
+  const int gu = (bf16 ? 8 : 4) * kU;
+  const int C = ctx->cfg.capacity;
+  if (max_valid > C) max_valid = C;
+  if (max_valid < 1) max_valid = 1;
+  const int64_t nq = (int64_t)B * rows;
+  const int64_t units = nq * H;
+  int64_t want = (kTargetWaves + units - 1) / units;
+  int64_t split_len = (max_valid + want - 1) / want;
+  split_len = ((split_len + gu - 1) / gu) * gu;
+  const int nsplit = (int)((max_valid + split_len - 1) / split_len);
+  if (nq * nsplit > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
+  float* part = nullptr;
+  if (nsplit > 1) {
+    part = (float*)scratch(ctx, "attn_part", (size_t)units * nsplit * PART * 4);
+    if (!part) return fail(ctx, MB_ERR_NOMEM, "attention partials allocation failed");
+  }
+  const size_t e = kv_elem_bytes(ctx);
+  const void* rk = (const char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
+  const void* rv = (const char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
+  const int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
+  const int64_t rs = (int64_t)H * C * HD;
+  dim3 grid((unsigned)(nq * nsplit), H / 4);
+  if (bf16)
+    hipLaunchKernelGGL((k_attn_split<true, kU>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
+                       q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, (int)split_len, nsplit,
+                       part, out, out_row_stride, out_seq_stride);
+  else
+    hipLaunchKernelGGL((k_attn_split<false, kU>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
+                       q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, (int)split_len, nsplit,
+                       part, out, out_row_stride, out_seq_stride);
+  MB_HIP(ctx, hipGetLastError());
+  if (nsplit > 1) {
+    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream,
+                       part, nsplit, n_rows, rows, (int)nq, out, out_row_stride, out_seq_stride);
+    MB_HIP(ctx, hipGetLastError());
+  }
+  return MB_OK;
+}
+
+int launch_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
+                            const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride) {
+  return launch_attn(ctx, layer, B, 1, q, q_stride, q_stride, pos, nullptr, (int64_t)max_pos + 1,
+                     out, out_stride, out_stride);
+}
+
+int launch_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
+                             int q_dtype, int64_t q_row_stride, int64_t q_seq_stride,
+                             const int32_t* pos0, const int32_t* n_rows, float* out,
+                             int64_t out_row_stride, int64_t out_seq_stride) {
+  if (q_dtype != MB_DT_F32)
+    return fail(ctx, MB_ERR_ARG, "the row-wise prefill attention takes fp32 queries");
+  return launch_attn(ctx, layer, B, rows_max, (const float*)q, q_row_stride, q_seq_stride, pos0,
+                     n_rows, ctx->cfg.capacity, out, out_row_stride, out_seq_stride);
+}
+
+}  // namespace mb

@@ -1,0 +1,193 @@
+"""GPU parity of the ring append (RoPE on K, slot = pos mod C) and of the
+split-softmax decode attention, through the C ABI, against the oracle.
+
+Bars: slot positions, K and V ring contents and the roped q are bit-exact
+(fp32 and bf16 storage); attention outputs within 1e-4 of the oracle on the
+same stored values, and within 2e-2 of the fp32 oracle when K/V are stored
+in bf16.
+"""
+import numpy as np
+import pytest
+
+import mockbird_amd as mb
+from mockbird_amd import synth
+from oracle import oracle
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+KV = [("f32", mb.MB_KV_F32), ("bf16", mb.MB_KV_BF16)]
+
+
+def _oracle_ring(B, C, kv, wrap=True):
+    return oracle.Ring(B, C, kv_bf16=(kv == mb.MB_KV_BF16), wrap=wrap)
+
+
+def _check_ring(ctx, ring, layer, seqs):
+    for b in seqs:
+        k, v, sp = ctx.read_ring(layer, b)
+        assert np.array_equal(sp, ring.slot_pos[b]), f"slot positions differ, seq {b}"
+        live = sp >= 0
+        assert np.array_equal(k[live], ring.K[b][live]), f"K differs, seq {b}"
+        assert np.array_equal(v[live], ring.V[b][live]), f"V differs, seq {b}"
+
+
+@pytest.mark.parametrize("name,kv", KV)
+def test_append_and_attention_small(name, kv):
+    say(f"small ring parity kv={name}")
+    B, C, L = 5, 64, 2
+    rng = np.random.default_rng(11)
+    with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=200, kv_dtype=kv) as ctx:
+        ring = _oracle_ring(B, C, kv)
+        ring32 = _oracle_ring(B, C, mb.MB_KV_F32)
+        # prefill-style rows: ragged counts, some starting late enough to wrap inside the call
+        n = np.array([1, 17, 64, 50, 64], np.int32)
+        pos0 = np.array([0, 3, 0, 40, 100], np.int32)
+        qkv = synth.qkv_rows(1, (B, 64))
+        q_gpu = ctx.ring_write_rows(1, qkv, pos0, n)
+        q_or = ring.write(qkv, pos0, n)
+        ring32.write(qkv, pos0, n)
+        for b in range(B):
+            assert np.array_equal(q_gpu[b, :n[b]], q_or[b, :n[b]])
+        _check_ring(ctx, ring, 1, range(B))
+        pos = pos0 + n
+        for step in range(70):  # appends that wrap every ring at least once
+            qkv1 = rng.standard_normal((B, 2304), dtype=np.float32)
+            q1 = ctx.ring_append(1, qkv1, pos)
+            assert np.array_equal(q1, ring.append(qkv1, pos))
+            ring32.append(qkv1, pos)
+            out = ctx.decode_attention(1, q1, pos)
+            want = ring.attend(q1, pos)
+            assert np.abs(out - want).max() < 1e-4, step
+            if kv == mb.MB_KV_BF16:
+                assert np.abs(out - ring32.attend(q1, pos)).max() < 2e-2
+            pos = pos + 1
+        _check_ring(ctx, ring, 1, range(B))
+        # layer 0 was never written: every slot still empty
+        assert (ctx.read_ring(0, 2)[2] == -1).all()
+
+
+def test_non_wrapping_ring_reports_range_error():
+    say("non-wrapping ring overflow")
+    with mb.Context(n_layers=1, capacity=8, max_seqs=1, max_rows=8, wrap=False) as ctx:
+        qkv = np.zeros((1, 2304), np.float32)
+        ctx.ring_append(0, qkv, [7])
+        with pytest.raises(mb.MbError) as e:
+            ctx.ring_append(0, qkv, [8])
+        assert e.value.code == mb.MB_ERR_RANGE and "exceeds the KV ring" in str(e.value)
+        # more rows than slots in one call is refused before any launch
+        with pytest.raises(mb.MbError) as e:
+            ctx.ring_write_rows(0, np.zeros((1, 9, 2304), np.float32), [0], [9])
+        assert e.value.code == mb.MB_ERR_ARG
+
+
+def test_poison_reset_and_empty_attention():
+    say("poison / reset")
+    with mb.Context(n_layers=1, capacity=16, max_seqs=2, max_rows=16) as ctx:
+        ctx.ring_poison(0, 1, 3, -12345.5)
+        k, v, sp = ctx.read_ring(0, 1, 0, 4)
+        assert (k[:3] == -12345.5).all() and (v[:3] == -12345.5).all() and (k[3] == 0).all()
+        assert (sp == -1).all()  # poison does not make a slot live
+        rng = np.random.default_rng(5)
+        for p in range(20):
+            q = ctx.ring_append(0, rng.standard_normal((2, 2304), dtype=np.float32), [p, p])
+        ctx.ring_reset([1])
+        assert (ctx.read_ring(0, 1)[2] == -1).all()
+        assert (ctx.read_ring(0, 0)[2] >= 0).all()
+        qkv = rng.standard_normal((2, 2304), dtype=np.float32)
+        q = ctx.ring_append(0, qkv, [0, 20])
+        out = ctx.decode_attention(0, q, [0, 20])
+        # sequence 1 sees only the row it just appended: its V, exactly weighted 1
+        assert np.abs(out[1] - qkv[1, 1536:]).max() < 1e-6
+        # a query with nothing live returns zeros
+        ctx.ring_reset([1])
+        assert np.abs(ctx.decode_attention(0, q, [0, 20])[1]).max() == 0.0
+
+
+@pytest.mark.parametrize("name,kv", KV)
+def test_c1_full_size(name, kv):
+    """B=64 sequences, C=2048, positions U[1, 6144) (about two thirds wrapped),
+    rings filled through the row writer on the device, one append + attention
+    step; 6 sequences checked against the oracle slot for slot, all 64 by the
+    closed-form window."""
+    torch = pytest.importorskip("torch")
+    say(f"C1 full size kv={name}")
+    B, C = 64, 2048
+    g = np.random.default_rng(20260101)
+    pos = g.integers(1, 6144, size=B).astype(np.int32)
+    start = np.maximum(0, pos - (C - 1)).astype(np.int32)
+    nfill = (pos - start).astype(np.int32)
+    sample = [int(np.argmin(pos)), int(np.argmax(pos))] + [int(i) for i in g.choice(B, 4, replace=False)]
+    dev = torch.device("cuda")
+    tg = torch.Generator(device=dev)
+    tg.manual_seed(7)
+    host_rows = {b: [] for b in sample}
+    with mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=256, kv_dtype=kv) as ctx:
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        chunk = 256
+        for c0 in range(0, int(nfill.max()), chunk):
+            qkv = torch.randn((B, chunk, 2304), generator=tg, device=dev, dtype=torch.float32)
+            n = torch.from_numpy(np.clip(nfill - c0, 0, chunk).astype(np.int32)).to(dev)
+            p0 = torch.from_numpy((start + c0).astype(np.int32)).to(dev)
+            ctx.ring_write_rows_dev(0, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+            host = qkv.cpu().numpy()
+            for b in sample:
+                host_rows[b].append(host[b, :max(0, min(chunk, nfill[b] - c0))])
+        step = torch.randn((B, 2304), generator=tg, device=dev, dtype=torch.float32)
+        q = torch.empty((B, 768), device=dev)
+        out = torch.empty((B, 768), device=dev)
+        pos_d = torch.from_numpy(pos).to(dev)
+        ctx.ring_append_dev(0, B, step.data_ptr(), pos_d.data_ptr(), q.data_ptr())
+        ctx.decode_attention_dev(0, B, q.data_ptr(), pos_d.data_ptr(), int(pos.max()), out.data_ptr())
+        torch.cuda.synchronize()
+        q_h, out_h, step_h = q.cpu().numpy(), out.cpu().numpy(), step.cpu().numpy()
+        assert np.isfinite(out_h).all()
+        for b in range(B):  # closed-form window for every sequence
+            sp = ctx.read_ring(0, b)[2]
+            lo = max(0, pos[b] - C + 1)
+            want = np.full(C, -1, np.int32)
+            for p in range(lo, pos[b] + 1):
+                want[p % C] = p
+            assert np.array_equal(sp, want), b
+        for b in sample:
+            ring = _oracle_ring(1, C, kv)
+            rows = np.concatenate(host_rows[b] + [step_h[b][None]])[None]
+            qo = ring.write(rows, [start[b]], [nfill[b] + 1])[0, -1]
+            assert np.array_equal(qo, q_h[b])
+            k, v, sp = ctx.read_ring(0, b)
+            assert np.array_equal(sp, ring.slot_pos[0])
+            assert np.array_equal(k, ring.K[0]) and np.array_equal(v, ring.V[0])
+            want = ring.attend(q_h[b][None], [pos[b]])[0]
+            assert np.abs(out_h[b] - want).max() < 1e-4, b
+
+
+def test_c4_eviction_stress():
+    """B=32, C=4096, positions 0..5000 (every ring wraps and evicts); at
+    4095, 4096, 4097 and 5000: slot positions of every sequence exact, two
+    sequences' rings bit-exact and attention within 1e-4 of the oracle."""
+    say("C4 eviction stress")
+    B, C = 32, 4096
+    watch = [0, 17]
+    rings = {b: _oracle_ring(1, C, mb.MB_KV_F32) for b in watch}
+    checks = (4095, 4096, 4097, 5000)
+    with mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=1) as ctx:
+        for p in range(5001):
+            qkv = np.random.default_rng([44, p]).standard_normal((B, 2304), dtype=np.float32)
+            posv = np.full(B, p, np.int32)
+            q = ctx.ring_append(0, qkv, posv)
+            for b in watch:
+                assert np.array_equal(q[b], rings[b].append(qkv[b][None], [p])[0])
+            if p in checks:
+                say(f"  checkpoint {p}")
+                out = ctx.decode_attention(0, q, posv)
+                lo = max(0, p - C + 1)
+                want_sp = np.full(C, -1, np.int32)
+                for pp in range(lo, p + 1):
+                    want_sp[pp % C] = pp
+                for b in range(B):
+                    assert np.array_equal(ctx.read_ring(0, b)[2], want_sp), (p, b)
+                for b in watch:
+                    k, v, sp = ctx.read_ring(0, b)
+                    assert np.array_equal(k, rings[b].K[0]) and np.array_equal(v, rings[b].V[0])
+                    want = rings[b].attend(q[b][None], [p])[0]
+                    assert np.abs(out[b] - want).max() < 1e-4, (p, b)
