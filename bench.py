@@ -1,0 +1,227 @@
+"""Benchmark of the MI355X decoder hot path (one GPU).
+
+    python bench.py [--steps K] [--warmup W] [--workload c1|c1-f32]
+
+Default workload (c1): the isolated KV ring append + decode attention step --
+B=64 independent sequences, 12 heads x 64, ring capacity 2048, bf16 KV
+storage, one query per sequence per step, write positions U[1, 6144) from a
+seed (about two thirds of the rings have wrapped).  A step is one layer's
+append + attention for all 64 sequences; twelve layer rings are stepped in
+turn (as a 12-layer decode does), so the 4.8 GB of KV never fits the 256 MB
+last-level cache and the GB/s are HBM figures.  Every sequence advances one
+position after each full pass over the twelve layers.
+
+value = algorithmic bytes of the step (K/V window read + q/k/v read + roped q,
+K, V write + output write) / wall time, inputs already resident in HBM.
+roofline = the decode-attention launch alone, timed with HIP events on the
+stream it runs on.  cpu_baseline = the C oracle (OpenMP) on a bounded sample
+of the same workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode frames/sec at B=1/64/256; KV-attn HBM GB/s as % of peak"
+HBM_PEAK_GBS = 8000.0
+D, H, HD, QKV = 768, 12, 64, 2304
+
+
+def c1_positions(B=64, seed=20260101):
+    g = np.random.default_rng(seed)
+    return g.integers(1, 6144, size=B).astype(np.int32)
+
+
+def attn_bytes(pos, C, e):
+    """Algorithmic bytes of one decode-attention launch: every live K and V
+    row once, q read (fp32) and the output written (fp32)."""
+    valid = np.minimum(pos.astype(np.int64) + 1, C)
+    return int(valid.sum()) * D * 2 * e + len(pos) * D * 4 * 2
+
+
+def append_bytes(B, e):
+    """q | k | v read (fp32), roped q written (fp32), K and V written (e bytes)."""
+    return B * (QKV * 4 + D * 4 + 2 * D * e)
+
+
+def run_c1(args, kv_name):
+    import torch
+
+    import mockbird_amd as mb
+
+    B, C, L = 64, 2048, 12
+    kv = mb.MB_KV_BF16 if kv_name == "bf16" else mb.MB_KV_F32
+    e = 2 if kv == mb.MB_KV_BF16 else 4
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=256, kv_dtype=kv)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    pos0 = c1_positions(B)
+    start = np.maximum(0, pos0 - (C - 1)).astype(np.int32)
+    nfill = (pos0 - start).astype(np.int32)
+    tg = torch.Generator(device=dev)
+    tg.manual_seed(7)
+    chunk = 256
+    for layer in range(L):
+        for c0 in range(0, int(nfill.max()), chunk):
+            qkv = torch.randn((B, chunk, QKV), generator=tg, device=dev)
+            n = torch.from_numpy(np.clip(nfill - c0, 0, chunk).astype(np.int32)).to(dev)
+            p0 = torch.from_numpy((start + c0).astype(np.int32)).to(dev)
+            ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+    torch.cuda.synchronize()
+    total = args.warmup + args.steps
+    tokens = total // L + 2
+    pos_all = torch.from_numpy((pos0[None, :] + np.arange(tokens)[:, None]).astype(np.int32)).to(dev)
+    qkv_l = [torch.randn((B, QKV), generator=tg, device=dev) for _ in range(L)]
+    q = torch.empty((B, D), device=dev)
+    out = torch.empty((B, D), device=dev)
+    max_pos = int(pos0.max()) + tokens
+
+    def step(s, ev=None):
+        layer, tok = s % L, s // L
+        p = pos_all[tok]
+        ctx.ring_append_dev(layer, B, qkv_l[layer].data_ptr(), p.data_ptr(), q.data_ptr())
+        if ev is not None:
+            ev[0].record(stream)
+        ctx.decode_attention_dev(layer, B, q.data_ptr(), p.data_ptr(), max_pos, out.data_ptr())
+        if ev is not None:
+            ev[1].record(stream)
+
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = t0.elapsed_time(t1)
+    attn_ms = np.array([a.elapsed_time(b) for a, b in evs])
+    step_bytes = 0
+    attn_total = 0
+    for i in range(args.steps):
+        tok = (args.warmup + i) // L
+        p = pos0 + tok
+        ab = attn_bytes(p, C, e)
+        attn_total += ab
+        step_bytes += ab + append_bytes(B, e)
+    ms_step = ms_total / args.steps
+    res = {
+        "kv": kv_name,
+        "ms_per_step": ms_step,
+        "gbs": step_bytes / args.steps / (ms_step * 1e-3) / 1e9,
+        "attn_us": float(attn_ms.mean() * 1e3),
+        "attn_bytes": attn_total / args.steps,
+        "attn_gbs": attn_total / args.steps / (attn_ms.mean() * 1e-3) / 1e9,
+        "mean_valid": float(np.minimum(pos0 + args.warmup // L + args.steps // (2 * L) + 1, C).mean()),
+    }
+    ctx.close()
+    return res
+
+
+def cpu_baseline_c1(seconds=12.0):
+    """The oracle (double-precision C, OpenMP over sequences) on a sample of the
+    c1 workload: 8 of the 64 sequences, fp32 rings, append + attention steps,
+    repeated until `seconds` have passed."""
+    from oracle import oracle
+
+    B, C = 8, 2048
+    pos = c1_positions(64)[:B]
+    g = np.random.default_rng(5)
+    ring = oracle.Ring(B, C)
+    for b in range(B):
+        lo = max(0, pos[b] - C + 1)
+        for p in range(lo, pos[b]):
+            ring.slot_pos[b, p % C] = p
+    ring.K[:] = g.standard_normal(ring.K.shape, dtype=np.float32)
+    ring.V[:] = g.standard_normal(ring.V.shape, dtype=np.float32)
+    qkv = g.standard_normal((B, QKV), dtype=np.float32)
+    nbytes, steps = 0, 0
+    t0 = time.perf_counter()
+    p = pos.copy()
+    while time.perf_counter() - t0 < seconds:
+        q = ring.append(qkv, p)
+        ring.attend(q, p)
+        nbytes += attn_bytes(p, C, 4) + append_bytes(B, 4)
+        p = p + 1
+        steps += 1
+    dt = time.perf_counter() - t0
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} append+attention steps of 8 of the 64 sequences (fp32 rings, "
+                      f"C=2048), {dt:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1200)
+    ap.add_argument("--warmup", type=int, default=48)
+    ap.add_argument("--workload", default="c1", choices=["c1"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--kv", default="both", choices=["both", "bf16"])
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sequences are "
+              "independent, so N GPUs would each run this same workload on their own share.",
+              file=sys.stderr)
+        return 2
+    bf16 = run_c1(args, "bf16")
+    f32 = run_c1(args, "f32") if args.kv == "both" else None
+    cpu = None if args.no_cpu_baseline else cpu_baseline_c1(args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(bf16["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(bf16["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "KV ring append + decode attention (isolated): B=64 sequences, 12 heads "
+                        "x 64, ring capacity 2048, bf16 KV storage, write positions U[1,6144) "
+                        "seed 20260101, one query per sequence per step, 12 layer rings in turn",
+            "kv_dtype": "bf16", "B": 64, "capacity": 2048, "heads": 12, "head_dim": 64,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(bf16["attn_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(bf16["attn_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode attention (k_attn_split + k_attn_combine)",
+            "avg_us": round(bf16["attn_us"], 2),
+            "bytes_per_launch": int(bf16["attn_bytes"]),
+        },
+        "cpu_baseline": cpu,
+        "f32_kv": None if f32 is None else {
+            "value": round(f32["gbs"], 2), "unit": "GB/s",
+            "ms_per_step": round(f32["ms_per_step"], 5),
+            "attn_gbs": round(f32["attn_gbs"], 1), "attn_us": round(f32["attn_us"], 2),
+            "frac": round(f32["attn_gbs"] / HBM_PEAK_GBS, 4)},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

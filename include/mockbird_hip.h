@@ -81,8 +81,9 @@ int mb_create(const mb_config* cfg, mb_ctx** out);
 /* Free everything (gpu.ts:283-291 dispose). */
 void mb_destroy(mb_ctx* ctx);
 const char* mb_last_error(const mb_ctx* ctx);
-/* Launch on `hip_stream` (a hipStream_t) instead of the context's own stream;
- * NULL restores the context's own stream. */
+/* Launch every later call on `hip_stream` (a hipStream_t; NULL is HIP's
+ * default stream).  A new context launches on a stream of its own, which
+ * mb_get_stream() returns until this is called. */
 int mb_set_stream(mb_ctx* ctx, void* hip_stream);
 void* mb_get_stream(mb_ctx* ctx);
 int mb_synchronize(mb_ctx* ctx);

@@ -58,6 +58,15 @@ def load():
         raise RuntimeError(
             f"{LIB_PATH} is missing: build it with `python -m mockbird_amd.build` "
             "(the HIP library is the only implementation; there is no fallback)")
+    # One HIP runtime per process: when PyTorch is present it carries its own
+    # libamdhip64.so.7, and a second copy loaded from /opt/rocm would own the
+    # device first and leave torch with "no ROCm-capable device".  Importing
+    # torch first makes the dynamic loader bind this library to torch's copy
+    # (same soname), so device pointers and streams are shared.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     sig = {
         "mb_abi_version": ([], C.c_int),

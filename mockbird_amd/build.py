@@ -27,7 +27,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
 
 HIP_FLAGS = [
-    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17",
+    "--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function", "-Wno-unused-result",
     "-I", os.path.join(ROOT, "include"),

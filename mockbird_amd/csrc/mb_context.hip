@@ -1,6 +1,7 @@
 // Context lifetime, errors, weights, ring bookkeeping and the host-pointer
 // entry points of the C ABI (include/mockbird_hip.h).  Kernels live in
 // ring.hip; this file only allocates, validates, stages and launches.
+#include <cmath>
 #include <cstring>
 
 #include "mb_internal.h"
@@ -134,11 +135,23 @@ int mb_create(const mb_config* cfg, mb_ctx** out) {
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipMalloc(ring V)"); break; }
     e = hipMalloc(&ctx->slot_pos, (size_t)slots * sizeof(int32_t));
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipMalloc(slot_pos)"); break; }
-    ctx->max_splits = (cfg->capacity + 63) / 64;
-    const size_t part_bytes = (size_t)cfg->max_seqs * H * ctx->max_splits * PART * sizeof(float);
-    e = hipMalloc(&ctx->part, part_bytes);
-    if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipMalloc(partials)"); break; }
-    ctx->device_bytes = 2 * (int64_t)ctx->ring_bytes + slots * 4 + (int64_t)part_bytes;
+    {
+      // (cos, sin) of float(pos) * inv_freq[i], in double, rounded to fp32
+      std::vector<float2> tab((size_t)kRopeTab * 32);
+      for (int i = 0; i < 32; i++) {
+        float inv;
+        memcpy(&inv, &kInvFreqBits[i], 4);
+        for (int p = 0; p < kRopeTab; p++) {
+          const float a = (float)p * inv;
+          tab[(size_t)p * 32 + i] = make_float2((float)cos((double)a), (float)sin((double)a));
+        }
+      }
+      e = hipMalloc(&ctx->rope_tab, tab.size() * sizeof(float2));
+      if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipMalloc(rope table)"); break; }
+      e = hipMemcpy(ctx->rope_tab, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice);
+      if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipMemcpy(rope table)"); break; }
+    }
+    ctx->device_bytes = 2 * (int64_t)ctx->ring_bytes + slots * 4 + (int64_t)kRopeTab * 32 * 8;
     // every slot empty; K/V zero so a read of an unwritten slot is well defined
     rc = launch_fill_kv(ctx, ctx->ring_k, (int64_t)(ctx->ring_bytes / kv_elem_bytes(ctx)), 0.f);
     if (rc) break;
@@ -167,7 +180,7 @@ void mb_destroy(mb_ctx* ctx) {
   (void)hipFree(ctx->ring_k);
   (void)hipFree(ctx->ring_v);
   (void)hipFree(ctx->slot_pos);
-  (void)hipFree(ctx->part);
+  (void)hipFree(ctx->rope_tab);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
 }
@@ -176,7 +189,7 @@ const char* mb_last_error(const mb_ctx* ctx) { return ctx ? ctx->err.c_str() : "
 
 int mb_set_stream(mb_ctx* ctx, void* hip_stream) {
   if (!ctx) return MB_ERR_ARG;
-  ctx->stream = hip_stream ? (hipStream_t)hip_stream : ctx->own_stream;
+  ctx->stream = (hipStream_t)hip_stream;
   return MB_OK;
 }
 

@@ -29,6 +29,20 @@ constexpr int CODES = 1024; // codebook size
 // running max and the running sum, padded to 68 floats (16-byte aligned).
 constexpr int PART = 68;
 
+// Positions whose RoPE cos/sin come from the context's table.
+constexpr int kRopeTab = 65536;
+
+// fp32 inverse frequencies of the exported graph (torch's fp32 values of
+// 1 / 10000^(2i/64)); six entries sit one ulp away from the correctly rounded
+// value, and the reference's ORT K fixture fixes which.
+constexpr uint32_t kInvFreqBits[32] = {
+    0x3f800000u, 0x3f3ff911u, 0x3f0ff59au, 0x3ed7e89bu, 0x3ea1e89bu, 0x3e72d423u,
+    0x3e361887u, 0x3e088d77u, 0x3dcccccdu, 0x3d99940du, 0x3d6655c2u, 0x3d2cba15u,
+    0x3d0186e3u, 0x3cc2434fu, 0x3c91ad39u, 0x3c5a7bf2u, 0x3c23d70au, 0x3bf5b9b0u,
+    0x3bb8449cu, 0x3b8a2e77u, 0x3b4f3e38u, 0x3b1b690du, 0x3ae91528u, 0x3aaec98eu,
+    0x3a83126fu, 0x3a44948cu, 0x3a136a16u, 0x39dd1725u, 0x39a5cb60u, 0x3978a815u,
+    0x393a7753u, 0x390bd472u};
+
 struct DeviceTensor {
   float* ptr = nullptr;
   std::vector<int64_t> dims;
@@ -59,9 +73,10 @@ struct mb_ctx {
   int32_t* slot_pos = nullptr;
   size_t ring_bytes = 0;  // bytes of ring_k (== ring_v)
 
-  // Split-softmax partials for decode attention: [max_seqs][H][max_splits][PART].
-  float* part = nullptr;
-  int max_splits = 0;
+  // RoPE cos/sin for positions [0, kRopeTab): (cos, sin) of pair i at
+  // position p in rope_tab[p * 32 + i]; later positions are computed in-kernel.
+  float2* rope_tab = nullptr;
+
 
   std::map<std::string, mb::DeviceTensor> weights;
   std::map<std::string, mb::Scratch> scratch;

@@ -11,16 +11,14 @@
 
 namespace mb {
 
-// fp32 inverse frequencies of the exported graph (torch's fp32 values of
-// 1 / 10000^(2i/64)); six entries sit one ulp away from the correctly rounded
-// value, and the reference's ORT K fixture fixes which.
 __constant__ uint32_t c_inv_freq_bits[32] = {
-    0x3f800000u, 0x3f3ff911u, 0x3f0ff59au, 0x3ed7e89bu, 0x3ea1e89bu, 0x3e72d423u,
-    0x3e361887u, 0x3e088d77u, 0x3dcccccdu, 0x3d99940du, 0x3d6655c2u, 0x3d2cba15u,
-    0x3d0186e3u, 0x3cc2434fu, 0x3c91ad39u, 0x3c5a7bf2u, 0x3c23d70au, 0x3bf5b9b0u,
-    0x3bb8449cu, 0x3b8a2e77u, 0x3b4f3e38u, 0x3b1b690du, 0x3ae91528u, 0x3aaec98eu,
-    0x3a83126fu, 0x3a44948cu, 0x3a136a16u, 0x39dd1725u, 0x39a5cb60u, 0x3978a815u,
-    0x393a7753u, 0x390bd472u};
+    kInvFreqBits[0], kInvFreqBits[1], kInvFreqBits[2], kInvFreqBits[3], kInvFreqBits[4],
+    kInvFreqBits[5], kInvFreqBits[6], kInvFreqBits[7], kInvFreqBits[8], kInvFreqBits[9],
+    kInvFreqBits[10], kInvFreqBits[11], kInvFreqBits[12], kInvFreqBits[13], kInvFreqBits[14],
+    kInvFreqBits[15], kInvFreqBits[16], kInvFreqBits[17], kInvFreqBits[18], kInvFreqBits[19],
+    kInvFreqBits[20], kInvFreqBits[21], kInvFreqBits[22], kInvFreqBits[23], kInvFreqBits[24],
+    kInvFreqBits[25], kInvFreqBits[26], kInvFreqBits[27], kInvFreqBits[28], kInvFreqBits[29],
+    kInvFreqBits[30], kInvFreqBits[31]};
 
 // ------------------------------------------------------------------ fills
 
@@ -71,7 +69,16 @@ int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value) {
 // cos/sin of pair `i` at absolute position `pos`: the angle is the fp32
 // product float(pos) * inv_freq[i] (as the graph's fp32 Einsum forms it), and
 // cos/sin of that fp32 angle are evaluated in double and rounded to fp32.
-__device__ __forceinline__ void rope_cs(int32_t pos, int i, float& c, float& s) {
+// Positions below kRopeTab read the context's table (built on the host with
+// the same recipe); later ones are evaluated here.
+__device__ __forceinline__ void rope_cs(const float2* __restrict__ tab, int32_t pos, int i,
+                                        float& c, float& s) {
+  if (pos < kRopeTab) {
+    const float2 t = tab[(int64_t)pos * 32 + i];
+    c = t.x;
+    s = t.y;
+    return;
+  }
   const float a = __fmul_rn((float)pos, __uint_as_float(c_inv_freq_bits[i]));
   double sd, cd;
   sincos((double)a, &sd, &cd);
@@ -80,10 +87,10 @@ __device__ __forceinline__ void rope_cs(int32_t pos, int i, float& c, float& s) 
 }
 
 // One rotated pair, evaluated as the graph does it: fp32 Mul, Mul, Add with
-// rotate_half(x) = (-x1, x0) -- never fused into an FMA.
+// rotate_half(x) = (-x1, x0) -- never fused into an FMA (the library is built
+// with -ffp-contract=off, so only explicit fmaf calls fuse).
 __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, float& o0,
                                           float& o1) {
-#pragma clang fp contract(off)
   o0 = __fadd_rn(__fmul_rn(x0, c), __fmul_rn(-x1, s));
   o1 = __fadd_rn(__fmul_rn(x1, c), __fmul_rn(x0, s));
 }
@@ -101,7 +108,7 @@ __global__ __launch_bounds__(256) void k_ring_write(
     const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows_max, int B,
     void* __restrict__ q_out, int64_t q_row_stride, int64_t q_seq_stride,
     void* __restrict__ ring_k, void* __restrict__ ring_v, int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, int wrap) {
+    int64_t ring_seq_stride, int C, int wrap, const float2* __restrict__ rope_tab) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row_id = t / 96;
   if (row_id >= (int64_t)B * rows_max) return;
@@ -124,7 +131,7 @@ __global__ __launch_bounds__(256) void k_ring_write(
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     float c, s;
-    rope_cs(pos, (d0 >> 1) + j, c, s);
+    rope_cs(rope_tab, pos, (d0 >> 1) + j, c, s);
     rope_pair(q[2 * j], q[2 * j + 1], c, s, qo[2 * j], qo[2 * j + 1]);
     rope_pair(k[2 * j], k[2 * j + 1], c, s, ko[2 * j], ko[2 * j + 1]);
   }
@@ -155,7 +162,8 @@ int launch_ring_write(mb_ctx* ctx, int layer, int B, int rows_max, const void* q
 #define MB_RW(A, Bq, Cq)                                                                        \
   hipLaunchKernelGGL((k_ring_write<A, Bq, Cq>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, \
                      qkv, qkv_row_stride, qkv_seq_stride, pos0, n_rows, rows_max, B, q_out,      \
-                     q_row_stride, q_seq_stride, rk, rv, sp, rs, ctx->cfg.capacity, ctx->cfg.wrap)
+                     q_row_stride, q_seq_stride, rk, rv, sp, rs, ctx->cfg.capacity, ctx->cfg.wrap,    \
+                     ctx->rope_tab)
   if (in_bf16) {
     if (kv_bf16) { if (q_bf16) MB_RW(true, true, true); else MB_RW(true, true, false); }
     else { if (q_bf16) MB_RW(true, false, true); else MB_RW(true, false, false); }
@@ -208,12 +216,18 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* acc, floa
 // slots [s * split_len, (s + 1) * split_len) of that range.
 //
 // Lane layout: LR = 64 / VD lanes hold one 64-dim row (VD dims each, one
-// 16-byte load), so a wave covers G = VD slots per load; U loads of K and V
-// are issued before any is used.  Scores are reduced across the LR lanes with
-// DPP; each lane group keeps its own online-softmax state (max, sum, VD
-// accumulators) and the G groups are merged with cross-row shuffles at the
-// end.  One split writes its normalised row directly; several write partials
-// (acc[64], max, sum) that k_attn_combine folds.
+// 16-byte load), so a wave covers G = VD consecutive slots -- 1 KB of one
+// (sequence, head) run -- per load instruction; U loads of K and V are issued
+// before any is used.  Scores are reduced across the LR lanes with DPP; each
+// lane group keeps its own online-softmax state (max, sum, VD accumulators)
+// and the G groups are merged with cross-row shuffles at the end.
+//
+// Liveness: for each tile of 256 slots every lane loads the stored positions
+// of 4 slots and the wave turns them into four 64-bit ballot masks, so the
+// per-slot test in the hot loop is a bit lookup, not a memory access.
+//
+// With one split the normalised row is written directly; with several each
+// wave writes a partial (acc[64], max, sum) for k_attn_combine.
 template <bool KV_BF16, int U>
 __global__ __launch_bounds__(256) void k_attn_split(
     const float* __restrict__ q, int64_t q_row_stride, int64_t q_seq_stride,
@@ -225,6 +239,7 @@ __global__ __launch_bounds__(256) void k_attn_split(
   constexpr int VD = KV_BF16 ? 8 : 4;
   constexpr int LR = 64 / VD;
   constexpr int G = VD;
+  constexpr int TILE = 256;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int head = blockIdx.y * 4 + wave;
   const int qidx = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
@@ -246,56 +261,68 @@ __global__ __launch_bounds__(256) void k_attn_split(
       qv[i] = t.x * 0.125f; qv[i + 1] = t.y * 0.125f; qv[i + 2] = t.z * 0.125f; qv[i + 3] = t.w * 0.125f;
     }
   }
-  const int64_t hoff = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
+  const char* kbase = (const char*)ring_k +
+      ((int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD) * (KV_BF16 ? 2 : 4);
+  const char* vbase = (const char*)ring_v +
+      ((int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD) * (KV_BF16 ? 2 : 4);
+  constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
   float m = -INFINITY, l = 0.f, acc[VD];
 #pragma unroll
   for (int i = 0; i < VD; i++) acc[i] = 0.f;
 
-  for (int base = s0; base < s1; base += G * U) {
-    uint4 kr[U], vr[U];
-    int spv[U];
-    bool ok[U];
+  for (int t0 = s0; t0 < s1; t0 += TILE) {
+    const int t1 = min(t0 + TILE, s1);
+    uint64_t live[4];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const int slot = base + u * G + g;
-      ok[u] = slot < s1;
-      const int sl = ok[u] ? slot : s0;
-      kr[u] = *(const uint4*)((const char*)ring_k + (hoff + (int64_t)sl * HD) * (KV_BF16 ? 2 : 4));
-      vr[u] = *(const uint4*)((const char*)ring_v + (hoff + (int64_t)sl * HD) * (KV_BF16 ? 2 : 4));
-      spv[u] = sp[sl];
+    for (int c = 0; c < 4; c++) {
+      const int idx = t0 + 4 * lane + c;
+      const int64_t p = idx < t1 ? (int64_t)sp[idx] : -1;
+      const int64_t dlt = cur - p;
+      live[c] = __ballot(p >= 0 && dlt >= 0 && dlt < C);
     }
-    float sc[U];
-    float mx = m;
+    for (int base = t0; base < t1; base += G * U) {
+      uint4 kr[U], vr[U];
+      bool ok[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      float kf[VD];
-      unpack<KV_BF16>(kr[u], kf);
-      float dot = 0.f;
+      for (int u = 0; u < U; u++) {
+        const int slot = base + u * G + g;
+        const int i = slot - t0;
+        ok[u] = slot < t1 && ((live[i & 3] >> (i >> 2)) & 1ull);
+        const int sl = slot < t1 ? slot : t0;
+        kr[u] = *(const uint4*)(kbase + (int64_t)sl * ROWB);
+        vr[u] = *(const uint4*)(vbase + (int64_t)sl * ROWB);
+      }
+      float sc[U];
+      float mx = m;
 #pragma unroll
-      for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
-      dot = group_sum<LR>(dot);
-      const int64_t dlt = cur - spv[u];
-      const bool live = ok[u] && spv[u] >= 0 && dlt >= 0 && dlt < C;
-      sc[u] = live ? dot : -INFINITY;
-      mx = fmaxf(mx, sc[u]);
+      for (int u = 0; u < U; u++) {
+        float kf[VD];
+        unpack<KV_BF16>(kr[u], kf);
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
+        dot = group_sum<LR>(dot);
+        sc[u] = ok[u] ? dot : -INFINITY;
+        mx = fmaxf(mx, sc[u]);
+      }
+      if (mx == -INFINITY) continue;  // nothing live yet in this lane group
+      const float scale = __expf(m - mx);
+      l *= scale;
+#pragma unroll
+      for (int i = 0; i < VD; i++) acc[i] *= scale;
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const float p = __expf(sc[u] - mx);
+        l += p;
+        float vf[VD];
+        unpack<KV_BF16>(vr[u], vf);
+#pragma unroll
+        for (int i = 0; i < VD; i++) acc[i] = fmaf(p, vf[i], acc[i]);
+      }
+      m = mx;
     }
-    if (mx == -INFINITY) continue;  // nothing live yet in this lane group
-    const float scale = __expf(m - mx);
-    l *= scale;
-#pragma unroll
-    for (int i = 0; i < VD; i++) acc[i] *= scale;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const float p = __expf(sc[u] - mx);
-      l += p;
-      float vf[VD];
-      unpack<KV_BF16>(vr[u], vf);
-#pragma unroll
-      for (int i = 0; i < VD; i++) acc[i] = fmaf(p, vf[i], acc[i]);
-    }
-    m = mx;
   }
 
   // fold the G lane groups: lanes sub, sub+LR, sub+2LR, ... hold the same dims
@@ -327,51 +354,72 @@ __global__ __launch_bounds__(256) void k_attn_split(
   }
 }
 
-// Fold the split partials of one (query, head): one wave, lane = dim.
+// Fold the split partials of one (query, head) -- one wave, lane = dim.
+// Lane s first holds split s's (max, sum) (nsplit <= 64), the wave forms the
+// global max and each split's weight, then every lane sums its dim over the
+// splits with independent loads.
 __global__ __launch_bounds__(256) void k_attn_combine(
     const float* __restrict__ part, int nsplit, const int32_t* __restrict__ n_rows, int rows,
-    int nq, float* __restrict__ out, int64_t out_row_stride, int64_t out_seq_stride) {
+    int64_t units, float* __restrict__ out, int64_t out_row_stride, int64_t out_seq_stride) {
   const int lane = threadIdx.x & 63;
   const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (query, head)
-  if (unit >= (int64_t)nq * H) return;
+  if (unit >= units) return;
   const int qidx = (int)(unit / H), head = (int)(unit % H);
   const int b = qidx / rows, r = qidx % rows;
   if (n_rows && r >= n_rows[b]) return;
   const float* pp = part + unit * nsplit * PART;
-  float m = -INFINITY;
-  for (int s = 0; s < nsplit; s++) m = fmaxf(m, pp[s * PART + 64]);
-  float l = 0.f, acc = 0.f;
-  if (m != -INFINITY) {
-    for (int s = 0; s < nsplit; s++) {
-      const float ms = pp[s * PART + 64];
-      if (ms == -INFINITY) continue;
-      const float w = __expf(ms - m);
-      l += pp[s * PART + 65] * w;
-      acc += pp[s * PART + lane] * w;
-    }
-  }
+  const float ms = lane < nsplit ? pp[lane * PART + 64] : -INFINITY;
+  const float ls = lane < nsplit ? pp[lane * PART + 65] : 0.f;
+  float M = ms;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+  const float w = (ms == -INFINITY) ? 0.f : __expf(ms - M);
+  float L = ls * w;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+  float acc = 0.f;
+  for (int s = 0; s < nsplit; s++) acc = fmaf(__shfl(w, s), pp[s * PART + lane], acc);
   out[(int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + head * HD + lane] =
-      l > 0.f ? acc / l : 0.f;
+      L > 0.f ? acc / L : 0.f;
 }
 
 // Launch the split attention for nq = B * rows queries.  The split length is
-// chosen so that about kTargetWaves waves cover the chip (256 CUs) while each
-// split stays a whole number of U-deep load batches.
+// chosen so that about `target` waves cover the chip (256 CUs) while each
+// split stays a whole number of U-deep load batches and there are at most 64
+// splits; MB_ATTN_WAVES and MB_ATTN_U override the defaults (tuning sweeps).
+template <bool BF16, int U>
+static void launch_split(mb_ctx* ctx, dim3 grid, const float* q, int64_t q_row_stride,
+                         int64_t q_seq_stride, const int32_t* pos0, const int32_t* n_rows, int rows,
+                         const void* rk, const void* rv, const int32_t* sp, int64_t rs, int C,
+                         int split_len, int nsplit, float* part, float* out,
+                         int64_t out_row_stride, int64_t out_seq_stride) {
+  hipLaunchKernelGGL((k_attn_split<BF16, U>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
+                     q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, split_len, nsplit, part,
+                     out, out_row_stride, out_seq_stride);
+}
+
+static int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
 static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
                        int64_t q_row_stride, int64_t q_seq_stride, const int32_t* pos0,
                        const int32_t* n_rows, int64_t max_valid, float* out,
                        int64_t out_row_stride, int64_t out_seq_stride) {
-  constexpr int kU = 8;
-  constexpr int64_t kTargetWaves = 8192;
+  static const int64_t target = env_int("MB_ATTN_WAVES", 8192);
+  static const int U = env_int("MB_ATTN_U", 16);
+  if (U != 4 && U != 8 && U != 16) return fail(ctx, MB_ERR_ARG, "MB_ATTN_U must be 4, 8 or 16");
   const bool bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
-  const int gu = (bf16 ? 8 : 4) * kU;
+  const int gu = (bf16 ? 8 : 4) * U;
   const int C = ctx->cfg.capacity;
   if (max_valid > C) max_valid = C;
   if (max_valid < 1) max_valid = 1;
   const int64_t nq = (int64_t)B * rows;
   const int64_t units = nq * H;
-  int64_t want = (kTargetWaves + units - 1) / units;
+  const int64_t want = (target + units - 1) / units;
   int64_t split_len = (max_valid + want - 1) / want;
+  if (split_len < (max_valid + 63) / 64) split_len = (max_valid + 63) / 64;
   split_len = ((split_len + gu - 1) / gu) * gu;
   const int nsplit = (int)((max_valid + split_len - 1) / split_len);
   if (nq * nsplit > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
@@ -386,18 +434,19 @@ static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
   const int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
   const int64_t rs = (int64_t)H * C * HD;
   dim3 grid((unsigned)(nq * nsplit), H / 4);
-  if (bf16)
-    hipLaunchKernelGGL((k_attn_split<true, kU>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
-                       q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, (int)split_len, nsplit,
-                       part, out, out_row_stride, out_seq_stride);
-  else
-    hipLaunchKernelGGL((k_attn_split<false, kU>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
-                       q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, (int)split_len, nsplit,
-                       part, out, out_row_stride, out_seq_stride);
+#define MB_SPLIT(BF, UU)                                                                       \
+  launch_split<BF, UU>(ctx, grid, q, q_row_stride, q_seq_stride, pos0, n_rows, rows, rk, rv, sp, \
+                       rs, C, (int)split_len, nsplit, part, out, out_row_stride, out_seq_stride)
+  if (bf16) {
+    if (U == 4) MB_SPLIT(true, 4); else if (U == 8) MB_SPLIT(true, 8); else MB_SPLIT(true, 16);
+  } else {
+    if (U == 4) MB_SPLIT(false, 4); else if (U == 8) MB_SPLIT(false, 8); else MB_SPLIT(false, 16);
+  }
+#undef MB_SPLIT
   MB_HIP(ctx, hipGetLastError());
   if (nsplit > 1) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream,
-                       part, nsplit, n_rows, rows, (int)nq, out, out_row_stride, out_seq_stride);
+                       part, nsplit, n_rows, rows, units, out, out_row_stride, out_seq_stride);
     MB_HIP(ctx, hipGetLastError());
   }
   return MB_OK;

@@ -67,6 +67,20 @@ def test_append_and_attention_small(name, kv):
         assert (ctx.read_ring(0, 2)[2] == -1).all()
 
 
+def test_rope_positions_beyond_the_table():
+    """Positions below 65536 take cos/sin from the context's table, later ones
+    are evaluated in-kernel; both must reproduce the oracle bit for bit."""
+    say("rope table boundary")
+    pos = np.array([0, 1, 65534, 65535, 65536, 65537, 1_000_003, 2**24 + 1], np.int32)
+    B = pos.size
+    with mb.Context(n_layers=1, capacity=7, max_seqs=B, max_rows=1) as ctx:
+        ring = oracle.Ring(B, 7)
+        qkv = synth.qkv_rows(3, (B,))
+        q = ctx.ring_append(0, qkv, pos)
+        assert np.array_equal(q, ring.append(qkv, pos))
+        _check_ring(ctx, ring, 0, range(B))
+
+
 def test_non_wrapping_ring_reports_range_error():
     say("non-wrapping ring overflow")
     with mb.Context(n_layers=1, capacity=8, max_seqs=1, max_rows=8, wrap=False) as ctx:
