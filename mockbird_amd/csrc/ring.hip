@@ -458,14 +458,4 @@ int launch_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, int64
                      out, out_stride, out_stride);
 }
 
-int launch_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
-                             int q_dtype, int64_t q_row_stride, int64_t q_seq_stride,
-                             const int32_t* pos0, const int32_t* n_rows, float* out,
-                             int64_t out_row_stride, int64_t out_seq_stride) {
-  if (q_dtype != MB_DT_F32)
-    return fail(ctx, MB_ERR_ARG, "the row-wise prefill attention takes fp32 queries");
-  return launch_attn(ctx, layer, B, rows_max, (const float*)q, q_row_stride, q_seq_stride, pos0,
-                     n_rows, ctx->cfg.capacity, out, out_row_stride, out_seq_stride);
-}
-
 }  // namespace mb

@@ -94,6 +94,10 @@ float or_bf16_round(float x) {
   return r;
 }
 
+void or_bf16_round_array(const float* x, int64_t n, float* out) {
+  for (int64_t i = 0; i < n; i++) out[i] = or_bf16_round(x[i]);
+}
+
 /* cos/sin of one RoPE pair at an absolute position (fp32 angle, fp32 result). */
 static void rope_cs(int64_t pos, int i, float* c, float* s) {
   float a = (float)pos * bits_to_f(OR_INV_FREQ_BITS[i]);

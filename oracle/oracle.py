@@ -44,6 +44,7 @@ def lib():
         L.or_inv_freq.argtypes = [_f32p]
         L.or_bf16_round.argtypes = [C.c_float]
         L.or_bf16_round.restype = C.c_float
+        L.or_bf16_round_array.argtypes = [_f32p, C.c_int64, _f32p]
         L.or_rope.argtypes = [_f32p, C.c_int, C.c_int64, _f32p]
         L.or_slot_of.argtypes = [C.c_int64, C.c_int, C.c_int]
         L.or_slot_live.argtypes = [C.c_int64, C.c_int64, C.c_int]
@@ -86,8 +87,10 @@ def inv_freq() -> np.ndarray:
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
-    f = np.vectorize(lambda v: lib().or_bf16_round(float(v)), otypes=[np.float32])
-    return f(np.asarray(x, np.float32))
+    x = _c(x, np.float32)
+    out = np.empty_like(x)
+    lib().or_bf16_round_array(x, x.size, out)
+    return out
 
 
 def rope(x: np.ndarray, pos: int) -> np.ndarray:

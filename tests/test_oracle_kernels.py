@@ -142,3 +142,18 @@ def test_gelu_tanh_vs_torch():
     ref = torch.nn.functional.gelu(torch.from_numpy(x).double(), approximate="tanh").numpy()
     assert np.abs(oracle.gelu(x) - ref).max() < 1e-6
     assert oracle.gelu(np.float32(0.0)) == 0.0
+
+
+def test_bf16_rounding_matches_torch():
+    """Round-to-nearest-even to bf16, checked against torch's own conversion,
+    including exact ties, the largest finite values and infinities."""
+    torch = pytest.importorskip("torch")
+    g = np.random.default_rng(9)
+    x = np.concatenate([
+        g.standard_normal(100000).astype(np.float32) * 10,
+        np.array([1 + 2**-8, 1 + 3 * 2**-8, -(1 + 2**-8), 3.4e38, -3.4e38, 1e-40, 0.0, -0.0,
+                  np.inf, -np.inf], np.float32),
+    ])
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    got = oracle.bf16_round(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
