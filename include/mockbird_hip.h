@@ -170,6 +170,53 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
                              int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out);
 
+/* ------------------------------------------------------------------ model
+ * The decoder around the rings, fp32 weights uploaded with mb_upload_tensor.
+ * Row ids are int32 [17]: text id in column 0 (< vocab), audio codes in
+ * columns 1..16 (< 1024, or 1024 = pad), as promptRows.ts:1-44 lays them out. */
+
+/* Local-head settings (LocalHeadSettings, gpu.ts:59-63): the text-head
+ * columns of audio_end and assistant_slot (7, 9) and the repetition penalty
+ * (1.2).  Those are also the defaults. */
+int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, float penalty);
+
+/* Global prefill of sequences b < B: ids [B][rows_max][17], n_rows[b] rows at
+ * positions 0 .. n_rows[b]-1 (n_rows[b] <= capacity).  Each sequence's rings
+ * are emptied first (a new utterance), every layer's K/V is written from
+ * slot 0, and last_hidden[b][768] receives ln_f of the sequence's last row.
+ * Replaces GpuTtsEngine.prefill / PrefillRunner.run (gpu.ts:173-192,
+ * prefill.ts:325-603). */
+int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+               float* last_hidden);
+
+/* One global decode step for sequences b < B: embed rows17[b][17], run every
+ * layer at position pos[b] (appending K/V to each layer's ring) and write
+ * ln_f into hidden[b][768].  Replaces GpuTtsEngine.decodeStep /
+ * DecodeRunner.globalStep (gpu.ts:244-258, decode.ts:712-775). */
+int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, float* hidden);
+
+/* The 17-step local frame head for sequences b < B from the global hidden
+ * state hidden[b][768]: cont[b] = 1 when the text head chooses the
+ * assistant slot over audio_end, then 16 greedy codes with the repetition
+ * penalty on each channel's history (codes[b][16]).  A sequence that stops
+ * keeps its history unchanged.  Replaces GpuTtsEngine.nextFrame /
+ * DecodeRunner.nextFrame (gpu.ts:268-272, decode.ts:788-939). */
+int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont);
+
+/* Forget the repetition history of `n` sequences (n < 0: all) -- the
+ * clearSeen part of engine.reset (decode.ts:276-280, gpu.ts:237-242). */
+int mb_clear_seen(mb_ctx* ctx, int n, const int32_t* seq_ids);
+
+/* Device-pointer forms.  mb_decode_step_dev takes rows17 [B][17], pos [B]
+ * (every pos <= max_pos) and hidden [B][768] in device memory;
+ * mb_local_frame_dev writes codes [B][16], cont [B] and, when rows17_out is
+ * not NULL, the next frame rows [assistant_id, codes...] (buildFrameRow,
+ * policy.ts:83-88), all in device memory (any output may be NULL). */
+int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos,
+                       int32_t max_pos, float* hidden);
+int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
+                       int32_t* rows17_out);
+
 #ifdef __cplusplus
 }
 #endif

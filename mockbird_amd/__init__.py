@@ -28,6 +28,8 @@ EXPORTS = (
     "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_ring_append", "mb_ring_write_rows",
     "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
+    "mb_set_local_head", "mb_prefill", "mb_decode_step", "mb_local_frame", "mb_clear_seen",
+    "mb_decode_step_dev", "mb_local_frame_dev",
 )
 
 
@@ -93,6 +95,13 @@ def load():
                                     C.c_int),
         "mb_prefill_attention_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp],
                                      C.c_int),
+        "mb_set_local_head": ([_vp, _i32, _i32, _f32], C.c_int),
+        "mb_prefill": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_decode_step": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_local_frame": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_clear_seen": ([_vp, C.c_int, _vp], C.c_int),
+        "mb_decode_step_dev": ([_vp, C.c_int, _vp, _vp, _i32, _vp], C.c_int),
+        "mb_local_frame_dev": ([_vp, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -247,3 +256,46 @@ class Context:
                               q_dtype=MB_DT_F32):
         self.check(self.lib.mb_prefill_attention_dev(self.h, layer, B, rows_max, q_ptr, q_dtype,
                                                      pos0_ptr, n_ptr, out_ptr))
+
+    # -- model
+    def set_local_head(self, audio_end_id: int = 7, assistant_id: int = 9, penalty: float = 1.2):
+        self.check(self.lib.mb_set_local_head(self.h, audio_end_id, assistant_id, penalty))
+
+    def prefill(self, ids: np.ndarray, n_rows) -> np.ndarray:
+        """ids [B][rows_max][17] -> last-row hidden [B][768]."""
+        ids, n_rows = _i32c(ids), _i32c(n_rows)
+        B, R = ids.shape[0], ids.shape[1]
+        out = np.zeros((B, D), np.float32)
+        self.check(self.lib.mb_prefill(self.h, B, R, ids.ctypes.data, n_rows.ctypes.data,
+                                       out.ctypes.data))
+        return out
+
+    def decode_step(self, rows17: np.ndarray, pos) -> np.ndarray:
+        rows17, pos = _i32c(rows17), _i32c(pos)
+        out = np.zeros((rows17.shape[0], D), np.float32)
+        self.check(self.lib.mb_decode_step(self.h, rows17.shape[0], rows17.ctypes.data,
+                                           pos.ctypes.data, out.ctypes.data))
+        return out
+
+    def local_frame(self, hidden: np.ndarray):
+        hidden = _f32c(hidden)
+        B = hidden.shape[0]
+        codes = np.zeros((B, NVQ), np.int32)
+        cont = np.zeros(B, np.int32)
+        self.check(self.lib.mb_local_frame(self.h, B, hidden.ctypes.data, codes.ctypes.data,
+                                           cont.ctypes.data))
+        return codes, cont.astype(bool)
+
+    def clear_seen(self, seq_ids=None):
+        if seq_ids is None:
+            self.check(self.lib.mb_clear_seen(self.h, -1, None))
+        else:
+            s = _i32c(seq_ids)
+            self.check(self.lib.mb_clear_seen(self.h, s.size, s.ctypes.data))
+
+    def decode_step_dev(self, B, rows_ptr, pos_ptr, max_pos, hidden_ptr):
+        self.check(self.lib.mb_decode_step_dev(self.h, B, rows_ptr, pos_ptr, max_pos, hidden_ptr))
+
+    def local_frame_dev(self, B, hidden_ptr, codes_ptr, cont_ptr, rows_out_ptr):
+        self.check(self.lib.mb_local_frame_dev(self.h, B, hidden_ptr, codes_ptr, cont_ptr,
+                                               rows_out_ptr))

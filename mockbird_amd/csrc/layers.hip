@@ -1,0 +1,235 @@
+// Per-layer glue of the decoder on gfx950: LayerNorm, row embedding, the
+// local head's embeddings, the continue/stop text-head decision, greedy
+// argmax with the repetition penalty, and frame-row feedback.
+#include "mb_internal.h"
+
+namespace mb {
+
+// ---------------------------------------------------------------- LayerNorm
+
+// One wave per row of 768 (12 values per lane): mean, then the centred
+// second moment, eps 1e-5, y = (x - mean) * rsqrt * w + b
+// (LAYERNORM_ROWS, kernels-batch.ts:99-147; ref-decode.mjs:85-99).
+// src_row (optional) maps output row i to input row src_row[i].
+__global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, int64_t ldx,
+                                                   const int32_t* __restrict__ src_row, int M,
+                                                   const float* __restrict__ w,
+                                                   const float* __restrict__ bb,
+                                                   float* __restrict__ y, int64_t ldy) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const float* xr = x + (int64_t)(src_row ? src_row[row] : row) * ldx;
+  float v[12];
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const float4 t = *(const float4*)(xr + i * 256 + lane * 4);
+    v[i * 4] = t.x; v[i * 4 + 1] = t.y; v[i * 4 + 2] = t.z; v[i * 4 + 3] = t.w;
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 12; i++) s += v[i];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  const float mean = s * (1.f / 768.f);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 12; i++) {
+    const float d = v[i] - mean;
+    q = fmaf(d, d, q);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
+  const float inv = 1.f / sqrtf(q * (1.f / 768.f) + 1e-5f);
+  float* yr = y + (int64_t)row * ldy;
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    const int c = i * 256 + lane * 4;
+    const float4 ww = *(const float4*)(w + c), bv = *(const float4*)(bb + c);
+    *(float4*)(yr + c) = make_float4((v[i * 4] - mean) * inv * ww.x + bv.x,
+                                     (v[i * 4 + 1] - mean) * inv * ww.y + bv.y,
+                                     (v[i * 4 + 2] - mean) * inv * ww.z + bv.z,
+                                     (v[i * 4 + 3] - mean) * inv * ww.w + bv.w);
+  }
+}
+
+int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,
+                     const float* w, const float* b, float* y, int64_t ldy) {
+  if (M <= 0) return MB_OK;
+  hipLaunchKernelGGL(k_layernorm, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, ctx->stream, x, ldx,
+                     src_row, M, w, b, y, ldy);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// ------------------------------------------------------------------ embedding
+
+// x[row] = wte[ids[row][0]] + sum_k audio_k[ids[row][1+k]], pad (1024) skipped,
+// summed in fp32 in channel order (EMBED_ROWS, kernels-batch.ts:45-92;
+// embedRowFor, promptRows.ts:21-36).  An id outside its table contributes
+// nothing (the host rejects such ids before launching).
+__global__ __launch_bounds__(256) void k_embed_rows(const int32_t* __restrict__ ids, int M,
+                                                    const float* __restrict__ wte, int vocab,
+                                                    AudioTables audio, float* __restrict__ x) {
+  const int row = blockIdx.x;
+  if (row >= M) return;
+  const int32_t* id = ids + (int64_t)row * ROW;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = 0.f;
+    const int t = id[0];
+    if (t >= 0 && t < vocab) acc = wte[(int64_t)t * D + d];
+    for (int k = 0; k < NVQ; k++) {
+      const int a = id[1 + k];
+      if (a == PAD || a < 0 || a >= CODES) continue;
+      acc = acc + audio.t[k][(int64_t)a * D + d];
+    }
+    x[(int64_t)row * D + d] = acc;
+  }
+}
+
+int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, int vocab,
+                      const AudioTables& audio, float* x) {
+  if (M <= 0) return MB_OK;
+  hipLaunchKernelGGL(k_embed_rows, dim3((unsigned)M), dim3(256), 0, ctx->stream, ids, M, wte, vocab,
+                     audio, x);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// The local head's step embeddings (EMBED_ROW_LOCAL modes 1 and 2,
+// kernels-decode.ts:96-124; ref-decode.mjs:238-251):
+//   step 1:  wte[assistant_id]
+//   step s>1: audio_{s-2}[tokens[b][s-2]]  (the previous channel's code)
+__global__ __launch_bounds__(256) void k_embed_local(int step, int B, const float* __restrict__ wte,
+                                                     int assistant_id, AudioTables audio,
+                                                     const int32_t* __restrict__ tokens,
+                                                     float* __restrict__ x) {
+  const int b = blockIdx.x;
+  if (b >= B) return;
+  const float* src;
+  if (step == 1) {
+    src = wte + (int64_t)assistant_id * D;
+  } else {
+    int t = tokens[b * NVQ + step - 2];
+    t = t < 0 ? 0 : (t >= CODES ? CODES - 1 : t);
+    src = audio.t[step - 2] + (int64_t)t * D;
+  }
+  for (int d = threadIdx.x; d < D; d += 256) x[(int64_t)b * D + d] = src[d];
+}
+
+int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
+                       const AudioTables& audio, const int32_t* tokens, float* x) {
+  hipLaunchKernelGGL(k_embed_local, dim3((unsigned)B), dim3(256), 0, ctx->stream, step, B, wte,
+                     assistant_id, audio, tokens, x);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// ------------------------------------------------------------ greedy choice
+
+// Continue/stop: two double-precision dot products of the step-0 hidden
+// state with text-head columns end_id and assistant_id; continue iff
+// assistant >= end (TEXT_HEAD_DECIDE kernels-decode.ts:487-518,
+// decideAssistantStop policy.ts:297-302).  One wave per sequence.
+__global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h, int B,
+                                                     const float* __restrict__ head, int vocab,
+                                                     int end_id, int assistant_id,
+                                                     int32_t* __restrict__ cont) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  double e = 0.0, a = 0.0;
+  for (int d = lane; d < D; d += 64) {
+    const double x = h[(int64_t)b * D + d];
+    e += x * (double)head[(int64_t)d * vocab + end_id];
+    a += x * (double)head[(int64_t)d * vocab + assistant_id];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    e += __shfl_xor(e, off);
+    a += __shfl_xor(a, off);
+  }
+  if (lane == 0) cont[b] = a >= e ? 1 : 0;
+}
+
+int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
+                       int assistant_id, int32_t* cont) {
+  hipLaunchKernelGGL(k_text_decide, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream, h, B,
+                     head, vocab, end_id, assistant_id, cont);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// Greedy argmax over 1024 logits with the HuggingFace repetition penalty on
+// this channel's seen set: a seen id's score is multiplied by the penalty
+// when negative and divided when not, formed in double as the JS reference
+// does (argmaxWithRepetitionPenalty, policy.ts:273-290; ARGMAX_PENALTY,
+// kernels-decode.ts:428-478).  Strict '>' keeps the lowest id on ties and a
+// NaN never wins.  The winner goes to tokens[b][ch]; the seen bit is set only
+// for sequences that continue (the reference stops before drawing codes).
+__global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
+                                                        int ch, float penalty,
+                                                        uint32_t* __restrict__ seen,
+                                                        const int32_t* __restrict__ cont,
+                                                        int32_t* __restrict__ tokens) {
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  uint32_t* sm = seen + ((int64_t)b * NVQ + ch) * 32;
+  // the penalty applies once the channel has emitted anything (policy.ts:282)
+  uint32_t any = lane < 32 ? sm[lane] : 0u;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) any |= __shfl_xor(any, off);
+  const bool apply = any != 0u && penalty != 1.f;
+  double best = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = lane; i < CODES; i += 64) {
+    double s = logits[(int64_t)b * CODES + i];
+    if (apply && ((sm[i >> 5] >> (i & 31)) & 1u)) s = s < 0 ? s * (double)penalty : s / (double)penalty;
+    if (s > best) {
+      best = s;
+      idx = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const double ob = __shfl_xor(best, off);
+    const int oi = __shfl_xor(idx, off);
+    if (ob > best || (ob == best && oi < idx)) {
+      best = ob;
+      idx = oi;
+    }
+  }
+  if (lane == 0) {
+    const int tok = idx == 0x7fffffff ? 0 : idx;
+    tokens[b * NVQ + ch] = tok;
+    if (!cont || cont[b]) sm[tok >> 5] |= 1u << (tok & 31);
+  }
+}
+
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
+                          uint32_t* seen, const int32_t* cont, int32_t* tokens) {
+  hipLaunchKernelGGL(k_argmax_penalty, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream,
+                     logits, B, ch, penalty, seen, cont, tokens);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// Frame row fed back to the global transformer: [assistant_id, codes...]
+// (buildFrameRow, policy.ts:83-88).
+__global__ void k_frame_rows(const int32_t* __restrict__ tokens, int B, int assistant_id,
+                             int32_t* __restrict__ rows17) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * ROW) return;
+  const int b = i / ROW, c = i % ROW;
+  rows17[i] = c == 0 ? assistant_id : tokens[b * NVQ + c - 1];
+}
+
+int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17) {
+  hipLaunchKernelGGL(k_frame_rows, dim3((unsigned)((B * ROW + 255) / 256)), dim3(256), 0,
+                     ctx->stream, tokens, B, assistant_id, rows17);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+}  // namespace mb

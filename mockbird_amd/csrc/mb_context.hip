@@ -181,6 +181,9 @@ void mb_destroy(mb_ctx* ctx) {
   (void)hipFree(ctx->ring_v);
   (void)hipFree(ctx->slot_pos);
   (void)hipFree(ctx->rope_tab);
+  for (void* p : {(void*)ctx->local_k, (void*)ctx->local_v, (void*)ctx->local_sp,
+                  (void*)ctx->local_pos, (void*)ctx->seen, (void*)ctx->tokens, (void*)ctx->cont})
+    (void)hipFree(p);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
 }
@@ -237,6 +240,7 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
   }
   t.numel = numel;
   t.dims.assign(dims, dims + ndims);
+  ctx->model_ok = false;
   MB_HIP(ctx, hipMemcpyAsync(t.ptr, data, (size_t)numel * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;
@@ -338,8 +342,9 @@ int mb_ring_write_rows_dev(mb_ctx* ctx, int layer, int B, int rows_max, const vo
     return fail(ctx, MB_ERR_ARG, "unknown dtype");
   if (B == 0) return MB_OK;
   if (!qkv || !pos0 || !n_rows) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return launch_ring_write(ctx, layer, B, rows_max, qkv, qkv_dtype, QKV, (int64_t)rows_max * QKV,
-                           pos0, n_rows, q_out, q_dtype, D, (int64_t)rows_max * D);
+  return launch_ring_write(ctx, global_ring(ctx, layer), B, rows_max, qkv, qkv_dtype,
+                           dense_rows(QKV, rows_max), pos0, n_rows, q_out, q_dtype,
+                           dense_rows(D, rows_max));
 }
 
 int mb_ring_append_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
@@ -352,8 +357,9 @@ int mb_ring_append_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_d
     return fail(ctx, MB_ERR_ARG, "row stride too small");
   if (B == 0) return MB_OK;
   if (!qkv || !pos) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return launch_ring_write(ctx, layer, B, 1, qkv, qkv_dtype, qkv_stride, qkv_stride, pos, nullptr,
-                           q_out, MB_DT_F32, q_stride, q_stride);
+  return launch_ring_write(ctx, global_ring(ctx, layer), B, 1, qkv, qkv_dtype,
+                           dense_rows(qkv_stride, 1), pos, nullptr, q_out, MB_DT_F32,
+                           dense_rows(q_stride, 1));
 }
 
 int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
@@ -364,7 +370,8 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
   if (max_pos < 0) return fail(ctx, MB_ERR_ARG, "max_pos %d is negative", max_pos);
   if (B == 0) return MB_OK;
   if (!q || !pos || !out) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return launch_decode_attention(ctx, layer, B, q, q_stride, pos, max_pos, out, out_stride);
+  return launch_attn(ctx, global_ring(ctx, layer), B, 1, q, dense_rows(q_stride, 1), pos, nullptr,
+                     (int64_t)max_pos + 1, out, dense_rows(out_stride, 1));
 }
 
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
@@ -376,8 +383,9 @@ int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const 
   if (q_dtype != MB_DT_F32 && q_dtype != MB_DT_BF16) return fail(ctx, MB_ERR_ARG, "unknown dtype");
   if (B == 0) return MB_OK;
   if (!q || !pos0 || !n_rows || !out) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return launch_prefill_attention(ctx, layer, B, rows_max, q, q_dtype, D, (int64_t)rows_max * D,
-                                  pos0, n_rows, out, D, (int64_t)rows_max * D);
+  return launch_prefill_attention(ctx, global_ring(ctx, layer), B, rows_max, q, q_dtype,
+                                  dense_rows(D, rows_max), pos0, n_rows, out,
+                                  dense_rows(D, rows_max));
 }
 
 // ---------------------------------------------------------- host pointers
@@ -400,9 +408,9 @@ int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float*
   MB_HIP(ctx, hipMemcpyAsync(d_qkv, qkv, rows * QKV * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos, pos0, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos + B, n_rows, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
-  rc = launch_ring_write(ctx, layer, B, rows_max, d_qkv, MB_DT_F32, QKV, (int64_t)rows_max * QKV,
-                         d_pos, d_pos + B, q_out ? d_q : nullptr, MB_DT_F32, D,
-                         (int64_t)rows_max * D);
+  rc = launch_ring_write(ctx, global_ring(ctx, layer), B, rows_max, d_qkv, MB_DT_F32,
+                         dense_rows(QKV, rows_max), d_pos, d_pos + B, q_out ? d_q : nullptr,
+                         MB_DT_F32, dense_rows(D, rows_max));
   if (rc) return rc;
   if (q_out) MB_HIP(ctx, hipMemcpyAsync(q_out, d_q, rows * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -423,8 +431,8 @@ int mb_ring_append(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_
   if (!d_qkv || !d_q || !d_pos) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
   MB_HIP(ctx, hipMemcpyAsync(d_qkv, qkv, (size_t)B * QKV * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos, pos, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
-  rc = launch_ring_write(ctx, layer, B, 1, d_qkv, MB_DT_F32, QKV, QKV, d_pos, nullptr,
-                         q_out ? d_q : nullptr, MB_DT_F32, D, D);
+  rc = launch_ring_write(ctx, global_ring(ctx, layer), B, 1, d_qkv, MB_DT_F32, dense_rows(QKV, 1),
+                         d_pos, nullptr, q_out ? d_q : nullptr, MB_DT_F32, dense_rows(D, 1));
   if (rc) return rc;
   if (q_out) MB_HIP(ctx, hipMemcpyAsync(q_out, d_q, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -448,7 +456,8 @@ int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int
   if (!d_q || !d_out || !d_pos) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
   MB_HIP(ctx, hipMemcpyAsync(d_q, q, (size_t)B * D * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos, pos, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
-  rc = launch_decode_attention(ctx, layer, B, d_q, D, d_pos, max_pos, d_out, D);
+  rc = launch_attn(ctx, global_ring(ctx, layer), B, 1, d_q, dense_rows(D, 1), d_pos, nullptr,
+                   (int64_t)max_pos + 1, d_out, dense_rows(D, 1));
   if (rc) return rc;
   MB_HIP(ctx, hipMemcpyAsync(out, d_out, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -473,8 +482,9 @@ int mb_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const floa
   MB_HIP(ctx, hipMemcpyAsync(d_q, q, rows * D * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos, pos0, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(d_pos + B, n_rows, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
-  rc = launch_prefill_attention(ctx, layer, B, rows_max, d_q, MB_DT_F32, D, (int64_t)rows_max * D,
-                                d_pos, d_pos + B, d_out, D, (int64_t)rows_max * D);
+  rc = launch_prefill_attention(ctx, global_ring(ctx, layer), B, rows_max, d_q, MB_DT_F32,
+                                dense_rows(D, rows_max), d_pos, d_pos + B, d_out,
+                                dense_rows(D, rows_max));
   if (rc) return rc;
   MB_HIP(ctx, hipMemcpyAsync(out, d_out, rows * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -57,6 +57,31 @@ struct Scratch {
 
 }  // namespace mb
 
+namespace mb {
+
+// The 16 audio-embedding tables (or heads), passed by value to kernels.
+struct AudioTables {
+  const float* t[NVQ];
+};
+
+// Device pointers of one d=768 transformer layer ([K, N] row-major matrices).
+struct LayerW {
+  const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
+  const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
+};
+
+// Every weight a model call needs, resolved from the uploaded tensors.
+struct ModelW {
+  std::vector<LayerW> layers;
+  const float *lnf_w, *lnf_b, *wte;
+  AudioTables audio_emb;
+  LayerW local;
+  const float *local_lnf_w, *local_lnf_b, *text_head;
+  AudioTables audio_heads;
+};
+
+}  // namespace mb
+
 struct mb_ctx {
   mb_config cfg{};
   int device = 0;
@@ -79,6 +104,21 @@ struct mb_ctx {
 
 
   std::map<std::string, mb::DeviceTensor> weights;
+  mb::ModelW model{};
+  bool model_ok = false;       // `model` resolved since the last upload
+  int32_t end_id = 7;          // audio_end_token_id
+  int32_t assistant_id = 9;    // audio_assistant_slot_token_id
+  float penalty = 1.2f;        // audio_repetition_penalty
+
+  // Local head state: a 17-slot fp32 cache per sequence, the per-channel
+  // repetition history, the last frame's codes and continue flags.
+  float* local_k = nullptr;
+  float* local_v = nullptr;
+  int32_t* local_sp = nullptr;
+  int32_t* local_pos = nullptr;  // [17][max_seqs], row s filled with s
+  uint32_t* seen = nullptr;      // [max_seqs][16][32]
+  int32_t* tokens = nullptr;     // [max_seqs][16]
+  int32_t* cont = nullptr;       // [max_seqs]
   std::map<std::string, mb::Scratch> scratch;
   int64_t device_bytes = 0;
   std::atomic<int> cancel{0};
@@ -111,18 +151,67 @@ inline int64_t slot_base(const mb_ctx* ctx, int layer, int seq) {
   return ((int64_t)layer * ctx->cfg.max_seqs + seq) * (int64_t)ctx->cfg.capacity;
 }
 
-// Kernel launchers (ring.hip).
-int launch_ring_write(mb_ctx* ctx, int layer, int B, int rows_max, const void* qkv, int qkv_dtype,
-                      int64_t qkv_row_stride, int64_t qkv_seq_stride, const int32_t* pos0,
-                      const int32_t* n_rows, void* q_out, int q_dtype, int64_t q_row_stride,
-                      int64_t q_seq_stride);
-int launch_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
-                            const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride);
+// A ring as the kernels see it: sequence 0's K/V/slot positions for one
+// layer (or for the local head's 17-slot cache).
+struct RingView {
+  void* k = nullptr;
+  void* v = nullptr;
+  int32_t* sp = nullptr;
+  int64_t seq_stride = 0;  // K/V elements between consecutive sequences
+  int C = 0;
+  int wrap = 1;
+  bool bf16 = false;
+};
+RingView global_ring(const mb_ctx* ctx, int layer);
+
+// Row addressing of a batched [B][rows] operand: row r of sequence b starts
+// at element row_off ? (row_off[b] + r) * row_stride : b * seq_stride + r * row_stride
+// (row_off packs ragged sequences back to back).
+struct Rows {
+  int64_t row_stride = 0;
+  int64_t seq_stride = 0;
+  const int32_t* row_off = nullptr;
+};
+inline Rows dense_rows(int64_t row_stride, int rows_max) {
+  Rows r;
+  r.row_stride = row_stride;
+  r.seq_stride = row_stride * rows_max;
+  return r;
+}
+__host__ __device__ inline int64_t row_at(const Rows& R, int b, int r) {
+  return R.row_off ? ((int64_t)R.row_off[b] + r) * R.row_stride
+                   : (int64_t)b * R.seq_stride + (int64_t)r * R.row_stride;
+}
+
+// Kernel launchers (ring.hip, prefill.hip).
+int launch_ring_write(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const void* qkv,
+                      int qkv_dtype, const Rows& qkv_rows, const int32_t* pos0,
+                      const int32_t* n_rows, void* q_out, int q_dtype, const Rows& q_rows);
+int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
+                const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
+                float* out, const Rows& out_rows);
+int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
+                             const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
+                             const int32_t* n_rows, float* out, const Rows& out_rows);
 int launch_fill_i32(mb_ctx* ctx, int32_t* p, int64_t n, int32_t value);
 int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value);
-int launch_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
-                             int q_dtype, int64_t q_row_stride, int64_t q_seq_stride,
-                             const int32_t* pos0, const int32_t* n_rows, float* out,
-                             int64_t out_row_stride, int64_t out_seq_stride);
+
+// gemm.hip
+enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2 };
+int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
+                const float* bias, float* Cm, int64_t ldc, int M);
+
+// layers.hip
+int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,
+                     const float* w, const float* b, float* y, int64_t ldy);
+int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, int vocab,
+                      const AudioTables& audio, float* x);
+int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
+                       const AudioTables& audio, const int32_t* tokens, float* x);
+int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
+                       int assistant_id, int32_t* cont);
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
+                          uint32_t* seen, const int32_t* cont, int32_t* tokens);
+int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);
 
 }  // namespace mb

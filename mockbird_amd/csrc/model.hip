@@ -1,0 +1,431 @@
+// The decoder around the ring: global prefill, one global decode step, and
+// the 17-step local frame head, each a sequence of launches on the context's
+// stream (LN -> QKV GEMM -> RoPE + ring write -> attention -> O GEMM (+x) ->
+// LN -> fc_in GEMM (+GELU) -> fc_out GEMM (+x) per layer; ref-decode.mjs:
+// 175-272 and decode.ts:474-620 give the order, including that each layer's
+// MLP follows its own attention).
+#include <cstring>
+
+#include "mb_internal.h"
+
+namespace mb {
+
+namespace {
+
+const DeviceTensor* find(mb_ctx* ctx, const std::string& name, std::initializer_list<int64_t> dims,
+                         std::string& missing) {
+  auto it = ctx->weights.find(name);
+  if (it == ctx->weights.end()) {
+    if (missing.empty()) missing = "weight not uploaded: " + name;
+    return nullptr;
+  }
+  const DeviceTensor& t = it->second;
+  if (t.dims.size() != dims.size() || !std::equal(dims.begin(), dims.end(), t.dims.begin())) {
+    if (missing.empty()) missing = "weight has the wrong shape: " + name;
+    return nullptr;
+  }
+  return &t;
+}
+
+int resolve_layer(mb_ctx* ctx, const std::string& p, LayerW& w, std::string& missing) {
+  auto get = [&](const char* n, std::initializer_list<int64_t> d) {
+    const DeviceTensor* t = find(ctx, p + n, d, missing);
+    return t ? (const float*)t->ptr : nullptr;
+  };
+  w.ln1_w = get("ln_1.weight", {D});
+  w.ln1_b = get("ln_1.bias", {D});
+  w.attn_w = get("attn.c_attn.weight", {D, QKV});
+  w.attn_b = get("attn.c_attn.bias", {QKV});
+  w.proj_w = get("attn.c_proj.weight", {D, D});
+  w.proj_b = get("attn.c_proj.bias", {D});
+  w.ln2_w = get("ln_2.weight", {D});
+  w.ln2_b = get("ln_2.bias", {D});
+  w.fc_in_w = get("mlp.fc_in.weight", {D, FFN});
+  w.fc_in_b = get("mlp.fc_in.bias", {FFN});
+  w.fc_out_w = get("mlp.fc_out.weight", {FFN, D});
+  w.fc_out_b = get("mlp.fc_out.bias", {D});
+  return missing.empty() ? MB_OK : MB_ERR_STATE;
+}
+
+// Resolve every weight once per upload (gpu.ts:339-343 throws "weight not
+// uploaded" the same way).  `local` selects the local-head half.
+int resolve(mb_ctx* ctx, bool global, bool local) {
+  if (ctx->model_ok) return MB_OK;
+  std::string missing;
+  ModelW& m = ctx->model;
+  const int64_t V = ctx->cfg.vocab;
+  if (V < 10) return fail(ctx, MB_ERR_STATE, "mb_config.vocab must cover the text ids (>= 10)");
+  auto get = [&](const std::string& n, std::initializer_list<int64_t> d) {
+    const DeviceTensor* t = find(ctx, n, d, missing);
+    return t ? (const float*)t->ptr : nullptr;
+  };
+  m.wte = get("core.model.transformer.wte.weight", {V, D});
+  for (int k = 0; k < NVQ; k++)
+    m.audio_emb.t[k] = get("core.model.audio_embeddings." + std::to_string(k) + ".weight", {CODES, D});
+  if (global) {
+    m.layers.assign(ctx->cfg.n_layers, LayerW{});
+    for (int l = 0; l < ctx->cfg.n_layers; l++)
+      resolve_layer(ctx, "core.model.transformer.h." + std::to_string(l) + ".", m.layers[l], missing);
+    m.lnf_w = get("core.model.transformer.ln_f.weight", {D});
+    m.lnf_b = get("core.model.transformer.ln_f.bias", {D});
+  }
+  if (local) {
+    resolve_layer(ctx, "model.local_transformer.h.0.", m.local, missing);
+    m.local_lnf_w = get("model.local_transformer.ln_f.weight", {D});
+    m.local_lnf_b = get("model.local_transformer.ln_f.bias", {D});
+    m.text_head = get("model.text_lm_head.weight", {D, V});
+    for (int k = 0; k < NVQ; k++)
+      m.audio_heads.t[k] = get("model.audio_lm_heads." + std::to_string(k) + ".weight", {D, CODES});
+  }
+  if (!missing.empty()) return fail(ctx, MB_ERR_STATE, "%s", missing.c_str());
+  if (global && local) ctx->model_ok = true;
+  return MB_OK;
+}
+
+int need_model(mb_ctx* ctx) {
+  if (ctx->model_ok) return MB_OK;
+  return resolve(ctx, true, true);
+}
+
+struct Act {
+  float *x, *norm, *qkv, *q, *att, *ffn, *logits;
+};
+
+int activations(mb_ctx* ctx, int64_t M, Act& a) {
+  a.x = (float*)scratch(ctx, "act_x", (size_t)M * D * 4);
+  a.norm = (float*)scratch(ctx, "act_norm", (size_t)M * D * 4);
+  a.qkv = (float*)scratch(ctx, "act_qkv", (size_t)M * QKV * 4);
+  a.q = (float*)scratch(ctx, "act_q", (size_t)M * D * 4);
+  a.att = (float*)scratch(ctx, "act_att", (size_t)M * D * 4);
+  a.ffn = (float*)scratch(ctx, "act_ffn", (size_t)M * FFN * 4);
+  a.logits = (float*)scratch(ctx, "act_logits", (size_t)M * CODES * 4);
+  if (!a.x || !a.norm || !a.qkv || !a.q || !a.att || !a.ffn || !a.logits)
+    return fail(ctx, MB_ERR_NOMEM, "activation allocation failed (%lld rows)", (long long)M);
+  return MB_OK;
+}
+
+int cancelled(mb_ctx* ctx) {
+  if (ctx->cancel.load()) return fail(ctx, MB_ERR_CANCELLED, "cancelled");
+  return MB_OK;
+}
+
+// One d=768 layer over M rows held in a.x.  Rows belong to B sequences with
+// n_rows[b] rows at positions pos0[b] + r (packed by `packed` when prefill is
+// set, else one row per sequence).
+int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int rows_max, int64_t M,
+              const int32_t* pos0, const int32_t* n_rows, const int32_t* row_off, bool prefill,
+              int64_t max_valid, Act& a) {
+  int rc;
+  if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln1_w, w.ln1_b, a.norm, D))) return rc;
+  if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, w.attn_w, QKV, D, w.attn_b, a.qkv, QKV, (int)M)))
+    return rc;
+  Rows qkv_rows, q_rows;
+  if (prefill) {
+    qkv_rows.row_stride = QKV;
+    qkv_rows.row_off = row_off;
+    q_rows.row_stride = D;
+    q_rows.row_off = row_off;
+  } else {
+    qkv_rows = dense_rows(QKV, 1);
+    q_rows = dense_rows(D, 1);
+  }
+  if ((rc = launch_ring_write(ctx, ring, B, rows_max, a.qkv, MB_DT_F32, qkv_rows, pos0, n_rows,
+                              a.q, MB_DT_F32, q_rows)))
+    return rc;
+  if (prefill)
+    rc = launch_prefill_attention(ctx, ring, B, rows_max, a.q, MB_DT_F32, q_rows, pos0, n_rows,
+                                  a.att, q_rows);
+  else
+    rc = launch_attn(ctx, ring, B, 1, a.q, q_rows, pos0, nullptr, max_valid, a.att, q_rows);
+  if (rc) return rc;
+  if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, w.proj_w, D, D, w.proj_b, a.x, D, (int)M))) return rc;
+  if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln2_w, w.ln2_b, a.norm, D))) return rc;
+  if ((rc = launch_gemm(ctx, EPI_GELU, a.norm, D, w.fc_in_w, FFN, D, w.fc_in_b, a.ffn, FFN, (int)M)))
+    return rc;
+  return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_w, D, FFN, w.fc_out_b, a.x, D, (int)M);
+}
+
+// Local-head state, allocated on first use: every local slot empty, seen
+// masks clear, local positions [17][max_seqs] = step.
+int local_state(mb_ctx* ctx) {
+  if (ctx->local_k) return MB_OK;
+  const int64_t S = ctx->cfg.max_seqs;
+  const size_t kv = (size_t)S * H * ROW * HD * 4;
+  MB_HIP(ctx, hipMalloc(&ctx->local_k, kv));
+  MB_HIP(ctx, hipMalloc(&ctx->local_v, kv));
+  MB_HIP(ctx, hipMalloc(&ctx->local_sp, (size_t)S * ROW * 4));
+  MB_HIP(ctx, hipMalloc(&ctx->local_pos, (size_t)S * ROW * 4));
+  MB_HIP(ctx, hipMalloc(&ctx->seen, (size_t)S * NVQ * 32 * 4));
+  MB_HIP(ctx, hipMalloc(&ctx->tokens, (size_t)S * NVQ * 4));
+  MB_HIP(ctx, hipMalloc(&ctx->cont, (size_t)S * 4));
+  ctx->device_bytes += (int64_t)(2 * kv + S * ROW * 8 + S * NVQ * 32 * 4 + S * NVQ * 4 + S * 4);
+  int rc;
+  if ((rc = launch_fill_kv(ctx, ctx->local_k, (int64_t)kv / 4, 0.f))) return rc;
+  if ((rc = launch_fill_kv(ctx, ctx->local_v, (int64_t)kv / 4, 0.f))) return rc;
+  if ((rc = launch_fill_i32(ctx, ctx->local_sp, S * ROW, -1))) return rc;
+  for (int s = 0; s < ROW; s++)
+    if ((rc = launch_fill_i32(ctx, ctx->local_pos + (int64_t)s * S, S, s))) return rc;
+  if ((rc = launch_fill_i32(ctx, (int32_t*)ctx->seen, S * NVQ * 32, 0))) return rc;
+  if ((rc = launch_fill_i32(ctx, ctx->tokens, S * NVQ, 0))) return rc;
+  return launch_fill_i32(ctx, ctx->cont, S, 0);
+}
+
+RingView local_ring(mb_ctx* ctx) {
+  RingView v;
+  v.k = ctx->local_k;
+  v.v = ctx->local_v;
+  v.sp = ctx->local_sp;
+  v.seq_stride = (int64_t)H * ROW * HD;
+  v.C = ROW;
+  v.wrap = 0;
+  v.bf16 = false;
+  return v;
+}
+
+int check_ids(mb_ctx* ctx, const int32_t* ids, int64_t rows) {
+  for (int64_t r = 0; r < rows; r++) {
+    const int32_t* id = ids + r * ROW;
+    if (id[0] < 0 || id[0] >= ctx->cfg.vocab)
+      return fail(ctx, MB_ERR_ARG, "row %lld: text id %d outside [0, %d)", (long long)r, id[0],
+                  ctx->cfg.vocab);
+    for (int k = 1; k < ROW; k++)
+      if (id[k] < 0 || id[k] > PAD)
+        return fail(ctx, MB_ERR_ARG, "row %lld: audio id %d outside [0, 1024]", (long long)r, id[k]);
+  }
+  return MB_OK;
+}
+
+// Global decode step on device buffers (rows17, pos, hidden all device).
+int decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, int64_t max_pos,
+                float* hidden) {
+  int rc;
+  Act a;
+  if ((rc = activations(ctx, B, a))) return rc;
+  const ModelW& m = ctx->model;
+  if ((rc = launch_embed_rows(ctx, rows17, B, m.wte, ctx->cfg.vocab, m.audio_emb, a.x))) return rc;
+  for (int l = 0; l < ctx->cfg.n_layers; l++) {
+    if ((rc = cancelled(ctx))) return rc;
+    if ((rc = run_layer(ctx, m.layers[l], global_ring(ctx, l), B, 1, B, pos, nullptr, nullptr, false,
+                        max_pos + 1, a)))
+      return rc;
+  }
+  return launch_layernorm(ctx, a.x, D, nullptr, B, m.lnf_w, m.lnf_b, hidden, D);
+}
+
+// The 17-step local head on device buffers; codes/cont/rows17_out optional.
+int local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
+                int32_t* rows17_out) {
+  int rc;
+  if ((rc = local_state(ctx))) return rc;
+  Act a;
+  if ((rc = activations(ctx, B, a))) return rc;
+  const ModelW& m = ctx->model;
+  const RingView ring = local_ring(ctx);
+  const int64_t S = ctx->cfg.max_seqs;
+  for (int step = 0; step < ROW; step++) {
+    if ((rc = cancelled(ctx))) return rc;
+    if (step == 0)
+      MB_HIP(ctx, hipMemcpyAsync(a.x, hidden, (size_t)B * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
+    else if ((rc = launch_embed_local(ctx, step, B, m.wte, ctx->assistant_id, m.audio_emb,
+                                      ctx->tokens, a.x)))
+      return rc;
+    if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
+                        nullptr, false, step + 1, a)))
+      return rc;
+    if ((rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
+      return rc;
+    if (step == 0) {
+      rc = launch_text_decide(ctx, a.norm, B, m.text_head, ctx->cfg.vocab, ctx->end_id,
+                              ctx->assistant_id, ctx->cont);
+    } else {
+      const int ch = step - 1;
+      if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr,
+                            a.logits, CODES, B)))
+        return rc;
+      rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
+                                 ctx->tokens);
+    }
+    if (rc) return rc;
+  }
+  if (codes)
+    MB_HIP(ctx, hipMemcpyAsync(codes, ctx->tokens, (size_t)B * NVQ * 4, hipMemcpyDeviceToDevice,
+                               ctx->stream));
+  if (cont)
+    MB_HIP(ctx, hipMemcpyAsync(cont, ctx->cont, (size_t)B * 4, hipMemcpyDeviceToDevice, ctx->stream));
+  if (rows17_out) return launch_frame_rows(ctx, ctx->tokens, B, ctx->assistant_id, rows17_out);
+  return MB_OK;
+}
+
+int check_b(mb_ctx* ctx, int B) {
+  if (!ctx) return MB_ERR_ARG;
+  if (B < 0 || B > ctx->cfg.max_seqs)
+    return fail(ctx, MB_ERR_ARG, "B %d out of [0, %d]", B, ctx->cfg.max_seqs);
+  return MB_OK;
+}
+
+}  // namespace
+
+}  // namespace mb
+
+using namespace mb;
+
+extern "C" {
+
+int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, float penalty) {
+  if (!ctx) return MB_ERR_ARG;
+  if (audio_end_id < 0 || assistant_id < 0 || audio_end_id >= ctx->cfg.vocab ||
+      assistant_id >= ctx->cfg.vocab || !(penalty > 0.f))
+    return fail(ctx, MB_ERR_ARG, "local head settings out of range");
+  ctx->end_id = audio_end_id;
+  ctx->assistant_id = assistant_id;
+  ctx->penalty = penalty;
+  return MB_OK;
+}
+
+int mb_clear_seen(mb_ctx* ctx, int n, const int32_t* seq_ids) {
+  int rc = check_b(ctx, 0);
+  if (rc) return rc;
+  if ((rc = local_state(ctx))) return rc;
+  if (n < 0) {
+    rc = launch_fill_i32(ctx, (int32_t*)ctx->seen, (int64_t)ctx->cfg.max_seqs * NVQ * 32, 0);
+    if (rc) return rc;
+  } else {
+    if (n > 0 && !seq_ids) return fail(ctx, MB_ERR_ARG, "mb_clear_seen: seq_ids is null");
+    for (int i = 0; i < n; i++) {
+      if (seq_ids[i] < 0 || seq_ids[i] >= ctx->cfg.max_seqs)
+        return fail(ctx, MB_ERR_ARG, "mb_clear_seen: sequence %d out of range", seq_ids[i]);
+      rc = launch_fill_i32(ctx, (int32_t*)ctx->seen + (int64_t)seq_ids[i] * NVQ * 32, NVQ * 32, 0);
+      if (rc) return rc;
+    }
+  }
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+               float* last_hidden) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!ids || !n_rows || !last_hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
+    return fail(ctx, MB_ERR_ARG, "rows_max %d out of [1, %d]", rows_max, ctx->cfg.max_rows);
+  if ((rc = need_model(ctx))) return rc;
+  std::vector<int32_t> off(B), last(B), zeros(B, 0);
+  int64_t M = 0;
+  for (int b = 0; b < B; b++) {
+    if (n_rows[b] < 1 || n_rows[b] > rows_max)
+      return fail(ctx, MB_ERR_ARG, "prefill called with %d rows for sequence %d", n_rows[b], b);
+    if (n_rows[b] > ctx->cfg.capacity)
+      return fail(ctx, MB_ERR_RANGE, "prompt of %d rows exceeds the KV ring (%d slots)", n_rows[b],
+                  ctx->cfg.capacity);
+    off[b] = (int32_t)M;
+    M += n_rows[b];
+    last[b] = (int32_t)(M - 1);
+  }
+  std::vector<int32_t> packed((size_t)M * ROW);
+  for (int b = 0; b < B; b++)
+    memcpy(packed.data() + (size_t)off[b] * ROW, ids + (size_t)b * rows_max * ROW,
+           (size_t)n_rows[b] * ROW * 4);
+  if ((rc = check_ids(ctx, packed.data(), M))) return rc;
+  Act a;
+  if ((rc = activations(ctx, M, a))) return rc;
+  int32_t* d_ids = (int32_t*)scratch(ctx, "prefill_ids", (size_t)M * ROW * 4);
+  int32_t* d_meta = (int32_t*)scratch(ctx, "prefill_meta", (size_t)B * 4 * 4);
+  float* d_hidden = (float*)scratch(ctx, "hidden", (size_t)B * D * 4);
+  if (!d_ids || !d_meta || !d_hidden) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  int32_t* d_off = d_meta;
+  int32_t* d_n = d_meta + B;
+  int32_t* d_pos0 = d_meta + 2 * B;
+  int32_t* d_last = d_meta + 3 * B;
+  MB_HIP(ctx, hipMemcpyAsync(d_ids, packed.data(), (size_t)M * ROW * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_off, off.data(), (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_n, n_rows, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_pos0, zeros.data(), (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_last, last.data(), (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  // a fresh utterance per sequence: every slot of its rings forgets its position
+  for (int l = 0; l < ctx->cfg.n_layers; l++)
+    if ((rc = launch_fill_i32(ctx, ctx->slot_pos + slot_base(ctx, l, 0), (int64_t)B * ctx->cfg.capacity, -1)))
+      return rc;
+  const ModelW& m = ctx->model;
+  if ((rc = launch_embed_rows(ctx, d_ids, (int)M, m.wte, ctx->cfg.vocab, m.audio_emb, a.x))) return rc;
+  for (int l = 0; l < ctx->cfg.n_layers; l++) {
+    if ((rc = cancelled(ctx))) return rc;
+    if ((rc = run_layer(ctx, m.layers[l], global_ring(ctx, l), B, rows_max, M, d_pos0, d_n, d_off,
+                        true, ctx->cfg.capacity, a)))
+      return rc;
+  }
+  if ((rc = launch_layernorm(ctx, a.x, D, d_last, B, m.lnf_w, m.lnf_b, d_hidden, D))) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(last_hidden, d_hidden, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, float* hidden) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!rows17 || !pos || !hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if ((rc = need_model(ctx))) return rc;
+  if ((rc = check_ids(ctx, rows17, B))) return rc;
+  int64_t max_pos = 0;
+  for (int b = 0; b < B; b++) {
+    if (pos[b] < 0) return fail(ctx, MB_ERR_ARG, "sequence %d: negative position %d", b, pos[b]);
+    if (!ctx->cfg.wrap && pos[b] >= ctx->cfg.capacity)
+      return fail(ctx, MB_ERR_RANGE,
+                  "decode position %d exceeds the KV ring (%d slots); it must be sized "
+                  "prefill_rows + max_new_frames",
+                  pos[b], ctx->cfg.capacity);
+    if (pos[b] > max_pos) max_pos = pos[b];
+  }
+  int32_t* d_rows = (int32_t*)scratch(ctx, "step_rows", (size_t)B * ROW * 4);
+  int32_t* d_pos = (int32_t*)scratch(ctx, "step_pos", (size_t)B * 4);
+  float* d_hidden = (float*)scratch(ctx, "hidden", (size_t)B * D * 4);
+  if (!d_rows || !d_pos || !d_hidden) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_rows, rows17, (size_t)B * ROW * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_pos, pos, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = decode_step(ctx, B, d_rows, d_pos, max_pos, d_hidden))) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(hidden, d_hidden, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!hidden || !codes || !cont) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if ((rc = need_model(ctx))) return rc;
+  float* d_hidden = (float*)scratch(ctx, "hidden", (size_t)B * D * 4);
+  int32_t* d_out = (int32_t*)scratch(ctx, "frame_out", (size_t)B * (NVQ + 1) * 4);
+  if (!d_hidden || !d_out) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_hidden, hidden, (size_t)B * D * 4, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = local_frame(ctx, B, d_hidden, d_out, d_out + (size_t)B * NVQ, nullptr))) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(codes, d_out, (size_t)B * NVQ * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(cont, d_out + (size_t)B * NVQ, (size_t)B * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos,
+                       int32_t max_pos, float* hidden) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!rows17 || !pos || !hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (max_pos < 0) return fail(ctx, MB_ERR_ARG, "max_pos %d is negative", max_pos);
+  if ((rc = need_model(ctx))) return rc;
+  return decode_step(ctx, B, rows17, pos, max_pos, hidden);
+}
+
+int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
+                       int32_t* rows17_out) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if ((rc = need_model(ctx))) return rc;
+  return local_frame(ctx, B, hidden, codes, cont, rows17_out);
+}
+
+}  // extern "C"

@@ -49,11 +49,10 @@ __device__ __forceinline__ float col_sum(float x) {
 
 // Q bf16 [B][rows_max][768] (roped), K/V bf16 ring, fp32 output.
 __global__ __launch_bounds__(256) void k_flash_bf16(
-    const uint16_t* __restrict__ q, int64_t q_row_stride, int64_t q_seq_stride,
-    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows_max,
-    const uint16_t* __restrict__ ring_k, const uint16_t* __restrict__ ring_v,
-    const int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, float* __restrict__ out,
-    int64_t out_row_stride, int64_t out_seq_stride) {
+    const uint16_t* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, const uint16_t* __restrict__ ring_k,
+    const uint16_t* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, float* __restrict__ out, Rows out_rows) {
   __shared__ uint16_t Ks[KT * KPAD];   // [slot][dim]
   __shared__ uint16_t Vt[HD * KPAD];   // [dim][slot]
   __shared__ int32_t Ps[KT];
@@ -76,8 +75,7 @@ __global__ __launch_bounds__(256) void k_flash_bf16(
   for (int kc = 0; kc < 2; kc++) {
     uint4 raw = make_uint4(0, 0, 0, 0);
     if (qvalid)
-      raw = *(const uint4*)(q + (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + h * HD +
-                            kc * 32 + grp * 8);
+      raw = *(const uint4*)(q + row_at(q_rows, b, r) + h * HD + kc * 32 + grp * 8);
     float f[8];
     unpack<true>(raw, f);
 #pragma unroll
@@ -160,7 +158,7 @@ __global__ __launch_bounds__(256) void k_flash_bf16(
   }
   if (!qvalid) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  float* op = out + (int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + h * HD;
+  float* op = out + row_at(out_rows, b, r) + h * HD;
 #pragma unroll
   for (int d = 0; d < 4; d++)
     *(float4*)(op + d * 16 + grp * 4) =
@@ -177,11 +175,10 @@ __global__ __launch_bounds__(256) void k_flash_bf16(
 // which is exactly the score element the lane already holds.
 template <bool KV_BF16>
 __global__ __launch_bounds__(256) void k_flash_f32(
-    const float* __restrict__ q, int64_t q_row_stride, int64_t q_seq_stride,
-    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows_max,
-    const void* __restrict__ ring_k, const void* __restrict__ ring_v,
-    const int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, float* __restrict__ out,
-    int64_t out_row_stride, int64_t out_seq_stride) {
+    const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, const void* __restrict__ ring_k,
+    const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, float* __restrict__ out, Rows out_rows) {
   __shared__ float Ks[KT * FPAD];  // [slot][dim]
   __shared__ float Vs[KT * FPAD];  // [slot][dim]
   __shared__ int32_t Ps[KT];
@@ -200,7 +197,7 @@ __global__ __launch_bounds__(256) void k_flash_f32(
 
   float qv[16];
   {
-    const float* qp = q + (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + h * HD + grp * 16;
+    const float* qp = q + (qvalid ? row_at(q_rows, b, r) : 0) + h * HD + grp * 16;
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
       float4 t = qvalid ? *(const float4*)(qp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -289,40 +286,32 @@ __global__ __launch_bounds__(256) void k_flash_f32(
   }
   if (!qvalid) return;
   const float inv = l > 0.f ? 1.f / l : 0.f;
-  float* op = out + (int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + h * HD;
+  float* op = out + row_at(out_rows, b, r) + h * HD;
 #pragma unroll
   for (int d = 0; d < 4; d++)
     *(float4*)(op + d * 16 + grp * 4) =
         make_float4(acc[d][0] * inv, acc[d][1] * inv, acc[d][2] * inv, acc[d][3] * inv);
 }
 
-int launch_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
-                             int q_dtype, int64_t q_row_stride, int64_t q_seq_stride,
-                             const int32_t* pos0, const int32_t* n_rows, float* out,
-                             int64_t out_row_stride, int64_t out_seq_stride) {
-  const bool kv_bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
-  if (q_dtype == MB_DT_BF16 && !kv_bf16)
+int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
+                             const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
+                             const int32_t* n_rows, float* out, const Rows& out_rows) {
+  if (q_dtype == MB_DT_BF16 && !ring.bf16)
     return fail(ctx, MB_ERR_ARG, "bf16 queries need a bf16 ring (the bf16 MFMA path)");
   if (B > 65535) return fail(ctx, MB_ERR_ARG, "at most 65535 sequences per prefill call");
-  const size_t e = kv_elem_bytes(ctx);
-  const void* rk = (const char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
-  const void* rv = (const char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
-  const int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
-  const int64_t rs = (int64_t)H * ctx->cfg.capacity * HD;
-  const int C = ctx->cfg.capacity;
+  if (B == 0 || rows_max == 0) return MB_OK;
   dim3 grid((unsigned)((rows_max + QT - 1) / QT), H, (unsigned)B);
   if (q_dtype == MB_DT_BF16)
-    hipLaunchKernelGGL(k_flash_bf16, grid, dim3(256), 0, ctx->stream, (const uint16_t*)q,
-                       q_row_stride, q_seq_stride, pos0, n_rows, rows_max, (const uint16_t*)rk,
-                       (const uint16_t*)rv, sp, rs, C, out, out_row_stride, out_seq_stride);
-  else if (kv_bf16)
-    hipLaunchKernelGGL(k_flash_f32<true>, grid, dim3(256), 0, ctx->stream, (const float*)q,
-                       q_row_stride, q_seq_stride, pos0, n_rows, rows_max, rk, rv, sp, rs, C, out,
-                       out_row_stride, out_seq_stride);
+    hipLaunchKernelGGL(k_flash_bf16, grid, dim3(256), 0, ctx->stream, (const uint16_t*)q, q_rows,
+                       pos0, n_rows, (const uint16_t*)ring.k, (const uint16_t*)ring.v, ring.sp,
+                       ring.seq_stride, ring.C, out, out_rows);
+  else if (ring.bf16)
+    hipLaunchKernelGGL(k_flash_f32<true>, grid, dim3(256), 0, ctx->stream, (const float*)q, q_rows,
+                       pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, out, out_rows);
   else
     hipLaunchKernelGGL(k_flash_f32<false>, grid, dim3(256), 0, ctx->stream, (const float*)q,
-                       q_row_stride, q_seq_stride, pos0, n_rows, rows_max, rk, rv, sp, rs, C, out,
-                       out_row_stride, out_seq_stride);
+                       q_rows, pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, out,
+                       out_rows);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

@@ -104,11 +104,11 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
 // With more than C rows in one call only the last C reach the ring.
 template <bool IN_BF16, bool KV_BF16, bool Q_BF16>
 __global__ __launch_bounds__(256) void k_ring_write(
-    const void* __restrict__ qkv, int64_t qkv_row_stride, int64_t qkv_seq_stride,
-    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows_max, int B,
-    void* __restrict__ q_out, int64_t q_row_stride, int64_t q_seq_stride,
-    void* __restrict__ ring_k, void* __restrict__ ring_v, int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, int wrap, const float2* __restrict__ rope_tab) {
+    const void* __restrict__ qkv, Rows qkv_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, int rows_max, int B, void* __restrict__ q_out,
+    Rows q_rows, void* __restrict__ ring_k, void* __restrict__ ring_v,
+    int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, int wrap,
+    const float2* __restrict__ rope_tab) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t row_id = t / 96;
   if (row_id >= (int64_t)B * rows_max) return;
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(256) void k_ring_write(
   const int slot = wrap ? (int)(p64 % C) : (int)p64;
 
   float q[8], k[8], v[8];
-  const int64_t roff = (int64_t)b * qkv_seq_stride + (int64_t)r * qkv_row_stride + head * HD + d0;
+  const int64_t roff = row_at(qkv_rows, b, r) + head * HD + d0;
   load8<IN_BF16>(qkv, roff, q);
   load8<IN_BF16>(qkv, roff + D, k);
   load8<IN_BF16>(qkv, roff + 2 * D, v);
@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256) void k_ring_write(
     rope_pair(q[2 * j], q[2 * j + 1], c, s, qo[2 * j], qo[2 * j + 1]);
     rope_pair(k[2 * j], k[2 * j + 1], c, s, ko[2 * j], ko[2 * j + 1]);
   }
-  if (q_out) store8<Q_BF16>(q_out, (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + head * HD + d0, qo);
+  if (q_out) store8<Q_BF16>(q_out, row_at(q_rows, b, r) + head * HD + d0, qo);
   // a row that a later row of the same call overwrites is never stored, so
   // every slot is written at most once per call (deterministic contents)
   if (n > C && r < n - C) return;
@@ -145,25 +145,31 @@ __global__ __launch_bounds__(256) void k_ring_write(
   if (part == 0) slot_pos[(int64_t)b * C + slot] = pos;
 }
 
-int launch_ring_write(mb_ctx* ctx, int layer, int B, int rows_max, const void* qkv, int qkv_dtype,
-                      int64_t qkv_row_stride, int64_t qkv_seq_stride, const int32_t* pos0,
-                      const int32_t* n_rows, void* q_out, int q_dtype, int64_t q_row_stride,
-                      int64_t q_seq_stride) {
+RingView global_ring(const mb_ctx* ctx, int layer) {
+  RingView v;
+  const size_t e = kv_elem_bytes(ctx);
+  v.k = (char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
+  v.v = (char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
+  v.sp = ctx->slot_pos + slot_base(ctx, layer, 0);
+  v.seq_stride = (int64_t)H * ctx->cfg.capacity * HD;
+  v.C = ctx->cfg.capacity;
+  v.wrap = ctx->cfg.wrap;
+  v.bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
+  return v;
+}
+
+int launch_ring_write(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const void* qkv,
+                      int qkv_dtype, const Rows& qkv_rows, const int32_t* pos0,
+                      const int32_t* n_rows, void* q_out, int q_dtype, const Rows& q_rows) {
   const int64_t threads = (int64_t)B * rows_max * 96;
   const int64_t blocks = (threads + 255) / 256;
   if (blocks > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many rows in one call");
-  const size_t e = kv_elem_bytes(ctx);
-  void* rk = (char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
-  void* rv = (char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
-  int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
-  const int64_t rs = (int64_t)H * ctx->cfg.capacity * HD;
-  const bool in_bf16 = qkv_dtype == MB_DT_BF16, kv_bf16 = ctx->cfg.kv_dtype == MB_KV_BF16,
-             q_bf16 = q_dtype == MB_DT_BF16;
+  if (blocks == 0) return MB_OK;
+  const bool in_bf16 = qkv_dtype == MB_DT_BF16, kv_bf16 = ring.bf16, q_bf16 = q_dtype == MB_DT_BF16;
 #define MB_RW(A, Bq, Cq)                                                                        \
   hipLaunchKernelGGL((k_ring_write<A, Bq, Cq>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, \
-                     qkv, qkv_row_stride, qkv_seq_stride, pos0, n_rows, rows_max, B, q_out,      \
-                     q_row_stride, q_seq_stride, rk, rv, sp, rs, ctx->cfg.capacity, ctx->cfg.wrap,    \
-                     ctx->rope_tab)
+                     qkv, qkv_rows, pos0, n_rows, rows_max, B, q_out, q_rows, ring.k, ring.v,     \
+                     ring.sp, ring.seq_stride, ring.C, ring.wrap, ctx->rope_tab)
   if (in_bf16) {
     if (kv_bf16) { if (q_bf16) MB_RW(true, true, true); else MB_RW(true, true, false); }
     else { if (q_bf16) MB_RW(true, false, true); else MB_RW(true, false, false); }
@@ -230,12 +236,11 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* acc, floa
 // wave writes a partial (acc[64], max, sum) for k_attn_combine.
 template <bool KV_BF16, int U>
 __global__ __launch_bounds__(256) void k_attn_split(
-    const float* __restrict__ q, int64_t q_row_stride, int64_t q_seq_stride,
-    const int32_t* __restrict__ pos0, const int32_t* __restrict__ n_rows, int rows,
-    const void* __restrict__ ring_k, const void* __restrict__ ring_v,
-    const int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, int split_len,
-    int nsplit, float* __restrict__ part, float* __restrict__ out, int64_t out_row_stride,
-    int64_t out_seq_stride) {
+    const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, int rows, const void* __restrict__ ring_k,
+    const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, int split_len, int nsplit, float* __restrict__ part,
+    float* __restrict__ out, Rows out_rows) {
   constexpr int VD = KV_BF16 ? 8 : 4;
   constexpr int LR = 64 / VD;
   constexpr int G = VD;
@@ -253,7 +258,7 @@ __global__ __launch_bounds__(256) void k_attn_split(
 
   float qv[VD];
   {
-    const float* qp = q + (int64_t)b * q_seq_stride + (int64_t)r * q_row_stride + head * HD + sub * VD;
+    const float* qp = q + row_at(q_rows, b, r) + head * HD + sub * VD;
 #pragma unroll
     for (int i = 0; i < VD; i += 4) {
       const float4 t = *(const float4*)(qp + i);
@@ -338,7 +343,7 @@ __global__ __launch_bounds__(256) void k_attn_split(
   if (g != 0) return;
   if (nsplit == 1) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    float* op = out + (int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + head * HD + sub * VD;
+    float* op = out + row_at(out_rows, b, r) + head * HD + sub * VD;
 #pragma unroll
     for (int i = 0; i < VD; i += 4)
       *(float4*)(op + i) = make_float4(acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv, acc[i + 3] * inv);
@@ -360,7 +365,7 @@ __global__ __launch_bounds__(256) void k_attn_split(
 // splits with independent loads.
 __global__ __launch_bounds__(256) void k_attn_combine(
     const float* __restrict__ part, int nsplit, const int32_t* __restrict__ n_rows, int rows,
-    int64_t units, float* __restrict__ out, int64_t out_row_stride, int64_t out_seq_stride) {
+    int64_t units, float* __restrict__ out, Rows out_rows) {
   const int lane = threadIdx.x & 63;
   const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (query, head)
   if (unit >= units) return;
@@ -379,8 +384,7 @@ __global__ __launch_bounds__(256) void k_attn_combine(
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
   float acc = 0.f;
   for (int s = 0; s < nsplit; s++) acc = fmaf(__shfl(w, s), pp[s * PART + lane], acc);
-  out[(int64_t)b * out_seq_stride + (int64_t)r * out_row_stride + head * HD + lane] =
-      L > 0.f ? acc / L : 0.f;
+  out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? acc / L : 0.f;
 }
 
 // Launch the split attention for nq = B * rows queries.  The split length is
@@ -388,14 +392,13 @@ __global__ __launch_bounds__(256) void k_attn_combine(
 // split stays a whole number of U-deep load batches and there are at most 64
 // splits; MB_ATTN_WAVES and MB_ATTN_U override the defaults (tuning sweeps).
 template <bool BF16, int U>
-static void launch_split(mb_ctx* ctx, dim3 grid, const float* q, int64_t q_row_stride,
-                         int64_t q_seq_stride, const int32_t* pos0, const int32_t* n_rows, int rows,
-                         const void* rk, const void* rv, const int32_t* sp, int64_t rs, int C,
-                         int split_len, int nsplit, float* part, float* out,
-                         int64_t out_row_stride, int64_t out_seq_stride) {
-  hipLaunchKernelGGL((k_attn_split<BF16, U>), grid, dim3(256), 0, ctx->stream, q, q_row_stride,
-                     q_seq_stride, pos0, n_rows, rows, rk, rv, sp, rs, C, split_len, nsplit, part,
-                     out, out_row_stride, out_seq_stride);
+static void launch_split(mb_ctx* ctx, dim3 grid, const float* q, const Rows& q_rows,
+                         const int32_t* pos0, const int32_t* n_rows, int rows,
+                         const RingView& ring, int split_len, int nsplit, float* part, float* out,
+                         const Rows& out_rows) {
+  hipLaunchKernelGGL((k_attn_split<BF16, U>), grid, dim3(256), 0, ctx->stream, q, q_rows, pos0,
+                     n_rows, rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, split_len,
+                     nsplit, part, out, out_rows);
 }
 
 static int env_int(const char* name, int dflt) {
@@ -403,19 +406,18 @@ static int env_int(const char* name, int dflt) {
   return v && *v ? atoi(v) : dflt;
 }
 
-static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
-                       int64_t q_row_stride, int64_t q_seq_stride, const int32_t* pos0,
-                       const int32_t* n_rows, int64_t max_valid, float* out,
-                       int64_t out_row_stride, int64_t out_seq_stride) {
+int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
+                const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
+                float* out, const Rows& out_rows) {
   static const int64_t target = env_int("MB_ATTN_WAVES", 8192);
   static const int U = env_int("MB_ATTN_U", 16);
   if (U != 4 && U != 8 && U != 16) return fail(ctx, MB_ERR_ARG, "MB_ATTN_U must be 4, 8 or 16");
-  const bool bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
-  const int gu = (bf16 ? 8 : 4) * U;
-  const int C = ctx->cfg.capacity;
+  const int gu = (ring.bf16 ? 8 : 4) * U;
+  const int C = ring.C;
   if (max_valid > C) max_valid = C;
   if (max_valid < 1) max_valid = 1;
   const int64_t nq = (int64_t)B * rows;
+  if (nq == 0) return MB_OK;
   const int64_t units = nq * H;
   const int64_t want = (target + units - 1) / units;
   int64_t split_len = (max_valid + want - 1) / want;
@@ -428,16 +430,10 @@ static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
     part = (float*)scratch(ctx, "attn_part", (size_t)units * nsplit * PART * 4);
     if (!part) return fail(ctx, MB_ERR_NOMEM, "attention partials allocation failed");
   }
-  const size_t e = kv_elem_bytes(ctx);
-  const void* rk = (const char*)ctx->ring_k + ring_base(ctx, layer, 0) * e;
-  const void* rv = (const char*)ctx->ring_v + ring_base(ctx, layer, 0) * e;
-  const int32_t* sp = ctx->slot_pos + slot_base(ctx, layer, 0);
-  const int64_t rs = (int64_t)H * C * HD;
   dim3 grid((unsigned)(nq * nsplit), H / 4);
-#define MB_SPLIT(BF, UU)                                                                       \
-  launch_split<BF, UU>(ctx, grid, q, q_row_stride, q_seq_stride, pos0, n_rows, rows, rk, rv, sp, \
-                       rs, C, (int)split_len, nsplit, part, out, out_row_stride, out_seq_stride)
-  if (bf16) {
+#define MB_SPLIT(BF, UU) \
+  launch_split<BF, UU>(ctx, grid, q, q_rows, pos0, n_rows, rows, ring, (int)split_len, nsplit, part, out, out_rows)
+  if (ring.bf16) {
     if (U == 4) MB_SPLIT(true, 4); else if (U == 8) MB_SPLIT(true, 8); else MB_SPLIT(true, 16);
   } else {
     if (U == 4) MB_SPLIT(false, 4); else if (U == 8) MB_SPLIT(false, 8); else MB_SPLIT(false, 16);
@@ -446,16 +442,10 @@ static int launch_attn(mb_ctx* ctx, int layer, int B, int rows, const float* q,
   MB_HIP(ctx, hipGetLastError());
   if (nsplit > 1) {
     hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream,
-                       part, nsplit, n_rows, rows, units, out, out_row_stride, out_seq_stride);
+                       part, nsplit, n_rows, rows, units, out, out_rows);
     MB_HIP(ctx, hipGetLastError());
   }
   return MB_OK;
-}
-
-int launch_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
-                            const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride) {
-  return launch_attn(ctx, layer, B, 1, q, q_stride, q_stride, pos, nullptr, (int64_t)max_pos + 1,
-                     out, out_stride, out_stride);
 }
 
 }  // namespace mb
