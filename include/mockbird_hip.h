@@ -189,6 +189,13 @@ int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, f
 int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
                float* last_hidden);
 
+/* mb_prefill returning ln_f of every row: hidden [B][rows_max][768], rows
+ * r >= n_rows[b] zeroed.  PrefillRunner.run reads back the whole [rows, 768]
+ * hidden block the same way (prefill.ts:325-603, compared row by row in
+ * tests/gpu/prefill.test.mjs:104-149). */
+int mb_prefill_rows(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+                    float* hidden);
+
 /* One global decode step for sequences b < B: embed rows17[b][17], run every
  * layer at position pos[b] (appending K/V to each layer's ring) and write
  * ln_f into hidden[b][768].  Replaces GpuTtsEngine.decodeStep /
@@ -202,6 +209,12 @@ int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos
  * keeps its history unchanged.  Replaces GpuTtsEngine.nextFrame /
  * DecodeRunner.nextFrame (gpu.ts:268-272, decode.ts:788-939). */
 int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont);
+
+/* Run local-head steps 0 .. max_step (< 17) without their greedy choices and
+ * return the last step's ln_f output out[b][768]; steps >= 2 embed the codes
+ * of the previous frame.  The conformance probe
+ * DecodeRunner.nextFrameSteps (decode.ts:970-1030). */
+int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float* out);
 
 /* Forget the repetition history of `n` sequences (n < 0: all) -- the
  * clearSeen part of engine.reset (decode.ts:276-280, gpu.ts:237-242). */

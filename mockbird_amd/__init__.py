@@ -28,8 +28,8 @@ EXPORTS = (
     "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_ring_append", "mb_ring_write_rows",
     "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
-    "mb_set_local_head", "mb_prefill", "mb_decode_step", "mb_local_frame", "mb_clear_seen",
-    "mb_decode_step_dev", "mb_local_frame_dev",
+    "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
+    "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
 )
 
 
@@ -97,6 +97,8 @@ def load():
                                      C.c_int),
         "mb_set_local_head": ([_vp, _i32, _i32, _f32], C.c_int),
         "mb_prefill": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_prefill_rows": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_local_steps": ([_vp, C.c_int, _vp, C.c_int, _vp], C.c_int),
         "mb_decode_step": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_local_frame": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_clear_seen": ([_vp, C.c_int, _vp], C.c_int),
@@ -268,6 +270,23 @@ class Context:
         out = np.zeros((B, D), np.float32)
         self.check(self.lib.mb_prefill(self.h, B, R, ids.ctypes.data, n_rows.ctypes.data,
                                        out.ctypes.data))
+        return out
+
+    def prefill_rows(self, ids: np.ndarray, n_rows) -> np.ndarray:
+        """ids [B][rows_max][17] -> hidden of every row [B][rows_max][768]."""
+        ids, n_rows = _i32c(ids), _i32c(n_rows)
+        B, R = ids.shape[0], ids.shape[1]
+        out = np.zeros((B, R, D), np.float32)
+        self.check(self.lib.mb_prefill_rows(self.h, B, R, ids.ctypes.data, n_rows.ctypes.data,
+                                            out.ctypes.data))
+        return out
+
+    def local_steps(self, hidden: np.ndarray, max_step: int) -> np.ndarray:
+        """ln_f output of local-head step `max_step` (no greedy choices)."""
+        hidden = _f32c(hidden)
+        out = np.zeros_like(hidden)
+        self.check(self.lib.mb_local_steps(self.h, hidden.shape[0], hidden.ctypes.data, max_step,
+                                           out.ctypes.data))
         return out
 
     def decode_step(self, rows17: np.ndarray, pos) -> np.ndarray:

@@ -160,8 +160,9 @@ int local_state(mb_ctx* ctx) {
   MB_HIP(ctx, hipMalloc(&ctx->cont, (size_t)S * 4));
   ctx->device_bytes += (int64_t)(2 * kv + S * ROW * 8 + S * NVQ * 32 * 4 + S * NVQ * 4 + S * 4);
   int rc;
-  if ((rc = launch_fill_kv(ctx, ctx->local_k, (int64_t)kv / 4, 0.f))) return rc;
-  if ((rc = launch_fill_kv(ctx, ctx->local_v, (int64_t)kv / 4, 0.f))) return rc;
+  // the local cache is fp32 whatever the global rings hold: clear it as words
+  if ((rc = launch_fill_i32(ctx, (int32_t*)ctx->local_k, (int64_t)kv / 4, 0))) return rc;
+  if ((rc = launch_fill_i32(ctx, (int32_t*)ctx->local_v, (int64_t)kv / 4, 0))) return rc;
   if ((rc = launch_fill_i32(ctx, ctx->local_sp, S * ROW, -1))) return rc;
   for (int s = 0; s < ROW; s++)
     if ((rc = launch_fill_i32(ctx, ctx->local_pos + (int64_t)s * S, S, s))) return rc;
@@ -212,17 +213,19 @@ int decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, i
   return launch_layernorm(ctx, a.x, D, nullptr, B, m.lnf_w, m.lnf_b, hidden, D);
 }
 
-// The 17-step local head on device buffers; codes/cont/rows17_out optional.
-int local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
-                int32_t* rows17_out) {
+// Local-head steps 0 .. last_step on device buffers.  With `pick` each step
+// ends in its greedy choice (the text decision at step 0, a code per channel
+// after it); without it the steps only run the layer and ln_f, embedding the
+// codes already held in ctx->tokens, and the last step's ln_f output is left in
+// a.norm (DecodeRunner.nextFrameSteps, decode.ts:970-1030).
+int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pick, Act& a) {
   int rc;
   if ((rc = local_state(ctx))) return rc;
-  Act a;
   if ((rc = activations(ctx, B, a))) return rc;
   const ModelW& m = ctx->model;
   const RingView ring = local_ring(ctx);
   const int64_t S = ctx->cfg.max_seqs;
-  for (int step = 0; step < ROW; step++) {
+  for (int step = 0; step <= last_step; step++) {
     if ((rc = cancelled(ctx))) return rc;
     if (step == 0)
       MB_HIP(ctx, hipMemcpyAsync(a.x, hidden, (size_t)B * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
@@ -234,6 +237,7 @@ int local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t
       return rc;
     if ((rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
       return rc;
+    if (!pick) continue;
     if (step == 0) {
       rc = launch_text_decide(ctx, a.norm, B, m.text_head, ctx->cfg.vocab, ctx->end_id,
                               ctx->assistant_id, ctx->cont);
@@ -247,6 +251,15 @@ int local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t
     }
     if (rc) return rc;
   }
+  return MB_OK;
+}
+
+// The 17-step local head on device buffers; codes/cont/rows17_out optional.
+int local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
+                int32_t* rows17_out) {
+  Act a;
+  int rc = local_steps(ctx, B, hidden, ROW - 1, true, a);
+  if (rc) return rc;
   if (codes)
     MB_HIP(ctx, hipMemcpyAsync(codes, ctx->tokens, (size_t)B * NVQ * 4, hipMemcpyDeviceToDevice,
                                ctx->stream));
@@ -302,12 +315,20 @@ int mb_clear_seen(mb_ctx* ctx, int n, const int32_t* seq_ids) {
   return MB_OK;
 }
 
-int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
-               float* last_hidden) {
+}  // extern "C"
+
+namespace mb {
+namespace {
+
+// Global prefill; ln_f of each sequence's last row goes to last_hidden
+// [B][768] and, when all_hidden is set, ln_f of every row to
+// all_hidden[B][rows_max][768] (rows past n_rows[b] are zeroed).
+int prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+            float* last_hidden, float* all_hidden) {
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
-  if (!ids || !n_rows || !last_hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (!ids || !n_rows || (!last_hidden && !all_hidden)) return fail(ctx, MB_ERR_ARG, "null pointer");
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
     return fail(ctx, MB_ERR_ARG, "rows_max %d out of [1, %d]", rows_max, ctx->cfg.max_rows);
   if ((rc = need_model(ctx))) return rc;
@@ -355,10 +376,43 @@ int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32
                         true, ctx->cfg.capacity, a)))
       return rc;
   }
-  if ((rc = launch_layernorm(ctx, a.x, D, d_last, B, m.lnf_w, m.lnf_b, d_hidden, D))) return rc;
-  MB_HIP(ctx, hipMemcpyAsync(last_hidden, d_hidden, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  if (last_hidden) {
+    if ((rc = launch_layernorm(ctx, a.x, D, d_last, B, m.lnf_w, m.lnf_b, d_hidden, D))) return rc;
+    MB_HIP(ctx, hipMemcpyAsync(last_hidden, d_hidden, (size_t)B * D * 4, hipMemcpyDeviceToHost,
+                               ctx->stream));
+  }
+  std::vector<float> rows;
+  if (all_hidden) {
+    if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, m.lnf_w, m.lnf_b, a.norm, D))) return rc;
+    rows.resize((size_t)M * D);
+    MB_HIP(ctx, hipMemcpyAsync(rows.data(), a.norm, rows.size() * 4, hipMemcpyDeviceToHost,
+                               ctx->stream));
+  }
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (all_hidden) {
+    memset(all_hidden, 0, (size_t)B * rows_max * D * 4);
+    for (int b = 0; b < B; b++)
+      memcpy(all_hidden + (size_t)b * rows_max * D, rows.data() + (size_t)off[b] * D,
+             (size_t)n_rows[b] * D * 4);
+  }
   return MB_OK;
+}
+
+}  // namespace
+}  // namespace mb
+
+extern "C" {
+
+int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+               float* last_hidden) {
+  if (ctx && !last_hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  return prefill(ctx, B, rows_max, ids, n_rows, last_hidden, nullptr);
+}
+
+int mb_prefill_rows(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
+                    float* hidden) {
+  if (ctx && !hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
+  return prefill(ctx, B, rows_max, ids, n_rows, nullptr, hidden);
 }
 
 int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, float* hidden) {
@@ -403,6 +457,24 @@ int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int3
   if ((rc = local_frame(ctx, B, d_hidden, d_out, d_out + (size_t)B * NVQ, nullptr))) return rc;
   MB_HIP(ctx, hipMemcpyAsync(codes, d_out, (size_t)B * NVQ * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(cont, d_out + (size_t)B * NVQ, (size_t)B * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float* out) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!hidden || !out) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (max_step < 0 || max_step >= ROW)
+    return fail(ctx, MB_ERR_ARG, "max_step %d out of [0, %d)", max_step, ROW);
+  if ((rc = need_model(ctx))) return rc;
+  float* d_hidden = (float*)scratch(ctx, "hidden", (size_t)B * D * 4);
+  if (!d_hidden) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_hidden, hidden, (size_t)B * D * 4, hipMemcpyHostToDevice, ctx->stream));
+  Act a;
+  if ((rc = local_steps(ctx, B, d_hidden, max_step, false, a))) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(out, a.norm, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;
 }

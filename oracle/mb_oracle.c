@@ -496,6 +496,30 @@ int or_local_frame(const or_model* M, const float* hidden, uint32_t* seen, int32
   return cont;
 }
 
+/* Local-head steps 0 .. max_step with no greedy choice, the conformance probe
+ * DecodeRunner.nextFrameSteps (decode.ts:970-1030): step 0 takes `hidden`,
+ * step 1 the assistant-slot text embedding, step s >= 2 the embedding of
+ * codes[s - 2] on channel s - 2.  out[768] = local ln_f of step max_step. */
+void or_local_steps(const or_model* M, const float* hidden, int max_step, const int32_t* codes,
+                    float* out) {
+  float* K = (float*)calloc((size_t)OR_ROW * OR_D, sizeof(float));
+  float* V = (float*)calloc((size_t)OR_ROW * OR_D, sizeof(float));
+  int32_t sp[OR_ROW];
+  for (int i = 0; i < OR_ROW; i++) sp[i] = -1;
+  float x[OR_D];
+  for (int step = 0; step <= max_step; step++) {
+    if (step == 0)
+      memcpy(x, hidden, sizeof x);
+    else if (step == 1)
+      memcpy(x, M->wte + (int64_t)M->assistant_id * OR_D, sizeof x);
+    else
+      memcpy(x, M->audio_emb[step - 2] + (int64_t)codes[step - 2] * OR_D, sizeof x);
+    local_step(M, x, step, K, V, sp, out);
+  }
+  free(K);
+  free(V);
+}
+
 /* Prompt rows of buildVoiceCloneRows with empty templates (policy.ts:49-80):
  * [audio_start] + one audio row per code frame + [audio_end] + text rows +
  * [audio_start].  Returns the row count (n_frames + n_text + 3). */

@@ -66,6 +66,7 @@ def lib():
         L.or_model_decode_step.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i32p, C.c_int,
                                            _f32p, _f32p, _i32p, _f32p]
         L.or_local_frame.argtypes = [C.c_void_p, _f32p, _u32p, _i32p, C.c_void_p]
+        L.or_local_steps.argtypes = [C.c_void_p, _f32p, C.c_int, _i32p, _f32p]
         L.or_model_prefill_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                              _i32p, _i32p, _f32p, _f32p, _i32p, _f32p]
         L.or_model_decode_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
@@ -268,6 +269,13 @@ class Model:
         x = np.zeros(D, np.float32)
         lib().or_embed_row(self.ptr, _c(row17, np.int32), x)
         return x
+
+    def local_steps(self, hidden, max_step: int, codes) -> np.ndarray:
+        """ln_f output of local-head step `max_step` with the codes fed in."""
+        out = np.zeros(D, np.float32)
+        lib().or_local_steps(self.ptr, _c(hidden, np.float32), int(max_step), _c(codes, np.int32),
+                             out)
+        return out
 
     def text_decide(self, h):
         e, a = C.c_double(), C.c_double()

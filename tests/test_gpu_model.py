@@ -201,3 +201,35 @@ def test_c3_many_voices_subset():
                 hs[b] = sts[b].decode_step(rows[b][None], [pos[b]])
                 assert np.abs(h[b] - hs[b][0]).max() < TOL[mb.MB_KV_BF16], (f, b)
             pos = pos + 1
+
+
+def test_prefill_rows_and_local_steps():
+    """PrefillRunner.run's whole hidden block (prefill.ts:325-603) and the
+    nextFrameSteps probe (decode.ts:970-1030) against the oracle: every row of
+    a ragged 3-voice prefill, then local steps 0, 1, 2, 9 and 16 fed with the
+    codes of the frame just chosen."""
+    say("prefill_rows + local_steps, 2 layers, 3 voices")
+    L, V, B, C = 2, 64, 3, 96
+    w = _c0_weights(n_layers=L, vocab=V, seed=11)
+    m = oracle.Model(w, n_layers=L, vocab=V)
+    prompts = [synth.prompt(40 + b, n_frames=4 + 5 * b, n_text=3 + 2 * b, vocab=V) for b in range(B)]
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    with _ctx(w, L, V, B, C) as ctx:
+        hid = ctx.prefill_rows(ids, n)
+        for b in range(B):
+            ref = oracle.ModelState(m, 1, C).prefill_all(0, prompts[b])
+            assert np.abs(hid[b, :n[b]] - ref).max() < 1e-4, b
+            assert not hid[b, n[b]:].any()
+        h = np.stack([hid[b, n[b] - 1] for b in range(B)])
+        codes, cont = ctx.local_frame(h)
+        assert cont.all()
+        for s in (0, 1, 2, 9, 16):
+            out = ctx.local_steps(h, s)
+            for b in range(B):
+                ref = m.local_steps(h[b], s, codes[b])
+                assert np.abs(out[b] - ref).max() < 1e-4, (s, b)
+        with pytest.raises(mb.MbError):
+            ctx.local_steps(h, 17)

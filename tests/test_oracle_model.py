@@ -103,3 +103,34 @@ def test_local_frame_updates_history_only_when_continuing(tiny):
             assert (margins[b, 1:] >= 0).all()
         else:
             assert bits.sum() == 0
+
+
+def test_local_steps_rederive_the_frame(tiny):
+    """nextFrameSteps (decode.ts:970-1030) run to step s, then the step's own
+    head, reproduces what the greedy frame chose at that step: the text
+    decision from step 0 and code s-1 (with its margin) from step s >= 1.  A
+    wrong embedding at any step (assistant slot, channel or code index)
+    changes later codes."""
+    m, w = tiny
+    g = np.random.default_rng(6)
+    col = w["model.text_lm_head.weight"]
+    heads = [w[f"model.audio_lm_heads.{k}.weight"] for k in range(16)]
+    n_cont = 0
+    for trial in range(4):
+        hidden = g.standard_normal(768).astype(np.float32)
+        st = oracle.ModelState(m, 1, 64)
+        codes, cont, margins = st.local_frame(hidden[None])
+        h0 = m.local_steps(hidden, 0, codes[0])
+        c, e, a = m.text_decide(h0)
+        assert c == cont[0] and np.isclose(a - e, margins[0, 0], rtol=1e-12)
+        if not cont[0]:
+            continue
+        n_cont += 1
+        seen = [[] for _ in range(16)]
+        for s in range(1, 17):
+            h = m.local_steps(hidden, s, codes[0])
+            logits = oracle.gemm(h[None], heads[s - 1])[0]
+            tok, bv, sv = oracle.argmax_penalty(logits, seen[s - 1])
+            assert tok == codes[0, s - 1], (trial, s)
+            assert np.isclose(bv - sv, margins[0, s], rtol=1e-9, atol=1e-12)
+    assert n_cont >= 1
