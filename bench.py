@@ -131,6 +131,123 @@ def run_c1(args, kv_name):
     return res
 
 
+def run_c2(args):
+    """Causal prefill attention, B=16, S=512, 12 heads x 64, bf16 q/k/v with
+    fp32 accumulation (bf16 MFMA), RoPE at pos = row, ring C=1024 from slot 0.
+    Returns the attention launch's mean time and TFLOP/s (algorithmic FLOPs
+    B*H*4*64*S(S+1)/2, causal half only)."""
+    import torch
+
+    import mockbird_amd as mb
+
+    B, S, C, reps = 16, 512, 1024, 50
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=S, kv_dtype=mb.MB_KV_BF16)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    tg = torch.Generator(device=dev)
+    tg.manual_seed(2)
+    qkv = torch.randn((B, S, QKV), generator=tg, device=dev).to(torch.bfloat16)
+    p0 = torch.zeros(B, dtype=torch.int32, device=dev)
+    n = torch.full((B,), S, dtype=torch.int32, device=dev)
+    q = torch.empty((B, S, D), dtype=torch.bfloat16, device=dev)
+    out = torch.empty((B, S, D), device=dev)
+    ctx.ring_write_rows_dev(0, B, S, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), q.data_ptr(),
+                            qkv_dtype=mb.MB_DT_BF16, q_dtype=mb.MB_DT_BF16)
+    for _ in range(5):
+        ctx.prefill_attention_dev(0, B, S, q.data_ptr(), p0.data_ptr(), n.data_ptr(), out.data_ptr(),
+                                  q_dtype=mb.MB_DT_BF16)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        ctx.prefill_attention_dev(0, B, S, q.data_ptr(), p0.data_ptr(), n.data_ptr(), out.data_ptr(),
+                                  q_dtype=mb.MB_DT_BF16)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs]) * 1e3)
+    flops = B * H * 4 * HD * S * (S + 1) / 2
+    ctx.close()
+    return {"workload": "causal prefill attention B=16 S=512 12x64 bf16 (fp32 acc)",
+            "avg_us": round(us, 2), "gflop": round(flops / 1e9, 3),
+            "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+            "frac_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
+
+
+def frame_prompts(B, seed=33):
+    """Voice-clone prompts with total lengths U[64, 400) (half code frames,
+    the rest text ids), as the many-voice decode configuration draws them."""
+    from mockbird_amd import synth
+
+    g = np.random.default_rng(seed)
+    lens = g.integers(64, 400, size=B)
+    return [synth.prompt(1000 + b, n_frames=int(l) // 2, n_text=int(l) - 3 - int(l) // 2,
+                         vocab=32000) for b, l in enumerate(lens)]
+
+
+def run_frames(weights, B, frames, kv_name, warmup=3):
+    """Greedy decode frames/s: prefill the prompts (untimed), then time
+    `frames` frames, each the 17-step local head (text decision + 16 codes with
+    the repetition penalty) followed by the 12-layer global decode step of the
+    frame row it produced.  Everything stays on the device; positions advance
+    one per frame."""
+    import torch
+
+    import mockbird_amd as mb
+    from mockbird_amd import synth
+
+    C = 1024
+    kv = mb.MB_KV_BF16 if kv_name == "bf16" else mb.MB_KV_F32
+    if B == 1:
+        prompts = [synth.prompt(0, n_frames=150, n_text=128, vocab=32000)]
+    else:
+        prompts = frame_prompts(B)
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=12, capacity=C, max_seqs=B, max_rows=int(n.max()), kv_dtype=kv)
+    ctx.upload_all(weights)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    t_pf = time.perf_counter()
+    h0 = ctx.prefill(ids, n)
+    t_pf = time.perf_counter() - t_pf
+    total = warmup + frames
+    pos_all = torch.from_numpy((n[None, :] + np.arange(total)[:, None]).astype(np.int32)).to(dev)
+    max_pos = int(n.max()) + total
+    if max_pos >= C:
+        raise ValueError("prompt + frames exceed the ring")
+    h = torch.from_numpy(h0).to(dev)
+    codes = torch.empty((B, 16), dtype=torch.int32, device=dev)
+    cont = torch.empty(B, dtype=torch.int32, device=dev)
+    rows = torch.empty((B, 17), dtype=torch.int32, device=dev)
+
+    def frame(f):
+        ctx.local_frame_dev(B, h.data_ptr(), codes.data_ptr(), cont.data_ptr(), rows.data_ptr())
+        ctx.decode_step_dev(B, rows.data_ptr(), pos_all[f].data_ptr(), max_pos, h.data_ptr())
+
+    for f in range(warmup):
+        frame(f)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for f in range(warmup, total):
+        frame(f)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1)
+    ok = bool(cont.all().item()) and bool(torch.isfinite(h).all().item())
+    ctx.close()
+    return {"B": B, "kv": kv_name, "frames": frames, "ms_per_frame": round(ms / frames, 4),
+            "frames_per_sec": round(B * frames / (ms * 1e-3), 1),
+            "prompt_rows": [int(n.min()), int(n.max())], "prefill_s": round(t_pf, 3),
+            "all_continued": ok}
+
+
 def cpu_baseline_c1(seconds=12.0):
     """The oracle (double-precision C, OpenMP over sequences) on a sample of the
     c1 workload: 8 of the 64 sequences, fp32 rings, append + attention steps,
@@ -173,12 +290,37 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-frames", action="store_true")
+    ap.add_argument("--legs", default="c1,c2,frames",
+                    help="comma list of c1 (append + decode attention), c2 (prefill attention), "
+                         "frames (model decode frames/s); the JSON line needs c1")
+    ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sequences are "
               "independent, so N GPUs would each run this same workload on their own share.",
               file=sys.stderr)
         return 2
+    legs = set(args.legs.split(","))
+    if args.no_prefill:
+        legs.discard("c2")
+    if args.no_frames:
+        legs.discard("frames")
+    c2 = run_c2(args) if "c2" in legs else None
+    frames = None
+    if "frames" in legs:
+        from mockbird_amd import synth
+
+        # random-init model with the benchmark's shapes; the assistant column of
+        # the text head equals the audio_end column, so no voice ever stops
+        w = synth.model_weights(n_layers=12, vocab=32000, seed=0)
+        w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]
+        plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
+        frames = [run_frames(w, b, *plan[b]) for b in map(int, args.frames_b.split(","))]
+    if "c1" not in legs:
+        print(json.dumps({"prefill_attention": c2, "frames_detail": frames}), flush=True)
+        return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
     cpu = None if args.no_cpu_baseline else cpu_baseline_c1(args.cpu_seconds)
@@ -218,6 +360,9 @@ def main():
             "ms_per_step": round(f32["ms_per_step"], 5),
             "attn_gbs": round(f32["attn_gbs"], 1), "attn_us": round(f32["attn_us"], 2),
             "frac": round(f32["attn_gbs"] / HBM_PEAK_GBS, 4)},
+        "prefill_attention": c2,
+        "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
+        "frames_detail": frames,
     }
     print(json.dumps(line), flush=True)
     return 0

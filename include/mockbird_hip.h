@@ -55,6 +55,8 @@ enum {
 
 enum { MB_KV_F32 = 0, MB_KV_BF16 = 1 };
 enum { MB_DT_F32 = 0, MB_DT_BF16 = 1 };
+/* Epilogues of mb_linear_dev. */
+enum { MB_EPI_STORE = 0, MB_EPI_GELU = 1, MB_EPI_ADD = 2 };
 
 typedef struct mb_config {
   int32_t n_layers;   /* global transformer layers (12) */
@@ -170,6 +172,19 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
                              int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out);
 
+/* Kernel-level projection on device pointers (row a7):
+ *   C[M][N] = epi(A[M][K] * W[K][N] + bias[N])
+ * W row-major [K, N] as the exported graph stores its MatMul initialisers;
+ * bias may be NULL; epi MB_EPI_STORE writes, MB_EPI_GELU applies gelu-tanh,
+ * MB_EPI_ADD adds into C (the residual).  fp32 products and accumulation.
+ * Needs N % 64 == 0, K % 128 == 0, lda and ldc multiples of 4 and 16-byte
+ * aligned pointers.  Replaces GEMM_NT (kernels-batch.ts:156-184, called
+ * prefill.ts:404-422, :464-482) and GEMV (kernels-decode.ts:127-142, called
+ * decode.ts:517-526, :553-562) with the GELU_TANH / ADD_RESIDUAL passes
+ * that follow them (kernels-decode.ts:330-340, :373-385) fused in. */
+int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda, const float* W,
+                  const float* bias, float* C, int64_t ldc, int epi);
+
 /* ------------------------------------------------------------------ model
  * The decoder around the rings, fp32 weights uploaded with mb_upload_tensor.
  * Row ids are int32 [17]: text id in column 0 (< vocab), audio codes in
@@ -192,9 +207,12 @@ int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32
 /* mb_prefill returning ln_f of every row: hidden [B][rows_max][768], rows
  * r >= n_rows[b] zeroed.  PrefillRunner.run reads back the whole [rows, 768]
  * hidden block the same way (prefill.ts:325-603, compared row by row in
- * tests/gpu/prefill.test.mjs:104-149). */
+ * tests/gpu/prefill.test.mjs:104-149).  layer_count (<= 0: every layer) runs
+ * only the first layers before ln_f, as run()'s layerCount argument does for
+ * single-layer conformance (prefill.ts:320-331); the other layers' rings are
+ * left empty. */
 int mb_prefill_rows(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
-                    float* hidden);
+                    int layer_count, float* hidden);
 
 /* One global decode step for sequences b < B: embed rows17[b][17], run every
  * layer at position pos[b] (appending K/V to each layer's ring) and write

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(PKG, "libmockbird_hip.so")
 MB_OK, MB_ERR_ARG, MB_ERR_RANGE, MB_ERR_HIP, MB_ERR_STATE, MB_ERR_CANCELLED, MB_ERR_NOMEM = range(7)
 MB_KV_F32, MB_KV_BF16 = 0, 1
 MB_DT_F32, MB_DT_BF16 = 0, 1
+MB_EPI_STORE, MB_EPI_GELU, MB_EPI_ADD = 0, 1, 2
 D, H, HD, QKV, FFN, NVQ, ROW, PAD, CODES = 768, 12, 64, 2304, 3072, 16, 17, 1024, 1024
 
 #: every symbol include/mockbird_hip.h declares (checked by the CPU tests)
@@ -30,6 +31,7 @@ EXPORTS = (
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
+    "mb_linear_dev",
 )
 
 
@@ -97,13 +99,15 @@ def load():
                                      C.c_int),
         "mb_set_local_head": ([_vp, _i32, _i32, _f32], C.c_int),
         "mb_prefill": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
-        "mb_prefill_rows": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_prefill_rows": ([_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp], C.c_int),
         "mb_local_steps": ([_vp, C.c_int, _vp, C.c_int, _vp], C.c_int),
         "mb_decode_step": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_local_frame": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_clear_seen": ([_vp, C.c_int, _vp], C.c_int),
         "mb_decode_step_dev": ([_vp, C.c_int, _vp, _vp, _i32, _vp], C.c_int),
         "mb_local_frame_dev": ([_vp, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+        "mb_linear_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int64, _vp, _vp, _vp,
+                           C.c_int64, C.c_int], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -259,6 +263,10 @@ class Context:
         self.check(self.lib.mb_prefill_attention_dev(self.h, layer, B, rows_max, q_ptr, q_dtype,
                                                      pos0_ptr, n_ptr, out_ptr))
 
+    def linear_dev(self, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc, epi=0):
+        self.check(self.lib.mb_linear_dev(self.h, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc,
+                                          epi))
+
     # -- model
     def set_local_head(self, audio_end_id: int = 7, assistant_id: int = 9, penalty: float = 1.2):
         self.check(self.lib.mb_set_local_head(self.h, audio_end_id, assistant_id, penalty))
@@ -272,13 +280,14 @@ class Context:
                                        out.ctypes.data))
         return out
 
-    def prefill_rows(self, ids: np.ndarray, n_rows) -> np.ndarray:
-        """ids [B][rows_max][17] -> hidden of every row [B][rows_max][768]."""
+    def prefill_rows(self, ids: np.ndarray, n_rows, layer_count: int = 0) -> np.ndarray:
+        """ids [B][rows_max][17] -> hidden of every row [B][rows_max][768]
+        after the first `layer_count` layers (0: all) and ln_f."""
         ids, n_rows = _i32c(ids), _i32c(n_rows)
         B, R = ids.shape[0], ids.shape[1]
         out = np.zeros((B, R, D), np.float32)
         self.check(self.lib.mb_prefill_rows(self.h, B, R, ids.ctypes.data, n_rows.ctypes.data,
-                                            out.ctypes.data))
+                                            int(layer_count), out.ctypes.data))
         return out
 
     def local_steps(self, hidden: np.ndarray, max_step: int) -> np.ndarray:

@@ -145,13 +145,249 @@ static void gemm_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const
                        K, bias, Cm, ldc, M);
 }
 
-// Pick the largest tile that still gives the chip (256 CUs) a block per CU,
-// else the smallest tile.
+// ---------------------------------------------------------------------------
+// Streaming GEMM for decode-sized M (M < kStreamMaxM): W is read straight
+// from HBM in the MFMA B-operand layout, one 16-byte load per lane, with no
+// LDS staging.  In 16x16x4 step t of a 16-deep k group, lane (l16 = lane & 15,
+// r = lane >> 4) feeds A[m0 + l16][k + 4r + t] and W[k + 4r + t][n + 4*l16 + j]
+// to column block j (j = 0..3), so block j's MFMA column c is the real column
+// n + 4c + j.  The products over t and r cover k .. k+15 exactly once, and a
+// lane's four column blocks end up holding four adjacent real columns, which
+// the epilogue writes as one float4.
+//
+// A workgroup owns MT rows x 64 columns and a k range; its four waves take
+// four consecutive quarters of that range and add their sums through LDS in
+// wave order.  Across workgroups the k range is split S ways (gridDim.z):
+// each split writes its sum to part[split][M][N] and k_gemm_reduce adds the
+// splits in split order, so every output is the same fixed-order sum on every
+// run.
+constexpr int kStreamMaxM = 1024;
+constexpr int kStreamChunk = 32;  // k rows per wave per pipeline stage
+constexpr int kStreamMaxSplit = 32;
+
+template <int EPI>
+__device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ bias, int n,
+                                            const float* cp) {
+  if (bias) {
+    const float4 b = *(const float4*)(bias + n);
+    v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+  }
+  if (EPI == EPI_GELU) {
+    v.x = gelu_tanh(v.x); v.y = gelu_tanh(v.y); v.z = gelu_tanh(v.z); v.w = gelu_tanh(v.w);
+  }
+  if (EPI == EPI_ADD) {
+    const float4 c = *(const float4*)cp;
+    v.x = c.x + v.x; v.y = c.y + v.y; v.z = c.z + v.z; v.w = c.w + v.w;
+  }
+  return v;
+}
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_stream(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int N, int kw,
+    const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
+    float* __restrict__ part) {
+  constexpr int MI = MT / 16;
+  __shared__ f32x4_t red[3][MI][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, r = lane >> 4;
+  const int n = blockIdx.x * 64 + 4 * l16;
+  const int m0 = blockIdx.y * MT;
+  const int S = gridDim.z, split = blockIdx.z;
+
+  f32x4_t acc[MI][4];
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  {
+    // Rows past M read row M - 1 (in bounds, no branch); their sums are
+    // never stored.
+    const float* Ap[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) Ap[i] = A + (int64_t)min(m0 + 16 * i + l16, M - 1) * lda + 4 * r;
+    const float* Wp = W + (int64_t)4 * r * N + n;
+    float4 a[2][2][MI], w[2][2][4];  // [stage][16-deep half][...]
+    auto load = [&](int st, int k) {
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) w[st][h][t] = *(const float4*)(Wp + (int64_t)(k + 16 * h + t) * N);
+#pragma unroll
+        for (int i = 0; i < MI; i++) a[st][h][i] = *(const float4*)(Ap[i] + k + 16 * h);
+      }
+    };
+    auto mma = [&](int st) {
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const float4 wt = w[st][h][t];
+#pragma unroll
+          for (int i = 0; i < MI; i++) {
+            const float av = t == 0 ? a[st][h][i].x : t == 1 ? a[st][h][i].y : t == 2 ? a[st][h][i].z : a[st][h][i].w;
+            acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.x, acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.y, acc[i][1], 0, 0, 0);
+            acc[i][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.z, acc[i][2], 0, 0, 0);
+            acc[i][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.w, acc[i][3], 0, 0, 0);
+          }
+        }
+    };
+    // Two register stages, chunk c in stage c & 1.  The loop body has no
+    // branch, so each stage's MFMAs wait only for that stage's loads: the
+    // stage-0 prefetch is always issued, re-reading the last chunk (in
+    // bounds, unused) when there is no next one.
+    const int k0 = (split * 4 + wave) * kw, k1 = k0 + kw, nc = kw / kStreamChunk;
+    load(0, k0);
+    int c = 0;
+    for (; c + 2 <= nc; c += 2) {
+      const int k = k0 + c * kStreamChunk;
+      load(1, k + kStreamChunk);
+      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+      mma(0);
+      load(0, min(k + 2 * kStreamChunk, k1 - kStreamChunk));
+      __builtin_amdgcn_sched_barrier(0);
+      mma(1);
+    }
+    if (c < nc) mma(0);
+  }
+
+  // the four waves' sums, added in wave order
+  if (wave > 0) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) red[wave - 1][i][j][lane] = acc[i][j];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int q = 0; q < 3; q++)
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[i][j] += red[q][i][j][lane];
+
+  // lane holds C[m0 + 16i + 4r + v][n + j] in acc[i][j][v]
+  if (S > 1) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int row = m0 + 16 * i + 4 * r + v;
+        if (row < M)
+          *(float4*)(part + ((int64_t)split * M + row) * N + n) =
+              make_float4(acc[i][0][v], acc[i][1][v], acc[i][2][v], acc[i][3][v]);
+      }
+    return;
+  }
+  const float4 bv = bias ? *(const float4*)(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int row = m0 + 16 * i + 4 * r + v;
+      if (row >= M) continue;
+      float4 val = make_float4(acc[i][0][v] + bv.x, acc[i][1][v] + bv.y, acc[i][2][v] + bv.z,
+                               acc[i][3][v] + bv.w);
+      float* cp = Cm + (int64_t)row * ldc + n;
+      *(float4*)cp = epilogue4<EPI>(val, nullptr, n, cp);
+    }
+}
+
+// C = epi(sum over splits of part, in split order, + bias); one float4 per thread.
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int S, int M,
+                                                     int N, const float* __restrict__ bias,
+                                                     float* __restrict__ Cm, int64_t ldc) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int q = N / 4;
+  if (u >= (int64_t)M * q) return;
+  const int row = (int)(u / q), col = (int)(u % q) * 4;
+  const float* p = part + (int64_t)row * N + col;
+  const int64_t stride = (int64_t)M * N;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  int s = 0;
+  for (; s + 4 <= S; s += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) v[t] = *(const float4*)(p + (s + t) * stride);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      sum.x += v[t].x; sum.y += v[t].y; sum.z += v[t].z; sum.w += v[t].w;
+    }
+  }
+  for (; s < S; s++) {
+    const float4 v = *(const float4*)(p + s * stride);
+    sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+  }
+  float* cp = Cm + (int64_t)row * ldc + col;
+  *(float4*)cp = epilogue4<EPI>(sum, bias, col, cp);
+}
+
+template <int MT>
+static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
+                         int K, const float* bias, float* Cm, int64_t ldc, int M) {
+  const int tx = N / 64, ty = (M + MT - 1) / MT, tiles = tx * ty;
+  // Smallest split S (4 waves x S workgroups share K in whole 32-row chunks,
+  // S at most kStreamMaxSplit) that gives every CU a workgroup; else the
+  // largest allowed.
+  const int quarters = K / (4 * kStreamChunk);
+  int S = 1;
+  for (int s = 1; s <= kStreamMaxSplit && s <= quarters; s++) {
+    if (quarters % s) continue;
+    S = s;
+    if ((int64_t)tiles * s >= 256) break;
+  }
+  float* part = nullptr;
+  if (S > 1) {
+    part = (float*)scratch(ctx, "gemm_part", (size_t)S * M * N * 4);
+    if (!part) return fail(ctx, MB_ERR_NOMEM, "gemm split-K partials (%d x %d x %d)", S, M, N);
+  }
+  dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
+  const int kw = K / (4 * S);
+  if (epi == EPI_GELU)
+    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_GELU>), grid, dim3(256), 0, ctx->stream, A, lda, W, N,
+                       kw, bias, Cm, ldc, M, part);
+  else if (epi == EPI_ADD)
+    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_ADD>), grid, dim3(256), 0, ctx->stream, A, lda, W, N,
+                       kw, bias, Cm, ldc, M, part);
+  else
+    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_STORE>), grid, dim3(256), 0, ctx->stream, A, lda, W,
+                       N, kw, bias, Cm, ldc, M, part);
+  if (S > 1) {
+    const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
+    if (epi == EPI_GELU)
+      hipLaunchKernelGGL(k_gemm_reduce<EPI_GELU>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M,
+                         N, bias, Cm, ldc);
+    else if (epi == EPI_ADD)
+      hipLaunchKernelGGL(k_gemm_reduce<EPI_ADD>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M, N,
+                         bias, Cm, ldc);
+    else
+      hipLaunchKernelGGL(k_gemm_reduce<EPI_STORE>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M,
+                         N, bias, Cm, ldc);
+  }
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// M < kStreamMaxM: the streaming kernel, 16 rows per workgroup up to M = 16
+// and 32 above.  32 rows keep a wave at 3 per SIMD, and at M = 256 already
+// give most projections >= 256 workgroups without a split (a split's
+// partials cost a write and a read of M x N per extra split).
+// Larger M: the LDS-tiled kernel with the largest tile that still gives the
+// chip (256 CUs) a block per CU, else the smallest tile.
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M) {
   if (M <= 0) return MB_OK;
-  if (N % 32 || K % GBK || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) || ((uintptr_t)W & 15))
+  if (N % 64 || K % (4 * kStreamChunk) || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
+      ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  if (M < kStreamMaxM) {
+    if (M <= 16) return stream_launch<16>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
+    return stream_launch<32>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
+  }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };
   if (N % 128 == 0 && blocks(128, 128) >= 256)
     gemm_launch<4, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);

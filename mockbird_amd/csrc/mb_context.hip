@@ -388,6 +388,18 @@ int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const 
                                   dense_rows(D, rows_max));
 }
 
+int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda, const float* W,
+                  const float* bias, float* C, int64_t ldc, int epi) {
+  if (!ctx) return MB_ERR_ARG;
+  if (M < 0 || N < 1 || K < 1) return fail(ctx, MB_ERR_ARG, "linear shape M %d N %d K %d", M, N, K);
+  if (epi != EPI_STORE && epi != EPI_GELU && epi != EPI_ADD)
+    return fail(ctx, MB_ERR_ARG, "unknown epilogue %d", epi);
+  if (M == 0) return MB_OK;
+  if (!A || !W || !C) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (lda < K || ldc < N) return fail(ctx, MB_ERR_ARG, "leading dimension below the row width");
+  return launch_gemm(ctx, epi, A, lda, W, N, K, bias, C, ldc, M);
+}
+
 // ---------------------------------------------------------- host pointers
 
 int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float* qkv,

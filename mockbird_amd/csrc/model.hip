@@ -320,14 +320,17 @@ int mb_clear_seen(mb_ctx* ctx, int n, const int32_t* seq_ids) {
 namespace mb {
 namespace {
 
-// Global prefill; ln_f of each sequence's last row goes to last_hidden
-// [B][768] and, when all_hidden is set, ln_f of every row to
-// all_hidden[B][rows_max][768] (rows past n_rows[b] are zeroed).
+// Global prefill through the first `layer_count` layers; ln_f of each
+// sequence's last row goes to last_hidden [B][768] and, when all_hidden is
+// set, ln_f of every row to all_hidden[B][rows_max][768] (rows past n_rows[b]
+// are zeroed).
 int prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
-            float* last_hidden, float* all_hidden) {
+            int layer_count, float* last_hidden, float* all_hidden) {
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
+  if (layer_count < 1 || layer_count > ctx->cfg.n_layers)
+    return fail(ctx, MB_ERR_ARG, "layer_count %d out of [1, %d]", layer_count, ctx->cfg.n_layers);
   if (!ids || !n_rows || (!last_hidden && !all_hidden)) return fail(ctx, MB_ERR_ARG, "null pointer");
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
     return fail(ctx, MB_ERR_ARG, "rows_max %d out of [1, %d]", rows_max, ctx->cfg.max_rows);
@@ -370,7 +373,7 @@ int prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t*
       return rc;
   const ModelW& m = ctx->model;
   if ((rc = launch_embed_rows(ctx, d_ids, (int)M, m.wte, ctx->cfg.vocab, m.audio_emb, a.x))) return rc;
-  for (int l = 0; l < ctx->cfg.n_layers; l++) {
+  for (int l = 0; l < layer_count; l++) {
     if ((rc = cancelled(ctx))) return rc;
     if ((rc = run_layer(ctx, m.layers[l], global_ring(ctx, l), B, rows_max, M, d_pos0, d_n, d_off,
                         true, ctx->cfg.capacity, a)))
@@ -406,13 +409,14 @@ extern "C" {
 int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
                float* last_hidden) {
   if (ctx && !last_hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return prefill(ctx, B, rows_max, ids, n_rows, last_hidden, nullptr);
+  return prefill(ctx, B, rows_max, ids, n_rows, ctx ? ctx->cfg.n_layers : 0, last_hidden, nullptr);
 }
 
 int mb_prefill_rows(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
-                    float* hidden) {
+                    int layer_count, float* hidden) {
   if (ctx && !hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
-  return prefill(ctx, B, rows_max, ids, n_rows, nullptr, hidden);
+  if (ctx && layer_count <= 0) layer_count = ctx->cfg.n_layers;
+  return prefill(ctx, B, rows_max, ids, n_rows, layer_count, nullptr, hidden);
 }
 
 int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, float* hidden) {

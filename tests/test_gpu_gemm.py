@@ -1,0 +1,95 @@
+"""GPU parity of the projections (row a7) through mb_linear_dev, against the
+oracle's GEMM (double accumulation, fp32 output; pinned by a float64 closed
+form in test_oracle_kernels.py).
+
+The shapes cover both kernels the library picks from -- the streaming
+split-K kernel for decode-sized M (16/32/64 rows per wave, one split or
+many) and the LDS-tiled kernel for prefill-sized M -- at the model's
+projection shapes (768 -> 2304, 768 -> 768, 768 -> 3072, 3072 -> 768, the
+1024-code audio heads) plus ragged M and a narrow N.  Bar: max-abs 1e-4
+(fp32 products and accumulation; outputs are O(1)).
+"""
+import numpy as np
+import pytest
+
+import mockbird_amd as mb
+from oracle import oracle
+from conftest import say
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (M, N, K)
+    (1, 2304, 768), (1, 768, 768), (1, 3072, 768), (1, 768, 3072), (1, 1024, 768),
+    (2, 2304, 768), (3, 64, 768), (4, 768, 3072), (5, 1024, 768), (16, 2304, 768), (17, 768, 3072), (32, 1024, 768), (33, 3072, 768),
+    (64, 2304, 768), (100, 768, 3072), (256, 2304, 768), (256, 768, 3072), (256, 1024, 768),
+    (1000, 768, 768), (1024, 2304, 768), (1500, 768, 3072), (4096, 3072, 768),
+]
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    with mb.Context(n_layers=1, capacity=16, max_seqs=1, max_rows=16) as c:
+        yield c
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+def test_linear_matches_oracle(ctx, M, N, K):
+    torch = pytest.importorskip("torch")
+    say(f"linear M={M} N={N} K={K}")
+    g = np.random.default_rng([M, N, K])
+    A = g.standard_normal((M, K), dtype=np.float32)
+    W = (g.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
+    bias = (g.standard_normal(N, dtype=np.float32) * np.float32(0.1))
+    C0 = g.standard_normal((M, N), dtype=np.float32)
+    dev = torch.device("cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    tA, tW, tb = (torch.from_numpy(x).to(dev) for x in (A, W, bias))
+    want_lin = oracle.gemm(A, W, bias)
+    for epi in (mb.MB_EPI_STORE, mb.MB_EPI_GELU, mb.MB_EPI_ADD):
+        tC = torch.from_numpy(C0).to(dev)
+        ctx.linear_dev(M, N, K, tA.data_ptr(), K, tW.data_ptr(), tb.data_ptr(), tC.data_ptr(), N, epi)
+        torch.cuda.synchronize()
+        got = tC.cpu().numpy()
+        if epi == mb.MB_EPI_STORE:
+            want = want_lin
+        elif epi == mb.MB_EPI_GELU:
+            want = oracle.gelu(want_lin) if M * N <= 300000 else None
+        else:
+            want = C0 + want_lin
+        if want is None:  # large GELU case: compare the pre-activation through STORE above
+            continue
+        err = float(np.abs(got - want).max())
+        assert err < 1e-4, (epi, err)
+
+
+def test_linear_is_deterministic_and_strided(ctx):
+    """Split-K partials are summed in split order by whichever block finishes
+    last, so repeated calls are bit-identical; A and C may be row-strided."""
+    torch = pytest.importorskip("torch")
+    say("linear determinism + strides")
+    for M in (1, 5):
+        N, K = 768, 3072
+        g = np.random.default_rng(9)
+        A = g.standard_normal((M, K + 32), dtype=np.float32)
+        W = g.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+        dev = torch.device("cuda")
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        tA, tW = torch.from_numpy(A).to(dev), torch.from_numpy(W).to(dev)
+        outs = []
+        for _ in range(5):
+            tC = torch.zeros((M, N + 64), device=dev)
+            ctx.linear_dev(M, N, K, tA.data_ptr(), K + 32, tW.data_ptr(), None, tC.data_ptr(), N + 64)
+            torch.cuda.synchronize()
+            outs.append(tC.cpu().numpy())
+        for o in outs[1:]:
+            assert np.array_equal(o, outs[0])
+        assert not outs[0][:, N:].any()
+        assert np.abs(outs[0][:, :N] - oracle.gemm(A[:, :K], W)).max() < 1e-4
+
+
+def test_linear_rejects_bad_shapes(ctx):
+    with pytest.raises(mb.MbError) as e:
+        ctx.linear_dev(4, 100, 768, 16, 768, 16, None, 16, 100)  # N % 64 != 0
+    assert e.value.code == mb.MB_ERR_ARG
+    with pytest.raises(mb.MbError):
+        ctx.linear_dev(4, 64, 768, 16, 700, 16, None, 16, 64)  # lda < K

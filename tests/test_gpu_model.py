@@ -204,8 +204,8 @@ def test_c3_many_voices_subset():
 
 
 def test_prefill_rows_and_local_steps():
-    """PrefillRunner.run's whole hidden block (prefill.ts:325-603) and the
-    nextFrameSteps probe (decode.ts:970-1030) against the oracle: every row of
+    """PrefillRunner.run's whole hidden block (prefill.ts:325-603), also cut
+    to one layer by its layerCount argument, and the nextFrameSteps probe (decode.ts:970-1030) against the oracle: every row of
     a ragged 3-voice prefill, then local steps 0, 1, 2, 9 and 16 fed with the
     codes of the frame just chosen."""
     say("prefill_rows + local_steps, 2 layers, 3 voices")
@@ -217,7 +217,13 @@ def test_prefill_rows_and_local_steps():
     ids = np.full((B, n.max(), 17), 1024, np.int32)
     for b, p in enumerate(prompts):
         ids[b, :n[b]] = p
+    m1 = oracle.Model(w, n_layers=1, vocab=V)
     with _ctx(w, L, V, B, C) as ctx:
+        hid1 = ctx.prefill_rows(ids, n, layer_count=1)
+        for b in range(B):
+            ref = oracle.ModelState(m1, 1, C).prefill_all(0, prompts[b])
+            assert np.abs(hid1[b, :n[b]] - ref).max() < 1e-4, b
+        assert (ctx.read_ring(1, 0)[2] == -1).all()
         hid = ctx.prefill_rows(ids, n)
         for b in range(B):
             ref = oracle.ModelState(m, 1, C).prefill_all(0, prompts[b])
