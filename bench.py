@@ -190,8 +190,8 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
     """Greedy decode frames/s: prefill the prompts (untimed), then time
     `frames` frames, each the 17-step local head (text decision + 16 codes with
     the repetition penalty) followed by the 12-layer global decode step of the
-    frame row it produced.  Everything stays on the device; positions advance
-    one per frame."""
+    frame row it produced.  Everything stays on the device (mb_decode_frames_dev:
+    one graph launch per frame); positions advance one per frame."""
     import torch
 
     import mockbird_amd as mb
@@ -216,27 +216,23 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
     h0 = ctx.prefill(ids, n)
     t_pf = time.perf_counter() - t_pf
     total = warmup + frames
-    pos_all = torch.from_numpy((n[None, :] + np.arange(total)[:, None]).astype(np.int32)).to(dev)
     max_pos = int(n.max()) + total
     if max_pos >= C:
         raise ValueError("prompt + frames exceed the ring")
     h = torch.from_numpy(h0).to(dev)
-    codes = torch.empty((B, 16), dtype=torch.int32, device=dev)
-    cont = torch.empty(B, dtype=torch.int32, device=dev)
-    rows = torch.empty((B, 17), dtype=torch.int32, device=dev)
-
-    def frame(f):
-        ctx.local_frame_dev(B, h.data_ptr(), codes.data_ptr(), cont.data_ptr(), rows.data_ptr())
-        ctx.decode_step_dev(B, rows.data_ptr(), pos_all[f].data_ptr(), max_pos, h.data_ptr())
-
-    for f in range(warmup):
-        frame(f)
+    pos = torch.from_numpy(n.copy()).to(dev)
+    codes = torch.empty((max(frames, warmup), B, 16), dtype=torch.int32, device=dev)
+    cont = torch.empty((max(frames, warmup), B), dtype=torch.int32, device=dev)
+    # warm-up frames into the same buffers: the first call captures the frame's
+    # HIP graph and the timed call replays it
+    ctx.decode_frames_dev(B, warmup, h.data_ptr(), pos.data_ptr(), max_pos, codes.data_ptr(),
+                          cont.data_ptr())
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     t0.record(stream)
-    for f in range(warmup, total):
-        frame(f)
+    ctx.decode_frames_dev(B, frames, h.data_ptr(), pos.data_ptr(), max_pos, codes.data_ptr(),
+                          cont.data_ptr())
     t1.record(stream)
     torch.cuda.synchronize()
     ms = t0.elapsed_time(t1)

@@ -248,6 +248,23 @@ int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t*
 int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
                        int32_t* rows17_out);
 
+/* The frame loop on the device: n_frames greedy frames for sequences b < B.
+ * Each frame is DecodeRunner.nextFrame on hidden (decode.ts:788-939), then
+ * the global decode step of its frame row [assistant_id, codes] at pos[b]
+ * (GpuTtsEngine.decodeStep, gpu.ts:244-257), whose ln_f output replaces
+ * hidden; pos[b] then advances by one if sequence b continued (the runtime's
+ * loop, runtime.ts:528-561).  codes [n_frames][B][16] and cont
+ * [n_frames][B] receive every frame.  Every sequence starts the call alive;
+ * one that stops stays stopped for the rest of the call, keeps its position,
+ * and its later frames carry cont = 0 with codes to be ignored.
+ * All pointers are device memory; max_pos bounds every position the call
+ * reaches (pos[b] + n_frames - 1).  The first frame runs as ordinary
+ * launches and the next ones replay it from a HIP graph, captured once and
+ * kept while B, max_pos, the pointers and the context's buffers stay the
+ * same, so the host issues one graph launch per frame.  Enqueue only. */
+int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
+                         int32_t max_pos, int32_t* codes, int32_t* cont);
+
 #ifdef __cplusplus
 }
 #endif

@@ -130,10 +130,12 @@ int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assis
 // Continue/stop: two double-precision dot products of the step-0 hidden
 // state with text-head columns end_id and assistant_id; continue iff
 // assistant >= end (TEXT_HEAD_DECIDE kernels-decode.ts:487-518,
-// decideAssistantStop policy.ts:297-302).  One wave per sequence.
+// decideAssistantStop policy.ts:297-302).  One wave per sequence.  With
+// `alive`, a sequence already stopped (alive[b] == 0) stays stopped.
 __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h, int B,
                                                      const float* __restrict__ head, int vocab,
                                                      int end_id, int assistant_id,
+                                                     const int32_t* __restrict__ alive,
                                                      int32_t* __restrict__ cont) {
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -149,13 +151,13 @@ __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h
     e += __shfl_xor(e, off);
     a += __shfl_xor(a, off);
   }
-  if (lane == 0) cont[b] = a >= e ? 1 : 0;
+  if (lane == 0) cont[b] = a >= e && (!alive || alive[b]) ? 1 : 0;
 }
 
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
-                       int assistant_id, int32_t* cont) {
+                       int assistant_id, const int32_t* alive, int32_t* cont) {
   hipLaunchKernelGGL(k_text_decide, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream, h, B,
-                     head, vocab, end_id, assistant_id, cont);
+                     head, vocab, end_id, assistant_id, alive, cont);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
@@ -228,6 +230,41 @@ __global__ void k_frame_rows(const int32_t* __restrict__ tokens, int B, int assi
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17) {
   hipLaunchKernelGGL(k_frame_rows, dim3((unsigned)((B * ROW + 255) / 256)), dim3(256), 0,
                      ctx->stream, tokens, B, assistant_id, rows17);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// End of a device-resident frame: frame f's codes and continue flags go to
+// codes[f][B][16] and cont_out[f][B] (f read from *frame_idx, then advanced),
+// every sequence that continued moves to its next position, and one that
+// stopped is latched in alive[].  One workgroup, so the counter update
+// follows every read of it.
+__global__ __launch_bounds__(256) void k_frame_emit(const int32_t* __restrict__ tokens,
+                                                    const int32_t* __restrict__ cont, int B,
+                                                    int32_t* __restrict__ frame_idx,
+                                                    int32_t* __restrict__ codes,
+                                                    int32_t* __restrict__ cont_out,
+                                                    int32_t* __restrict__ pos,
+                                                    int32_t* __restrict__ alive) {
+  __shared__ int f;
+  if (threadIdx.x == 0) f = *frame_idx;
+  __syncthreads();
+  for (int i = threadIdx.x; i < B * NVQ; i += blockDim.x) codes[(int64_t)f * B * NVQ + i] = tokens[i];
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const int c = cont[b];
+    cont_out[(int64_t)f * B + b] = c;
+    alive[b] = c;
+    if (c) pos[b] += 1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *frame_idx = f + 1;
+}
+
+int launch_frame_emit(mb_ctx* ctx, const int32_t* tokens, const int32_t* cont, int B,
+                      int32_t* frame_idx, int32_t* codes, int32_t* cont_out, int32_t* pos,
+                      int32_t* alive) {
+  hipLaunchKernelGGL(k_frame_emit, dim3(1), dim3(256), 0, ctx->stream, tokens, cont, B, frame_idx,
+                     codes, cont_out, pos, alive);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

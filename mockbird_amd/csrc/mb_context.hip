@@ -37,6 +37,7 @@ void* scratch(mb_ctx* ctx, const char* name, size_t bytes) {
     s.bytes = 0;
   }
   size_t want = bytes < 4096 ? 4096 : bytes;
+  ctx->graph_gen++;
   if (hipMalloc(&s.ptr, want) != hipSuccess) {
     s.ptr = nullptr;
     return nullptr;
@@ -184,6 +185,8 @@ void mb_destroy(mb_ctx* ctx) {
   for (void* p : {(void*)ctx->local_k, (void*)ctx->local_v, (void*)ctx->local_sp,
                   (void*)ctx->local_pos, (void*)ctx->seen, (void*)ctx->tokens, (void*)ctx->cont})
     (void)hipFree(p);
+  if (ctx->frame_exec) (void)hipGraphExecDestroy(ctx->frame_exec);
+  if (ctx->capture_stream) (void)hipStreamDestroy(ctx->capture_stream);
   if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
   delete ctx;
 }
@@ -241,6 +244,7 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
   t.numel = numel;
   t.dims.assign(dims, dims + ndims);
   ctx->model_ok = false;
+  ctx->graph_gen++;
   MB_HIP(ctx, hipMemcpyAsync(t.ptr, data, (size_t)numel * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;

@@ -120,6 +120,16 @@ struct mb_ctx {
   int32_t* tokens = nullptr;     // [max_seqs][16]
   int32_t* cont = nullptr;       // [max_seqs]
   std::map<std::string, mb::Scratch> scratch;
+  // Bumped whenever a buffer a captured graph may point at moves (scratch
+  // reallocation, weight upload, first-use local-head state).
+  uint64_t graph_gen = 0;
+  // The captured frame of mb_decode_frames_dev and what it was captured for.
+  hipGraphExec_t frame_exec = nullptr;
+  hipStream_t capture_stream = nullptr;
+  uint64_t frame_key[8] = {};
+  // While mb_decode_frames_dev enqueues a frame: the sequences still alive
+  // (a stopped sequence stays stopped); null for the per-call entry points.
+  int32_t* frame_alive = nullptr;
   int64_t device_bytes = 0;
   std::atomic<int> cancel{0};
 };
@@ -209,9 +219,12 @@ int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, 
 int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
                        const AudioTables& audio, const int32_t* tokens, float* x);
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
-                       int assistant_id, int32_t* cont);
+                       int assistant_id, const int32_t* alive, int32_t* cont);
 int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
                           uint32_t* seen, const int32_t* cont, int32_t* tokens);
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);
+int launch_frame_emit(mb_ctx* ctx, const int32_t* tokens, const int32_t* cont, int B,
+                      int32_t* frame_idx, int32_t* codes, int32_t* cont_out, int32_t* pos,
+                      int32_t* alive);
 
 }  // namespace mb

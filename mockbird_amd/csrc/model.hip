@@ -159,6 +159,7 @@ int local_state(mb_ctx* ctx) {
   MB_HIP(ctx, hipMalloc(&ctx->tokens, (size_t)S * NVQ * 4));
   MB_HIP(ctx, hipMalloc(&ctx->cont, (size_t)S * 4));
   ctx->device_bytes += (int64_t)(2 * kv + S * ROW * 8 + S * NVQ * 32 * 4 + S * NVQ * 4 + S * 4);
+  ctx->graph_gen++;
   int rc;
   // the local cache is fp32 whatever the global rings hold: clear it as words
   if ((rc = launch_fill_i32(ctx, (int32_t*)ctx->local_k, (int64_t)kv / 4, 0))) return rc;
@@ -240,7 +241,7 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
     if (!pick) continue;
     if (step == 0) {
       rc = launch_text_decide(ctx, a.norm, B, m.text_head, ctx->cfg.vocab, ctx->end_id,
-                              ctx->assistant_id, ctx->cont);
+                              ctx->assistant_id, ctx->frame_alive, ctx->cont);
     } else {
       const int ch = step - 1;
       if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr,
@@ -492,6 +493,90 @@ int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t*
   if (max_pos < 0) return fail(ctx, MB_ERR_ARG, "max_pos %d is negative", max_pos);
   if ((rc = need_model(ctx))) return rc;
   return decode_step(ctx, B, rows17, pos, max_pos, hidden);
+}
+
+}  // extern "C"
+
+namespace mb {
+namespace {
+
+// One device-resident frame: local head on `hidden` -> frame rows, global
+// decode step of those rows at pos -> `hidden`, then the frame's codes and
+// flags to the outputs and pos += cont.
+int enqueue_frame(mb_ctx* ctx, int B, float* hidden, int32_t* pos, int32_t max_pos, int32_t* rows,
+                  int32_t* frame_idx, int32_t* alive, int32_t* codes, int32_t* cont) {
+  ctx->frame_alive = alive;
+  int rc = local_frame(ctx, B, hidden, nullptr, nullptr, rows);
+  ctx->frame_alive = nullptr;
+  if (rc) return rc;
+  if ((rc = decode_step(ctx, B, rows, pos, max_pos, hidden))) return rc;
+  return launch_frame_emit(ctx, ctx->tokens, ctx->cont, B, frame_idx, codes, cont, pos, alive);
+}
+
+}  // namespace
+}  // namespace mb
+
+extern "C" {
+
+int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
+                         int32_t max_pos, int32_t* codes, int32_t* cont) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (n_frames < 0) return fail(ctx, MB_ERR_ARG, "n_frames %d is negative", n_frames);
+  if (B == 0 || n_frames == 0) return MB_OK;
+  if (!hidden || !pos || !codes || !cont) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (max_pos < 0) return fail(ctx, MB_ERR_ARG, "max_pos %d is negative", max_pos);
+  if (!ctx->cfg.wrap && max_pos >= ctx->cfg.capacity)
+    return fail(ctx, MB_ERR_RANGE, "decode position %d exceeds the KV ring (%d slots)", max_pos,
+                ctx->cfg.capacity);
+  if ((rc = need_model(ctx))) return rc;
+  if ((rc = cancelled(ctx))) return rc;
+  int32_t* fidx = (int32_t*)scratch(ctx, "frame_idx", 4);
+  int32_t* rows = (int32_t*)scratch(ctx, "frame_rows", (size_t)B * ROW * 4);
+  int32_t* alive = (int32_t*)scratch(ctx, "frame_alive", (size_t)B * 4);
+  if (!fidx || !rows || !alive) return fail(ctx, MB_ERR_NOMEM, "frame staging allocation failed");
+  if ((rc = launch_fill_i32(ctx, fidx, 1, 0))) return rc;
+  if ((rc = launch_fill_i32(ctx, alive, B, 1))) return rc;
+  // Frame 0 runs eagerly: it sizes every scratch buffer the frame touches, so
+  // nothing is allocated while the next frame is captured.
+  if ((rc = enqueue_frame(ctx, B, hidden, pos, max_pos, rows, fidx, alive, codes, cont))) return rc;
+  if (n_frames == 1) return MB_OK;
+  const uint64_t key[8] = {(uint64_t)B, (uint64_t)max_pos, (uint64_t)(uintptr_t)hidden,
+                           (uint64_t)(uintptr_t)pos, (uint64_t)(uintptr_t)codes,
+                           (uint64_t)(uintptr_t)cont, ctx->graph_gen, 1};
+  if (!ctx->frame_exec || memcmp(key, ctx->frame_key, sizeof key) != 0) {
+    if (ctx->frame_exec) {
+      MB_HIP(ctx, hipGraphExecDestroy(ctx->frame_exec));
+      ctx->frame_exec = nullptr;
+    }
+    if (!ctx->capture_stream)
+      MB_HIP(ctx, hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking));
+    hipStream_t saved = ctx->stream;
+    ctx->stream = ctx->capture_stream;
+    MB_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    rc = enqueue_frame(ctx, B, hidden, pos, max_pos, rows, fidx, alive, codes, cont);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    ctx->stream = saved;
+    if (rc || e != hipSuccess || ctx->graph_gen != key[6]) {
+      if (graph) (void)hipGraphDestroy(graph);
+      if (rc) return rc;
+      if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+      return fail(ctx, MB_ERR_STATE, "a buffer moved while the frame was captured");
+    }
+    const hipError_t ei = hipGraphInstantiate(&ctx->frame_exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) {
+      ctx->frame_exec = nullptr;
+      return hip_fail(ctx, ei, "hipGraphInstantiate");
+    }
+    memcpy(ctx->frame_key, key, sizeof key);
+  }
+  for (int f = 1; f < n_frames; f++) {
+    if ((rc = cancelled(ctx))) return rc;
+    MB_HIP(ctx, hipGraphLaunch(ctx->frame_exec, ctx->stream));
+  }
+  return MB_OK;
 }
 
 int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,

@@ -239,3 +239,115 @@ def test_prefill_rows_and_local_steps():
                 assert np.abs(out[b] - ref).max() < 1e-4, (s, b)
         with pytest.raises(mb.MbError):
             ctx.local_steps(h, 17)
+
+
+def _per_call_frames(ctx, h, pos, max_pos, F, latch):
+    """The frame loop driven call by call on device buffers: local frame, then
+    the decode step of its row; positions advance for voices that continued
+    (with `latch`, a voice that stopped stays stopped)."""
+    import torch
+
+    B = pos.shape[0]
+    dev = h.device
+    codes = torch.zeros((B, 16), dtype=torch.int32, device=dev)
+    cont = torch.zeros(B, dtype=torch.int32, device=dev)
+    rows = torch.zeros((B, 17), dtype=torch.int32, device=dev)
+    alive = torch.ones(B, dtype=torch.int32, device=dev)
+    out_codes, out_cont = [], []
+    for f in range(F):
+        ctx.local_frame_dev(B, h.data_ptr(), codes.data_ptr(), cont.data_ptr(), rows.data_ptr())
+        ctx.decode_step_dev(B, rows.data_ptr(), pos.data_ptr(), max_pos, h.data_ptr())
+        eff = cont * alive if latch else cont
+        if latch:
+            alive = eff.clone()
+        pos += eff
+        torch.cuda.synchronize()
+        out_codes.append(codes.cpu().numpy().copy())
+        out_cont.append(eff.cpu().numpy().copy())
+    return np.stack(out_codes), np.stack(out_cont)
+
+
+def _prompt_batch(B, V, seed):
+    prompts = [synth.prompt(seed + b, n_frames=3 + 4 * b, n_text=4 + b, vocab=V) for b in range(B)]
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    return ids, n
+
+
+def test_device_frame_loop_matches_per_call_frames():
+    """mb_decode_frames_dev (frame 0 as plain launches, later frames replayed
+    from a captured HIP graph) against the same frames driven call by call:
+    codes, flags, positions and hidden states agree bit for bit over three
+    calls -- a capture, a recapture for new output buffers, and a replay of
+    the cached graph."""
+    torch = pytest.importorskip("torch")
+    say("device frame loop vs per-call frames (capture, recapture, replay)")
+    L, V, B, C, F = 2, 64, 4, 128, 12
+    w = _c0_weights(n_layers=L, vocab=V, seed=21)
+    ids, n = _prompt_batch(B, V, 60)
+    max_pos = int(n.max()) + F
+    dev = torch.device("cuda")
+    with _ctx(w, L, V, B, C) as ref:
+        ref.set_stream(torch.cuda.current_stream().cuda_stream)
+        h = torch.from_numpy(ref.prefill(ids, n)).to(dev)
+        pos = torch.from_numpy(n.copy()).to(dev)
+        want_codes, want_cont = _per_call_frames(ref, h, pos, max_pos, F, latch=False)
+        want_h, want_pos = h.cpu().numpy(), pos.cpu().numpy()
+    assert want_cont.all()
+    with _ctx(w, L, V, B, C) as ctx:
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        h = torch.from_numpy(ctx.prefill(ids, n)).to(dev)
+        pos = torch.from_numpy(n.copy()).to(dev)
+        bufs = [(torch.full((4, B, 16), -1, dtype=torch.int32, device=dev),
+                 torch.full((4, B), -1, dtype=torch.int32, device=dev)) for _ in range(2)]
+        got = []
+        for cb, fb in [bufs[0], bufs[1], bufs[1]]:
+            ctx.decode_frames_dev(B, 4, h.data_ptr(), pos.data_ptr(), max_pos, cb.data_ptr(),
+                                  fb.data_ptr())
+            torch.cuda.synchronize()
+            got.append((cb.cpu().numpy().copy(), fb.cpu().numpy().copy()))
+        assert np.array_equal(np.concatenate([g[1] for g in got]), want_cont)
+        assert np.array_equal(np.concatenate([g[0] for g in got]), want_codes)
+        assert np.array_equal(pos.cpu().numpy(), want_pos)
+        assert np.array_equal(h.cpu().numpy(), want_h)
+
+
+def test_device_frame_loop_stops_voices():
+    """An untied model whose voices stop at different frames: within one call a
+    stopped voice stays stopped and keeps its position; the voices still
+    going match the call-by-call loop bit for bit."""
+    torch = pytest.importorskip("torch")
+    say("device frame loop with stopping voices")
+    L, V, B, C, F = 2, 64, 6, 128, 10
+    w = synth.model_weights(n_layers=L, vocab=V, seed=21, bias_std=0.02, ln_std=0.1)
+    ids, n = _prompt_batch(B, V, 80)
+    max_pos = int(n.max()) + F
+    dev = torch.device("cuda")
+    with _ctx(w, L, V, B, C) as ref:
+        ref.set_stream(torch.cuda.current_stream().cuda_stream)
+        h = torch.from_numpy(ref.prefill(ids, n)).to(dev)
+        pos = torch.from_numpy(n.copy()).to(dev)
+        want_codes, want_cont = _per_call_frames(ref, h, pos, max_pos, F, latch=True)
+        want_h, want_pos = h.cpu().numpy(), pos.cpu().numpy()
+    with _ctx(w, L, V, B, C) as ctx:
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        h = torch.from_numpy(ctx.prefill(ids, n)).to(dev)
+        pos = torch.from_numpy(n.copy()).to(dev)
+        cb = torch.full((F, B, 16), -1, dtype=torch.int32, device=dev)
+        fb = torch.full((F, B), -1, dtype=torch.int32, device=dev)
+        ctx.decode_frames_dev(B, F, h.data_ptr(), pos.data_ptr(), max_pos, cb.data_ptr(),
+                              fb.data_ptr())
+        torch.cuda.synchronize()
+        got_codes, got_cont = cb.cpu().numpy(), fb.cpu().numpy()
+    say(f"  frames continued per voice: {want_cont.sum(0).tolist()}")
+    assert want_cont[0].any() and not want_cont[-1].all(), "expected a mix of going and stopped voices"
+    assert np.array_equal(got_cont, want_cont)
+    live = want_cont.astype(bool)
+    assert np.array_equal(got_codes[live], want_codes[live])
+    assert np.array_equal(pos.cpu().numpy(), want_pos)
+    going = want_cont[-1].astype(bool)
+    assert np.array_equal(h.cpu().numpy()[going], want_h[going])
+    # the latch: once 0, a voice's flag stays 0
+    assert (np.diff(got_cont, axis=0) <= 0).all()
