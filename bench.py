@@ -35,6 +35,22 @@ HBM_PEAK_GBS = 8000.0
 D, H, HD, QKV = 768, 12, 64, 2304
 
 
+PROFILE = os.path.join(ROOT, "profiles", "decode_attention_b64_c2048.md")
+
+
+def profiled_traffic(key="traffic_bytes_per_launch_bf16"):
+    """HBM bytes per decode-attention launch from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs scaled by a known-size copy), or
+    None when the summary holds no such line."""
+    try:
+        for line in open(PROFILE):
+            if line.startswith(key + ":"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def c1_positions(B=64, seed=20260101):
     g = np.random.default_rng(seed)
     return g.integers(1, 6144, size=B).astype(np.int32)
@@ -175,6 +191,31 @@ def run_c2(args):
             "frac_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
 
 
+def run_copy(nbytes=1 << 31, reps=10):
+    """A plain device-to-device copy of `nbytes` (torch's copy kernel): the
+    achievable HBM rate on this box, and the known-size kernel the HBM byte
+    counters are calibrated against."""
+    import torch
+
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        dst.copy_(src)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = float(np.mean([a.elapsed_time(b) for a, b in evs]) * 1e3)
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "avg_us": round(us, 2),
+            "gbs": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
+
+
 def frame_prompts(B, seed=33):
     """Voice-clone prompts with total lengths U[64, 400) (half code frames,
     the rest text ids), as the many-voice decode configuration draws them."""
@@ -288,9 +329,10 @@ def main():
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
-    ap.add_argument("--legs", default="c1,c2,frames",
-                    help="comma list of c1 (append + decode attention), c2 (prefill attention), "
-                         "frames (model decode frames/s); the JSON line needs c1")
+    ap.add_argument("--legs", default="copy,c1,c2,frames",
+                    help="comma list of copy (plain 2 GiB HBM copy), c1 (append + decode "
+                         "attention), c2 (prefill attention), frames (model decode frames/s); "
+                         "the JSON line needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -303,6 +345,7 @@ def main():
         legs.discard("c2")
     if args.no_frames:
         legs.discard("frames")
+    copy = run_copy() if "copy" in legs else None
     c2 = run_c2(args) if "c2" in legs else None
     frames = None
     if "frames" in legs:
@@ -315,7 +358,8 @@ def main():
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
         frames = [run_frames(w, b, *plan[b]) for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
-        print(json.dumps({"prefill_attention": c2, "frames_detail": frames}), flush=True)
+        print(json.dumps({"hbm_copy": copy, "prefill_attention": c2, "frames_detail": frames}),
+              flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -345,7 +389,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(bf16["attn_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(),
             "kernel": "decode attention (k_attn_split + k_attn_combine)",
             "avg_us": round(bf16["attn_us"], 2),
             "bytes_per_launch": int(bf16["attn_bytes"]),
@@ -356,6 +400,7 @@ def main():
             "ms_per_step": round(f32["ms_per_step"], 5),
             "attn_gbs": round(f32["attn_gbs"], 1), "attn_us": round(f32["attn_us"], 2),
             "frac": round(f32["attn_gbs"] / HBM_PEAK_GBS, 4)},
+        "hbm_copy": copy,
         "prefill_attention": c2,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
         "frames_detail": frames,

@@ -265,6 +265,15 @@ int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, 
 int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
                          int32_t max_pos, int32_t* codes, int32_t* cont);
 
+/* Host-pointer form of mb_decode_frames_dev: hidden [B][768] and pos [B] are
+ * read, and on return hold the state after the last frame (the hidden state
+ * and position the next frame starts from); codes [n_frames][B][16] and cont
+ * [n_frames][B] receive every frame.  Synchronises before returning.  The
+ * whole of WgpuTtsRuntime's frame loop (runtime.ts:539-561: nextFrame, then
+ * decodeStep at prompt_rows + step) for many voices in one call. */
+int mb_decode_frames(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
+                     int32_t* codes, int32_t* cont);
+
 #ifdef __cplusplus
 }
 #endif

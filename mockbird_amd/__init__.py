@@ -31,7 +31,7 @@ EXPORTS = (
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
-    "mb_linear_dev", "mb_decode_frames_dev",
+    "mb_linear_dev", "mb_decode_frames_dev", "mb_decode_frames",
 )
 
 
@@ -109,6 +109,7 @@ def load():
         "mb_linear_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int64, _vp, _vp, _vp,
                            C.c_int64, C.c_int], C.c_int),
         "mb_decode_frames_dev": ([_vp, C.c_int, C.c_int, _vp, _vp, _i32, _vp, _vp], C.c_int),
+        "mb_decode_frames": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -267,6 +268,17 @@ class Context:
     def decode_frames_dev(self, B, n_frames, hidden_ptr, pos_ptr, max_pos, codes_ptr, cont_ptr):
         self.check(self.lib.mb_decode_frames_dev(self.h, B, n_frames, hidden_ptr, pos_ptr, max_pos,
                                                  codes_ptr, cont_ptr))
+
+    def decode_frames(self, hidden: np.ndarray, pos, n_frames: int):
+        """Host form of the frame loop: returns (codes [n][B][16], cont [n][B],
+        hidden after the last frame [B][768], positions after it [B])."""
+        h, p = _f32c(hidden).copy(), _i32c(pos).copy()
+        B = h.shape[0]
+        codes = np.zeros((n_frames, B, NVQ), np.int32)
+        cont = np.zeros((n_frames, B), np.int32)
+        self.check(self.lib.mb_decode_frames(self.h, B, n_frames, h.ctypes.data, p.ctypes.data,
+                                             codes.ctypes.data, cont.ctypes.data))
+        return codes, cont.astype(bool), h, p
 
     def linear_dev(self, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc, epi=0):
         self.check(self.lib.mb_linear_dev(self.h, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc,

@@ -73,6 +73,7 @@ def build_addon() -> str | None:
     if not os.path.exists(os.path.join(node_inc, "node_api.h")):
         sys.stderr.write("node_api.h not found; skipping the N-API addon\n")
         return None
+    os.makedirs(os.path.dirname(ADDON), exist_ok=True)
     tmp = ADDON + ".tmp"
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-Wall", "-I", node_inc,
           "-I", os.path.join(ROOT, "include"), src, "-o", tmp, "-L", PKG, "-lmockbird_hip",

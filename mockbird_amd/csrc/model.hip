@@ -579,6 +579,42 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
   return MB_OK;
 }
 
+int mb_decode_frames(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
+                     int32_t* codes, int32_t* cont) {
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (n_frames < 0) return fail(ctx, MB_ERR_ARG, "n_frames %d is negative", n_frames);
+  if (B == 0 || n_frames == 0) return MB_OK;
+  if (!hidden || !pos || !codes || !cont) return fail(ctx, MB_ERR_ARG, "null pointer");
+  int64_t max_pos = 0;
+  for (int b = 0; b < B; b++) {
+    if (pos[b] < 0) return fail(ctx, MB_ERR_ARG, "sequence %d: negative position %d", b, pos[b]);
+    if ((int64_t)pos[b] + n_frames - 1 > max_pos) max_pos = (int64_t)pos[b] + n_frames - 1;
+  }
+  if (max_pos > INT32_MAX) return fail(ctx, MB_ERR_ARG, "positions overflow int32");
+  float* d_hidden = (float*)scratch(ctx, "frames_hidden", (size_t)B * D * 4);
+  int32_t* d_pos = (int32_t*)scratch(ctx, "frames_pos", (size_t)B * 4);
+  int32_t* d_codes = (int32_t*)scratch(ctx, "frames_codes", (size_t)n_frames * B * NVQ * 4);
+  int32_t* d_cont = (int32_t*)scratch(ctx, "frames_cont", (size_t)n_frames * B * 4);
+  if (!d_hidden || !d_pos || !d_codes || !d_cont)
+    return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_hidden, hidden, (size_t)B * D * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_pos, pos, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  if ((rc = mb_decode_frames_dev(ctx, B, n_frames, d_hidden, d_pos, (int32_t)max_pos, d_codes,
+                                 d_cont))) {
+    (void)hipStreamSynchronize(ctx->stream);
+    return rc;
+  }
+  MB_HIP(ctx, hipMemcpyAsync(hidden, d_hidden, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(pos, d_pos, (size_t)B * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(codes, d_codes, (size_t)n_frames * B * NVQ * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(cont, d_cont, (size_t)n_frames * B * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
 int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
                        int32_t* rows17_out) {
   int rc = check_b(ctx, B);

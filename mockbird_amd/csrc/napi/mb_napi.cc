@@ -1,0 +1,650 @@
+// mockbird_hip.node -- the thin N-API binding of libmockbird_hip.so for the
+// JavaScript host engine (mockbird_amd/engine/engine.mjs).
+//
+// The reference host reaches the GPU through WebGPU (src/lib/tts/engine/gpu.ts,
+// prefill.ts, decode.ts); this addon is the one place JavaScript meets the C ABI
+// of include/mockbird_hip.h.  It holds no state of its own beyond the context
+// handle, checks every typed-array length against the sizes the C call will
+// read or write (the C ABI trusts its pointers), copies nothing it does not
+// have to (typed arrays are passed by their backing store), and turns a
+// non-zero status into a thrown Error carrying mb_last_error() and the status
+// name as `code` (MB_ERR_RANGE, ...).
+//
+// Every function is synchronous, as every reference engine call is awaited
+// before the next one starts (runtime.ts:523-561 never overlaps two calls).
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "mockbird_hip.h"
+
+namespace {
+
+constexpr int64_t kD = 768, kQkv = 2304, kRow = 17, kNvq = 16;
+
+const char* status_name(int rc) {
+  switch (rc) {
+    case MB_ERR_ARG: return "MB_ERR_ARG";
+    case MB_ERR_RANGE: return "MB_ERR_RANGE";
+    case MB_ERR_HIP: return "MB_ERR_HIP";
+    case MB_ERR_STATE: return "MB_ERR_STATE";
+    case MB_ERR_CANCELLED: return "MB_ERR_CANCELLED";
+    case MB_ERR_NOMEM: return "MB_ERR_NOMEM";
+    default: return "MB_ERR_UNKNOWN";
+  }
+}
+
+// Thrown-error helpers: each returns nullptr so callers can `return throw_*`.
+napi_value throw_type(napi_env env, const std::string& msg) {
+  napi_throw_type_error(env, "ERR_INVALID_ARG_TYPE", msg.c_str());
+  return nullptr;
+}
+napi_value throw_range(napi_env env, const std::string& msg) {
+  napi_throw_range_error(env, "ERR_OUT_OF_RANGE", msg.c_str());
+  return nullptr;
+}
+
+// An Error with .code = status name and .status = the numeric code.
+napi_value throw_status(napi_env env, mb_ctx* ctx, int rc) {
+  const char* msg = ctx ? mb_last_error(ctx) : "mb_create failed";
+  napi_value code, text, err, st;
+  napi_create_string_utf8(env, status_name(rc), NAPI_AUTO_LENGTH, &code);
+  napi_create_string_utf8(env, msg && *msg ? msg : status_name(rc), NAPI_AUTO_LENGTH, &text);
+  napi_create_error(env, code, text, &err);
+  napi_create_int32(env, rc, &st);
+  napi_set_named_property(env, err, "status", st);
+  napi_throw(env, err);
+  return nullptr;
+}
+
+struct Args {
+  napi_env env;
+  size_t argc = 12;
+  napi_value argv[12];
+  bool ok = true;
+  Args(napi_env e, napi_callback_info info) : env(e) {
+    napi_get_cb_info(e, info, &argc, argv, nullptr, nullptr);
+  }
+  napi_value at(size_t i) {
+    if (i < argc) return argv[i];
+    napi_value u;
+    napi_get_undefined(env, &u);
+    return u;
+  }
+};
+
+bool get_i64(napi_env env, napi_value v, int64_t* out, const char* what) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_number) {
+    throw_type(env, std::string(what) + " must be a number");
+    return false;
+  }
+  double d;
+  napi_get_value_double(env, v, &d);
+  if (!(d == (double)(int64_t)d) || d < -2147483648.0 || d > 2147483647.0) {
+    throw_range(env, std::string(what) + " must be a 32-bit integer");
+    return false;
+  }
+  *out = (int64_t)d;
+  return true;
+}
+
+bool get_int(napi_env env, napi_value v, int* out, const char* what) {
+  int64_t x;
+  if (!get_i64(env, v, &x, what)) return false;
+  *out = (int)x;
+  return true;
+}
+
+bool get_f32(napi_env env, napi_value v, float* out, const char* what) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_number) {
+    throw_type(env, std::string(what) + " must be a number");
+    return false;
+  }
+  double d;
+  napi_get_value_double(env, v, &d);
+  *out = (float)d;
+  return true;
+}
+
+mb_ctx* get_ctx(napi_env env, napi_value v) {
+  void* p = nullptr;
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t != napi_external || napi_get_value_external(env, v, &p) != napi_ok || !p) {
+    throw_type(env, "the first argument must be a live context handle");
+    return nullptr;
+  }
+  mb_ctx** slot = (mb_ctx**)p;
+  if (!*slot) {
+    throw_type(env, "the context was destroyed");
+    return nullptr;
+  }
+  return *slot;
+}
+
+// A typed array of the expected element type with at least `need` elements
+// (need < 0: any length); `allow_null` accepts null/undefined (-> nullptr).
+template <typename T>
+bool get_array(napi_env env, napi_value v, napi_typedarray_type want, int64_t need, T** out,
+               int64_t* len, const char* what, bool allow_null = false) {
+  napi_valuetype vt;
+  napi_typeof(env, v, &vt);
+  if (allow_null && (vt == napi_null || vt == napi_undefined)) {
+    *out = nullptr;
+    if (len) *len = 0;
+    return true;
+  }
+  bool is_ta = false;
+  napi_is_typedarray(env, v, &is_ta);
+  napi_typedarray_type type;
+  size_t n = 0, off = 0;
+  void* data = nullptr;
+  napi_value ab;
+  if (!is_ta || napi_get_typedarray_info(env, v, &type, &n, &data, &ab, &off) != napi_ok ||
+      type != want) {
+    const char* tn = want == napi_float32_array ? "a Float32Array" : "an Int32Array";
+    throw_type(env, std::string(what) + " must be " + tn);
+    return false;
+  }
+  if (need >= 0 && (int64_t)n < need) {
+    throw_range(env, std::string(what) + " holds " + std::to_string(n) + " elements, needs " +
+                         std::to_string(need));
+    return false;
+  }
+  *out = (T*)data;
+  if (len) *len = (int64_t)n;
+  return true;
+}
+
+napi_value new_f32(napi_env env, int64_t n, float** data) {
+  napi_value ab, ta;
+  void* p = nullptr;
+  napi_create_arraybuffer(env, (size_t)n * 4, &p, &ab);
+  if (n) std::memset(p, 0, (size_t)n * 4);
+  napi_create_typedarray(env, napi_float32_array, (size_t)n, ab, 0, &ta);
+  *data = (float*)p;
+  return ta;
+}
+
+napi_value new_i32(napi_env env, int64_t n, int32_t** data) {
+  napi_value ab, ta;
+  void* p = nullptr;
+  napi_create_arraybuffer(env, (size_t)n * 4, &p, &ab);
+  if (n) std::memset(p, 0, (size_t)n * 4);
+  napi_create_typedarray(env, napi_int32_array, (size_t)n, ab, 0, &ta);
+  *data = (int32_t*)p;
+  return ta;
+}
+
+napi_value num(napi_env env, double x) {
+  napi_value v;
+  napi_create_double(env, x, &v);
+  return v;
+}
+
+napi_value undef(napi_env env) {
+  napi_value v;
+  napi_get_undefined(env, &v);
+  return v;
+}
+
+bool read_config_field(napi_env env, napi_value obj, const char* key, int32_t* out) {
+  bool has = false;
+  napi_has_named_property(env, obj, key, &has);
+  if (!has) return true;  // keep the default
+  napi_value v;
+  napi_get_named_property(env, obj, key, &v);
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_undefined) return true;
+  if (t == napi_boolean) {
+    bool b;
+    napi_get_value_bool(env, v, &b);
+    *out = b ? 1 : 0;
+    return true;
+  }
+  int x;
+  if (!get_int(env, v, &x, key)) return false;
+  *out = x;
+  return true;
+}
+
+void finalize_ctx(napi_env, void* data, void*) {
+  mb_ctx** slot = (mb_ctx**)data;
+  if (*slot) mb_destroy(*slot);
+  delete slot;
+}
+
+// ---------------------------------------------------------------- bindings
+
+napi_value AbiVersion(napi_env env, napi_callback_info) { return num(env, mb_abi_version()); }
+
+// create({nLayers, vocab, capacity, maxSeqs, maxRows, kvDtype, wrap, device}) -> handle
+napi_value Create(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_config cfg{12, 16384, 1024, 1, 512, MB_KV_F32, 1, 0};
+  napi_valuetype t;
+  napi_typeof(env, a.at(0), &t);
+  if (t != napi_object) return throw_type(env, "create() takes a config object");
+  napi_value o = a.at(0);
+  if (!read_config_field(env, o, "nLayers", &cfg.n_layers) ||
+      !read_config_field(env, o, "vocab", &cfg.vocab) ||
+      !read_config_field(env, o, "capacity", &cfg.capacity) ||
+      !read_config_field(env, o, "maxSeqs", &cfg.max_seqs) ||
+      !read_config_field(env, o, "maxRows", &cfg.max_rows) ||
+      !read_config_field(env, o, "kvDtype", &cfg.kv_dtype) ||
+      !read_config_field(env, o, "wrap", &cfg.wrap) ||
+      !read_config_field(env, o, "device", &cfg.device))
+    return nullptr;
+  mb_ctx* ctx = nullptr;
+  int rc = mb_create(&cfg, &ctx);
+  if (rc != MB_OK) {
+    napi_throw_error(env, status_name(rc), "mb_create failed (bad configuration or no device)");
+    return nullptr;
+  }
+  mb_ctx** slot = new mb_ctx*(ctx);
+  napi_value h;
+  napi_create_external(env, slot, finalize_ctx, nullptr, &h);
+  return h;
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  void* p = nullptr;
+  napi_valuetype t;
+  napi_typeof(env, a.at(0), &t);
+  if (t != napi_external || napi_get_value_external(env, a.at(0), &p) != napi_ok || !p)
+    return throw_type(env, "destroy() takes a context handle");
+  mb_ctx** slot = (mb_ctx**)p;
+  if (*slot) mb_destroy(*slot);
+  *slot = nullptr;
+  return undef(env);
+}
+
+napi_value DeviceBytes(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  return num(env, (double)mb_device_bytes(ctx));
+}
+
+// uploadTensor(h, name, Float32Array data, dims: number[])
+napi_value UploadTensor(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, a.at(1), nullptr, 0, &len) != napi_ok)
+    return throw_type(env, "name must be a string");
+  std::string name(len, '\0');
+  napi_get_value_string_utf8(env, a.at(1), &name[0], len + 1, &len);
+  bool is_arr = false;
+  napi_is_array(env, a.at(3), &is_arr);
+  if (!is_arr) return throw_type(env, "dims must be an array of numbers");
+  uint32_t nd = 0;
+  napi_get_array_length(env, a.at(3), &nd);
+  if (nd < 1 || nd > 4) return throw_range(env, "dims must have 1 to 4 entries");
+  std::vector<int64_t> dims(nd);
+  int64_t numel = 1;
+  for (uint32_t i = 0; i < nd; i++) {
+    napi_value e;
+    napi_get_element(env, a.at(3), i, &e);
+    if (!get_i64(env, e, &dims[i], "dims[i]")) return nullptr;
+    if (dims[i] <= 0) return throw_range(env, "dims must be positive");
+    numel *= dims[i];
+  }
+  float* data;
+  int64_t n;
+  if (!get_array(env, a.at(2), napi_float32_array, numel, &data, &n, "data")) return nullptr;
+  if (n != numel) return throw_range(env, "data length does not match dims for " + name);
+  int rc = mb_upload_tensor(ctx, name.c_str(), data, dims.data(), (int)nd);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+napi_value Cancel(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  bool on = true;
+  napi_valuetype t;
+  napi_typeof(env, a.at(1), &t);
+  if (t == napi_boolean) napi_get_value_bool(env, a.at(1), &on);
+  int rc = mb_cancel(ctx, on ? 1 : 0);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+napi_value SetLocalHead(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int end_id, assistant;
+  float penalty;
+  if (!get_int(env, a.at(1), &end_id, "audioEndTokenId") ||
+      !get_int(env, a.at(2), &assistant, "audioAssistantSlotTokenId") ||
+      !get_f32(env, a.at(3), &penalty, "repetitionPenalty"))
+    return nullptr;
+  int rc = mb_set_local_head(ctx, end_id, assistant, penalty);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+// ringReset(h, Int32Array seqIds | null) / clearSeen(h, Int32Array seqIds | null)
+template <int (*F)(mb_ctx*, int, const int32_t*)>
+napi_value SeqListCall(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int32_t* ids;
+  int64_t n;
+  if (!get_array(env, a.at(1), napi_int32_array, -1, &ids, &n, "seqIds", true)) return nullptr;
+  int rc = F(ctx, ids ? (int)n : -1, ids);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+napi_value RingPoison(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, seq, n;
+  float sentinel;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &seq, "seq") ||
+      !get_int(env, a.at(3), &n, "nSlots") || !get_f32(env, a.at(4), &sentinel, "sentinel"))
+    return nullptr;
+  int rc = mb_ring_poison(ctx, layer, seq, n, sentinel);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+// readRing(h, layer, seq, slot0, n) -> {key, value, slotPos}
+napi_value ReadRing(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, seq, slot0, n;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &seq, "seq") ||
+      !get_int(env, a.at(3), &slot0, "slot0") || !get_int(env, a.at(4), &n, "n"))
+    return nullptr;
+  if (n < 0) return throw_range(env, "n must be >= 0");
+  float *k, *v;
+  int32_t* sp;
+  napi_value K = new_f32(env, (int64_t)n * kD, &k), V = new_f32(env, (int64_t)n * kD, &v);
+  napi_value S = new_i32(env, n, &sp);
+  int rc = mb_read_ring(ctx, layer, seq, slot0, n, k, v, sp);
+  if (rc) return throw_status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "key", K);
+  napi_set_named_property(env, o, "value", V);
+  napi_set_named_property(env, o, "slotPos", S);
+  return o;
+}
+
+// ringAppend(h, layer, B, qkv Float32Array[B*2304], pos Int32Array[B]) -> q Float32Array[B*768]
+napi_value RingAppend(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, B;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &B, "B")) return nullptr;
+  if (B < 0) return throw_range(env, "B must be >= 0");
+  float* qkv;
+  int32_t* pos;
+  if (!get_array(env, a.at(3), napi_float32_array, (int64_t)B * kQkv, &qkv, nullptr, "qkv") ||
+      !get_array(env, a.at(4), napi_int32_array, B, &pos, nullptr, "pos"))
+    return nullptr;
+  float* q;
+  napi_value Q = new_f32(env, (int64_t)B * kD, &q);
+  int rc = mb_ring_append(ctx, layer, B, qkv, pos, q);
+  if (rc) return throw_status(env, ctx, rc);
+  return Q;
+}
+
+// ringWriteRows(h, layer, B, rowsMax, qkv[B*rowsMax*2304], pos0[B], nRows[B]) -> q[B*rowsMax*768]
+napi_value RingWriteRows(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, B, R;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &B, "B") ||
+      !get_int(env, a.at(3), &R, "rowsMax"))
+    return nullptr;
+  if (B < 0 || R < 0) return throw_range(env, "B and rowsMax must be >= 0");
+  float* qkv;
+  int32_t *p0, *nr;
+  if (!get_array(env, a.at(4), napi_float32_array, (int64_t)B * R * kQkv, &qkv, nullptr, "qkv") ||
+      !get_array(env, a.at(5), napi_int32_array, B, &p0, nullptr, "pos0") ||
+      !get_array(env, a.at(6), napi_int32_array, B, &nr, nullptr, "nRows"))
+    return nullptr;
+  float* q;
+  napi_value Q = new_f32(env, (int64_t)B * R * kD, &q);
+  int rc = mb_ring_write_rows(ctx, layer, B, R, qkv, p0, nr, q);
+  if (rc) return throw_status(env, ctx, rc);
+  return Q;
+}
+
+// decodeAttention(h, layer, B, q[B*768], pos[B]) -> out[B*768]
+napi_value DecodeAttention(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, B;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &B, "B")) return nullptr;
+  if (B < 0) return throw_range(env, "B must be >= 0");
+  float* q;
+  int32_t* pos;
+  if (!get_array(env, a.at(3), napi_float32_array, (int64_t)B * kD, &q, nullptr, "q") ||
+      !get_array(env, a.at(4), napi_int32_array, B, &pos, nullptr, "pos"))
+    return nullptr;
+  float* out;
+  napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  int rc = mb_decode_attention(ctx, layer, B, q, pos, out);
+  if (rc) return throw_status(env, ctx, rc);
+  return O;
+}
+
+// prefillAttention(h, layer, B, rowsMax, q[B*rowsMax*768], pos0[B], nRows[B]) -> out
+napi_value PrefillAttention(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, B, R;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &B, "B") ||
+      !get_int(env, a.at(3), &R, "rowsMax"))
+    return nullptr;
+  if (B < 0 || R < 0) return throw_range(env, "B and rowsMax must be >= 0");
+  float* q;
+  int32_t *p0, *nr;
+  if (!get_array(env, a.at(4), napi_float32_array, (int64_t)B * R * kD, &q, nullptr, "q") ||
+      !get_array(env, a.at(5), napi_int32_array, B, &p0, nullptr, "pos0") ||
+      !get_array(env, a.at(6), napi_int32_array, B, &nr, nullptr, "nRows"))
+    return nullptr;
+  float* out;
+  napi_value O = new_f32(env, (int64_t)B * R * kD, &out);
+  int rc = mb_prefill_attention(ctx, layer, B, R, q, p0, nr, out);
+  if (rc) return throw_status(env, ctx, rc);
+  return O;
+}
+
+// prefill(h, B, rowsMax, ids Int32Array[B*rowsMax*17], nRows Int32Array[B], layerCount?, allRows?)
+//   -> Float32Array: [B*768] last-row hidden, or [B*rowsMax*768] with allRows
+napi_value Prefill(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B, R, layer_count = 0;
+  if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &R, "rowsMax")) return nullptr;
+  if (B < 0 || R < 0) return throw_range(env, "B and rowsMax must be >= 0");
+  int32_t *ids, *nr;
+  if (!get_array(env, a.at(3), napi_int32_array, (int64_t)B * R * kRow, &ids, nullptr, "ids") ||
+      !get_array(env, a.at(4), napi_int32_array, B, &nr, nullptr, "nRows"))
+    return nullptr;
+  napi_valuetype t;
+  napi_typeof(env, a.at(5), &t);
+  if (t != napi_undefined && t != napi_null && !get_int(env, a.at(5), &layer_count, "layerCount"))
+    return nullptr;
+  bool all_rows = false;
+  napi_typeof(env, a.at(6), &t);
+  if (t == napi_boolean) napi_get_value_bool(env, a.at(6), &all_rows);
+  float* out;
+  int rc;
+  napi_value O;
+  if (all_rows || layer_count > 0) {
+    O = new_f32(env, (int64_t)B * R * kD, &out);
+    rc = mb_prefill_rows(ctx, B, R, ids, nr, layer_count, out);
+  } else {
+    O = new_f32(env, (int64_t)B * kD, &out);
+    rc = mb_prefill(ctx, B, R, ids, nr, out);
+  }
+  if (rc) return throw_status(env, ctx, rc);
+  return O;
+}
+
+// decodeStep(h, B, rows17 Int32Array[B*17], pos Int32Array[B]) -> hidden Float32Array[B*768]
+napi_value DecodeStep(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B;
+  if (!get_int(env, a.at(1), &B, "B")) return nullptr;
+  if (B < 0) return throw_range(env, "B must be >= 0");
+  int32_t *rows, *pos;
+  if (!get_array(env, a.at(2), napi_int32_array, (int64_t)B * kRow, &rows, nullptr, "rows17") ||
+      !get_array(env, a.at(3), napi_int32_array, B, &pos, nullptr, "pos"))
+    return nullptr;
+  float* out;
+  napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  int rc = mb_decode_step(ctx, B, rows, pos, out);
+  if (rc) return throw_status(env, ctx, rc);
+  return O;
+}
+
+// localFrame(h, B, hidden Float32Array[B*768]) -> {codes Int32Array[B*16], cont Int32Array[B]}
+napi_value LocalFrame(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B;
+  if (!get_int(env, a.at(1), &B, "B")) return nullptr;
+  if (B < 0) return throw_range(env, "B must be >= 0");
+  float* hidden;
+  if (!get_array(env, a.at(2), napi_float32_array, (int64_t)B * kD, &hidden, nullptr, "hidden"))
+    return nullptr;
+  int32_t *codes, *cont;
+  napi_value Cd = new_i32(env, (int64_t)B * kNvq, &codes), Ct = new_i32(env, B, &cont);
+  int rc = mb_local_frame(ctx, B, hidden, codes, cont);
+  if (rc) return throw_status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "codes", Cd);
+  napi_set_named_property(env, o, "cont", Ct);
+  return o;
+}
+
+// localSteps(h, B, hidden[B*768], maxStep) -> Float32Array[B*768]
+napi_value LocalSteps(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B, max_step;
+  if (!get_int(env, a.at(1), &B, "B")) return nullptr;
+  if (B < 0) return throw_range(env, "B must be >= 0");
+  float* hidden;
+  if (!get_array(env, a.at(2), napi_float32_array, (int64_t)B * kD, &hidden, nullptr, "hidden") ||
+      !get_int(env, a.at(3), &max_step, "maxStep"))
+    return nullptr;
+  float* out;
+  napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  int rc = mb_local_steps(ctx, B, hidden, max_step, out);
+  if (rc) return throw_status(env, ctx, rc);
+  return O;
+}
+
+// decodeFrames(h, B, nFrames, hidden Float32Array[B*768] (in/out), pos Int32Array[B] (in/out))
+//   -> {codes Int32Array[nFrames*B*16], cont Int32Array[nFrames*B]}
+napi_value DecodeFrames(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B, nf;
+  if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &nf, "nFrames")) return nullptr;
+  if (B < 0 || nf < 0) return throw_range(env, "B and nFrames must be >= 0");
+  float* hidden;
+  int32_t* pos;
+  if (!get_array(env, a.at(3), napi_float32_array, (int64_t)B * kD, &hidden, nullptr, "hidden") ||
+      !get_array(env, a.at(4), napi_int32_array, B, &pos, nullptr, "pos"))
+    return nullptr;
+  int32_t *codes, *cont;
+  napi_value Cd = new_i32(env, (int64_t)nf * B * kNvq, &codes);
+  napi_value Ct = new_i32(env, (int64_t)nf * B, &cont);
+  int rc = mb_decode_frames(ctx, B, nf, hidden, pos, codes, cont);
+  if (rc) return throw_status(env, ctx, rc);
+  napi_value o;
+  napi_create_object(env, &o);
+  napi_set_named_property(env, o, "codes", Cd);
+  napi_set_named_property(env, o, "cont", Ct);
+  return o;
+}
+
+napi_value LastError(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  napi_value s;
+  napi_create_string_utf8(env, mb_last_error(ctx), NAPI_AUTO_LENGTH, &s);
+  return s;
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  struct Fn {
+    const char* name;
+    napi_callback cb;
+  } fns[] = {
+      {"abiVersion", AbiVersion},
+      {"create", Create},
+      {"destroy", Destroy},
+      {"deviceBytes", DeviceBytes},
+      {"uploadTensor", UploadTensor},
+      {"cancel", Cancel},
+      {"setLocalHead", SetLocalHead},
+      {"ringReset", SeqListCall<mb_ring_reset>},
+      {"clearSeen", SeqListCall<mb_clear_seen>},
+      {"ringPoison", RingPoison},
+      {"readRing", ReadRing},
+      {"ringAppend", RingAppend},
+      {"ringWriteRows", RingWriteRows},
+      {"decodeAttention", DecodeAttention},
+      {"prefillAttention", PrefillAttention},
+      {"prefill", Prefill},
+      {"decodeStep", DecodeStep},
+      {"localFrame", LocalFrame},
+      {"localSteps", LocalSteps},
+      {"decodeFrames", DecodeFrames},
+      {"lastError", LastError},
+  };
+  for (const Fn& f : fns) {
+    napi_value v;
+    napi_create_function(env, f.name, NAPI_AUTO_LENGTH, f.cb, nullptr, &v);
+    napi_set_named_property(env, exports, f.name, v);
+  }
+  napi_value kv;
+  napi_create_object(env, &kv);
+  napi_set_named_property(env, kv, "F32", num(env, MB_KV_F32));
+  napi_set_named_property(env, kv, "BF16", num(env, MB_KV_BF16));
+  napi_set_named_property(env, exports, "KV", kv);
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

@@ -1,0 +1,28 @@
+import type { EngineWeights, LocalHeadSettings } from "./gpu";
+
+export class MultiVoiceEngine {
+  readonly maxVoices: number;
+  readonly capacity: number;
+  prefill(prompts: number[][][]): Promise<Float32Array[]>;
+  generate(nFrames: number): Promise<{ frames: number[][][]; stopped: boolean[] }>;
+  nextFrames(hidden: Float32Array[]): Promise<(number[] | null)[]>;
+  decodeSteps(rows: Int32Array[], positions: number[]): Promise<Float32Array[]>;
+  reset(voices?: number[]): void;
+  dispose(): void;
+}
+
+export type MultiVoiceOptions = {
+  localHead: LocalHeadSettings;
+  maxVoices: number;
+  capacity?: number;
+  maxRows?: number;
+  kvDtype?: "f32" | "bf16";
+  wrap?: boolean;
+  device?: number;
+};
+
+export function createMultiVoiceEngine(
+  tables: EngineWeights,
+  log: ((message: string) => void) | null,
+  options: MultiVoiceOptions,
+): Promise<MultiVoiceEngine>;

@@ -1,0 +1,87 @@
+/** Handle of one mb_ctx (rings, weights and activations on one GPU). */
+export type NativeHandle = { readonly __mbContext: unique symbol };
+
+export type NativeConfig = {
+  nLayers?: number;
+  vocab?: number;
+  capacity?: number;
+  maxSeqs?: number;
+  maxRows?: number;
+  kvDtype?: number;
+  wrap?: boolean | number;
+  device?: number;
+};
+
+/** An Error thrown by the addon: `code` names the MB_ERR_* status. */
+export interface NativeError extends Error {
+  code: string;
+  status: number;
+}
+
+export interface Native {
+  readonly KV: { F32: number; BF16: number };
+  abiVersion(): number;
+  create(config: NativeConfig): NativeHandle;
+  destroy(h: NativeHandle): void;
+  deviceBytes(h: NativeHandle): number;
+  uploadTensor(h: NativeHandle, name: string, data: Float32Array, dims: number[]): void;
+  cancel(h: NativeHandle, on?: boolean): void;
+  setLocalHead(h: NativeHandle, audioEnd: number, assistant: number, penalty: number): void;
+  ringReset(h: NativeHandle, seqIds: Int32Array | null): void;
+  clearSeen(h: NativeHandle, seqIds: Int32Array | null): void;
+  ringPoison(h: NativeHandle, layer: number, seq: number, nSlots: number, sentinel: number): void;
+  readRing(
+    h: NativeHandle,
+    layer: number,
+    seq: number,
+    slot0: number,
+    n: number,
+  ): { key: Float32Array; value: Float32Array; slotPos: Int32Array };
+  ringAppend(h: NativeHandle, layer: number, B: number, qkv: Float32Array, pos: Int32Array): Float32Array;
+  ringWriteRows(
+    h: NativeHandle,
+    layer: number,
+    B: number,
+    rowsMax: number,
+    qkv: Float32Array,
+    pos0: Int32Array,
+    nRows: Int32Array,
+  ): Float32Array;
+  decodeAttention(h: NativeHandle, layer: number, B: number, q: Float32Array, pos: Int32Array): Float32Array;
+  prefillAttention(
+    h: NativeHandle,
+    layer: number,
+    B: number,
+    rowsMax: number,
+    q: Float32Array,
+    pos0: Int32Array,
+    nRows: Int32Array,
+  ): Float32Array;
+  prefill(
+    h: NativeHandle,
+    B: number,
+    rowsMax: number,
+    ids: Int32Array,
+    nRows: Int32Array,
+    layerCount?: number,
+    allRows?: boolean,
+  ): Float32Array;
+  decodeStep(h: NativeHandle, B: number, rows17: Int32Array, pos: Int32Array): Float32Array;
+  localFrame(h: NativeHandle, B: number, hidden: Float32Array): { codes: Int32Array; cont: Int32Array };
+  localSteps(h: NativeHandle, B: number, hidden: Float32Array, maxStep: number): Float32Array;
+  decodeFrames(
+    h: NativeHandle,
+    B: number,
+    nFrames: number,
+    hidden: Float32Array,
+    pos: Int32Array,
+  ): { codes: Int32Array; cont: Int32Array };
+  lastError(h: NativeHandle): string;
+}
+
+export function loadNative(): Native;
+export function kvDtypeCode(native: Native, name?: "f32" | "bf16"): number;
+export const ROW_WIDTH: 17;
+export const N_VQ: 16;
+export const HIDDEN: 768;
+export const AUDIO_PAD_ID: 1024;

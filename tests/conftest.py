@@ -21,3 +21,21 @@ def say(msg: str) -> None:
 @pytest.fixture
 def rng():
     return np.random.default_rng(0x2F6E2B1)
+
+
+def write_sidecar(manifest_path: str, tensors) -> None:
+    """Write (name, float32 array) pairs as one raw little-endian f32 sidecar
+    plus its JSON manifest {"data", "tensors": [{"name", "dims", "offset"}]},
+    in the given order (the order anonymous projections are resolved by)."""
+    import json
+
+    data_path = manifest_path + ".data"
+    entries, off = [], 0
+    with open(data_path, "wb") as f:
+        for name, arr in tensors:
+            a = np.ascontiguousarray(arr, dtype="<f4")
+            f.write(a.tobytes())
+            entries.append({"name": name, "dims": list(a.shape), "offset": off})
+            off += a.nbytes
+    with open(manifest_path, "w") as f:
+        json.dump({"data": os.path.basename(data_path), "tensors": entries}, f)

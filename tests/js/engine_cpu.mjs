@@ -1,0 +1,85 @@
+// CPU-side checks of the JavaScript host: the addon loads and exports every
+// binding, the engine modules import, weight tables resolve anonymous
+// projections by shape and offset order (as prefill.ts:78-107 and
+// decodeWeights.ts:24-51 do), and argument errors surface as exceptions
+// before any device call.  Prints one JSON object.
+import { loadNative } from "../../mockbird_amd/engine/native.mjs";
+import { createGpuEngine, EngineNotImplemented, frameRowFrom } from "../../mockbird_amd/engine/gpu.mjs";
+import { resolveEngineTensors, tableOf } from "../../mockbird_amd/engine/weights.mjs";
+import { stageRows } from "../../mockbird_amd/engine/prefill.mjs";
+
+const out = {};
+const native = loadNative();
+out.exports = Object.keys(native).sort();
+out.abi = native.abiVersion();
+
+// two tiny tables: two global layers (vocab 16) with every projection but
+// layer 0's c_attn anonymous, and a local head whose matrices are all anonymous
+let offset = 0;
+let tag = 1;
+out.tags = {};
+const add = (map, name, dims) => {
+  const n = dims.reduce((a, b) => a * b, 1);
+  map.set(name, { name, dims, data: new Float32Array(n).fill(tag), offset });
+  out.tags[name] = tag;
+  tag += 1;
+  offset += n * 4;
+};
+const layer = (map, p, anon) => {
+  add(map, `${p}ln_1.weight`, [768]);
+  add(map, `${p}ln_1.bias`, [768]);
+  add(map, anon ? `onnx::MatMul_${tag}` : `${p}attn.c_attn.weight`, [768, 2304]);
+  add(map, `${p}attn.c_attn.bias`, [2304]);
+  add(map, `onnx::MatMul_${tag}`, [768, 768]);
+  add(map, `${p}attn.c_proj.bias`, [768]);
+  add(map, `${p}ln_2.weight`, [768]);
+  add(map, `${p}ln_2.bias`, [768]);
+  add(map, `onnx::MatMul_${tag}`, [768, 3072]);
+  add(map, `${p}mlp.fc_in.bias`, [3072]);
+  add(map, `onnx::MatMul_${tag}`, [3072, 768]);
+  add(map, `${p}mlp.fc_out.bias`, [768]);
+};
+const g = new Map();
+layer(g, "core.model.transformer.h.0.", false);
+layer(g, "core.model.transformer.h.1.", true);
+add(g, "core.model.transformer.ln_f.weight", [768]);
+add(g, "core.model.transformer.ln_f.bias", [768]);
+add(g, "core.model.transformer.wte.weight", [16, 768]);
+for (let k = 0; k < 16; k += 1) add(g, `core.model.audio_embeddings.${k}.weight`, [1024, 768]);
+const l = new Map();
+offset = 0;
+layer(l, "model.local_transformer.h.0.", true);
+add(l, "model.local_transformer.ln_f.weight", [768]);
+add(l, "model.local_transformer.ln_f.bias", [768]);
+add(l, "onnx::MatMul_text", [768, 16]);
+for (let k = 0; k < 16; k += 1) add(l, `onnx::MatMul_audio_${k}`, [768, 1024]);
+const global = tableOf(g);
+const local = tableOf(l);
+const r = resolveEngineTensors({ global, local });
+out.vocab = r.vocab;
+out.layers = r.layers;
+out.resolved = r.tensors.map((x) => [x.name, x.dims, x.data[0]]);
+
+// staging and frame rows
+out.staged = Array.from(stageRows([[6], [8, 1, 2, 3]]));
+out.frameRow = Array.from(frameRowFrom(9, [5, 6, 7]));
+
+// errors before any device call
+const errs = {};
+try {
+  native.create({ nLayers: 0 });
+} catch (e) {
+  errs.badConfig = [e.code, e.message];
+}
+try {
+  native.prefill({}, 1, 1, new Int32Array(17), Int32Array.of(1));
+} catch (e) {
+  errs.badHandle = [e.name, e.message];
+}
+try {
+  createGpuEngine();
+} catch (e) {
+  errs.notImplemented = [e instanceof EngineNotImplemented, e.name];
+}
+out.errors = errs;
+console.log(JSON.stringify(out));

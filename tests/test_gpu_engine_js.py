@@ -1,0 +1,112 @@
+"""The JavaScript host engine on the GPU, through the N-API addon: the
+reference runtime's frame loop on GpuTtsEngine and the batched
+MultiVoiceEngine, each checked against the oracle on the same seeded model.
+
+The weights travel as sidecar + manifest tables with the projections under
+anonymous names, so the engine must resolve them by shape and offset order
+as the reference's loaders do.  Bars: hidden states within 1e-4 (fp32 KV),
+greedy codes bit-exact (a difference is allowed only at an oracle near tie,
+after which that voice is no longer compared), the non-wrapping ring's
+range error and the decode-before-prefill error as the reference throws them.
+"""
+import json
+import os
+import shutil
+import subprocess
+
+import numpy as np
+import pytest
+
+from mockbird_amd import synth
+from oracle import oracle
+from conftest import say, write_sidecar
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+L, V, C, FRAMES = 2, 64, 128, 6
+NEAR_TIE = 2e-5
+
+
+def _tables(w, tmp):
+    glob, loc = [], []
+    n_anon = 0
+    for name, arr in w.items():
+        anon = arr.ndim == 2 and not name.endswith("wte.weight") and "audio_embeddings" not in name
+        key = f"onnx::MatMul_{n_anon}" if anon else name
+        n_anon += anon
+        (loc if name.startswith("model.") else glob).append((key, arr))
+    write_sidecar(os.path.join(tmp, "global.json"), glob)
+    write_sidecar(os.path.join(tmp, "local.json"), loc)
+
+
+def _oracle_frames(m, prompt, frames):
+    st = oracle.ModelState(m, 1, C)
+    h = st.prefill_all(0, prompt)[-1][None]
+    out = [(h[0].copy(), None, None)]
+    pos = prompt.shape[0]
+    for _ in range(frames):
+        oc, ocont, margins = st.local_frame(h)
+        if not ocont[0]:
+            out.append((None, None, margins[0]))
+            break
+        h = st.decode_step(synth.frame_row(oc[0])[None], [pos])
+        out.append((h[0].copy(), oc[0].copy(), margins[0]))
+        pos += 1
+    return out
+
+
+def _check_codes(js_frames, ref, label):
+    """Compare frame by frame; stop at an oracle near tie.  Returns frames compared."""
+    n = 0
+    for f, frame in enumerate(js_frames):
+        _, oc, margins = ref[f + 1]
+        assert oc is not None, f"{label}: the oracle stopped at frame {f}, the engine did not"
+        diff = [c for c in range(16) if frame[c] != oc[c]]
+        if diff:
+            assert margins[diff[0] + 1] < NEAR_TIE, f"{label} frame {f}: {frame} != {list(oc)}"
+            say(f"  {label}: near tie at frame {f} channel {diff[0]}")
+            return n
+        n += 1
+    return n
+
+
+def test_engine_runtime_loop_and_multivoice_match_oracle(tmp_path):
+    if shutil.which("node") is None:
+        pytest.fail("node is not installed")
+    w = synth.model_weights(n_layers=L, vocab=V, seed=11, bias_std=0.02, ln_std=0.1)
+    w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]  # never stops
+    prompts = [synth.prompt(40 + b, n_frames=4 + 5 * b, n_text=6 + b, vocab=V) for b in range(3)]
+    _tables(w, str(tmp_path))
+    spec = {"layers": L, "maxSlots": C, "frames": FRAMES, "prompts": [p.tolist() for p in prompts]}
+    (tmp_path / "case.json").write_text(json.dumps(spec))
+    say("JS engine: single-voice runtime loop + 3-voice MultiVoiceEngine")
+    r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "engine_run.mjs"), str(tmp_path)],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-4000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert any("warmup" in m for m in out["log"])
+    m = oracle.Model(w, n_layers=L, vocab=V)
+
+    s = out["single"]
+    ref = _oracle_frames(m, prompts[0], FRAMES)
+    assert np.abs(np.array(s["prefillHidden"], np.float32) - ref[0][0]).max() < 1e-4
+    st = oracle.ModelState(m, 1, C)
+    st.prefill_all(0, prompts[0])
+    k_ref = st.K[0, 0][:4]
+    assert np.abs(np.array(s["layer0Key"], np.float32).reshape(4, 768) - k_ref).max() < 1e-4
+    n = _check_codes(s["frames"], ref, "single")
+    for f in range(n):
+        assert np.abs(np.array(s["hiddens"][f], np.float32) - ref[f + 1][0]).max() < 1e-4, f
+    assert len(s["frames"]) == FRAMES and s["position"] == prompts[0].shape[0] + FRAMES
+    assert s["rangeError"][0] == "MB_ERR_RANGE" and "exceeds the KV ring" in s["rangeError"][1]
+    assert s["beforePrefill"] == "decodeStep before prefill"
+    say(f"  single voice: {n} of {FRAMES} frames bit-exact")
+
+    mv = out["multi"]
+    for b, p in enumerate(prompts):
+        ref = _oracle_frames(m, p, FRAMES)
+        assert np.abs(np.array(mv["prefillHidden"][b], np.float32) - ref[0][0]).max() < 1e-4, b
+        assert not mv["stopped"][b]
+        n = _check_codes(mv["frames"][b], ref, f"voice {b}")
+        say(f"  multi-voice {b}: {n} of {FRAMES} frames bit-exact")
