@@ -11,10 +11,13 @@ turn (as a 12-layer decode does), so the 4.8 GB of KV never fits the 256 MB
 last-level cache and the GB/s are HBM figures.  Every sequence advances one
 position after each full pass over the twelve layers.
 
-value = algorithmic bytes of the step (K/V window read + q/k/v read + roped q,
-K, V write + output write) / wall time, inputs already resident in HBM.
-roofline = the decode-attention launch alone, timed with HIP events on the
-stream it runs on.  cpu_baseline = the C oracle (OpenMP) on a bounded sample
+A step is one fused launch (k_attn_unit with the append): value = its
+algorithmic bytes (live K/V window read once, q | k | v read, new K/V row and
+the output written) / the launch's average duration, from HIP events around
+the back-to-back timed launches on the stream they run on, inputs resident in
+HBM.  The roofline object is the same launch; `traffic` comes from the
+committed rocprofv3 PMC summary.  The two-launch path (append, then
+attention) is timed beside it.  cpu_baseline = the C oracle (OpenMP) on a bounded sample
 of the same workload on this host's cores.
 """
 from __future__ import annotations
@@ -68,7 +71,21 @@ def append_bytes(B, e):
     return B * (QKV * 4 + D * 4 + 2 * D * e)
 
 
+def fused_bytes(pos, C, e):
+    """Algorithmic bytes of one fused append + attention launch: the fused
+    q | k | v row read (fp32), the window's older live K and V rows read once,
+    the new K and V row written, the output written (fp32)."""
+    valid = np.minimum(pos.astype(np.int64) + 1, C)
+    return int(valid.sum()) * D * 2 * e + len(pos) * (QKV + D) * 4
+
+
 def run_c1(args, kv_name):
+    """One step = one layer's ring append + decode attention for all 64
+    sequences, as one fused launch (mb_append_attend_dev); twelve layer rings
+    are stepped in turn and every sequence advances one position after each
+    pass over the twelve.  The same steps through the two separate entry
+    points (mb_ring_append_dev, then mb_decode_attention_dev) are timed beside
+    it on a shorter run."""
     import torch
 
     import mockbird_amd as mb
@@ -93,7 +110,8 @@ def run_c1(args, kv_name):
             p0 = torch.from_numpy((start + c0).astype(np.int32)).to(dev)
             ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
     torch.cuda.synchronize()
-    total = args.warmup + args.steps
+    unfused_steps = min(args.steps, 240)
+    total = args.warmup + args.steps + unfused_steps
     tokens = total // L + 2
     pos_all = torch.from_numpy((pos0[None, :] + np.arange(tokens)[:, None]).astype(np.int32)).to(dev)
     qkv_l = [torch.randn((B, QKV), generator=tg, device=dev) for _ in range(L)]
@@ -101,47 +119,51 @@ def run_c1(args, kv_name):
     out = torch.empty((B, D), device=dev)
     max_pos = int(pos0.max()) + tokens
 
-    def step(s, ev=None):
+    def step(s):
+        layer, tok = s % L, s // L
+        ctx.append_attend_dev(layer, B, qkv_l[layer].data_ptr(), pos_all[tok].data_ptr(), max_pos,
+                              out.data_ptr())
+
+    def step_unfused(s):
         layer, tok = s % L, s // L
         p = pos_all[tok]
         ctx.ring_append_dev(layer, B, qkv_l[layer].data_ptr(), p.data_ptr(), q.data_ptr())
-        if ev is not None:
-            ev[0].record(stream)
         ctx.decode_attention_dev(layer, B, q.data_ptr(), p.data_ptr(), max_pos, out.data_ptr())
-        if ev is not None:
-            ev[1].record(stream)
+
+    def timed(fn, first, n):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for i in range(n):
+            fn(first + i)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1)
 
     for s in range(args.warmup):
         step(s)
-    torch.cuda.synchronize()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    t0.record(stream)
-    for i in range(args.steps):
-        step(args.warmup + i, evs[i])
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = t0.elapsed_time(t1)
-    attn_ms = np.array([a.elapsed_time(b) for a, b in evs])
-    step_bytes = 0
-    attn_total = 0
-    for i in range(args.steps):
-        tok = (args.warmup + i) // L
-        p = pos0 + tok
-        ab = attn_bytes(p, C, e)
-        attn_total += ab
-        step_bytes += ab + append_bytes(B, e)
+    ms_total = timed(step, args.warmup, args.steps)
+    ms_unfused = timed(step_unfused, args.warmup + args.steps, unfused_steps)
+
+    def mean_bytes(fn, first, n):
+        tot = 0
+        for i in range(n):
+            tot += fn(pos0 + (first + i) // L)
+        return tot / n
+
+    b_fused = mean_bytes(lambda p: fused_bytes(p, C, e), args.warmup, args.steps)
+    b_unfused = mean_bytes(lambda p: attn_bytes(p, C, e) + append_bytes(B, e),
+                           args.warmup + args.steps, unfused_steps)
     ms_step = ms_total / args.steps
     res = {
         "kv": kv_name,
         "ms_per_step": ms_step,
-        "gbs": step_bytes / args.steps / (ms_step * 1e-3) / 1e9,
-        "attn_us": float(attn_ms.mean() * 1e3),
-        "attn_bytes": attn_total / args.steps,
-        "attn_gbs": attn_total / args.steps / (attn_ms.mean() * 1e-3) / 1e9,
-        "mean_valid": float(np.minimum(pos0 + args.warmup // L + args.steps // (2 * L) + 1, C).mean()),
+        "bytes_per_step": b_fused,
+        "gbs": b_fused / (ms_step * 1e-3) / 1e9,
+        "unfused_ms_per_step": ms_unfused / unfused_steps,
+        "unfused_gbs": b_unfused / (ms_unfused / unfused_steps * 1e-3) / 1e9,
+        "mean_valid": float(np.minimum(pos0 + (args.warmup + args.steps // 2) // L + 1, C).mean()),
     }
     ctx.close()
     return res
@@ -287,11 +309,12 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
 
 def cpu_baseline_c1(seconds=12.0):
     """The oracle (double-precision C, OpenMP over sequences) on a sample of the
-    c1 workload: 8 of the 64 sequences, fp32 rings, append + attention steps,
-    repeated until `seconds` have passed."""
+    c1 workload: one sequence per host thread (at most the 64), fp32 rings,
+    append + attention steps, repeated until `seconds` have passed."""
     from oracle import oracle
 
-    B, C = 8, 2048
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    B, C = max(1, min(64, threads)), 2048
     pos = c1_positions(64)[:B]
     g = np.random.default_rng(5)
     ring = oracle.Ring(B, C)
@@ -308,14 +331,13 @@ def cpu_baseline_c1(seconds=12.0):
     while time.perf_counter() - t0 < seconds:
         q = ring.append(qkv, p)
         ring.attend(q, p)
-        nbytes += attn_bytes(p, C, 4) + append_bytes(B, 4)
+        nbytes += fused_bytes(p, C, 4)
         p = p + 1
         steps += 1
     dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} append+attention steps of 8 of the 64 sequences (fp32 rings, "
-                      f"C=2048), {dt:.1f} s"}
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": B, "kind": "port",
+            "sample": f"{steps} append+attention steps of {B} of the 64 sequences (fp32 rings, "
+                      f"C=2048, OpenMP over sequences), {dt:.1f} s"}
 
 
 def main():
@@ -385,21 +407,23 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(bf16["attn_gbs"], 1),
+            "achieved": round(bf16["gbs"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(bf16["attn_gbs"] / HBM_PEAK_GBS, 4),
+            "frac": round(bf16["gbs"] / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(),
-            "kernel": "decode attention (k_attn_split + k_attn_combine)",
-            "avg_us": round(bf16["attn_us"], 2),
-            "bytes_per_launch": int(bf16["attn_bytes"]),
+            "kernel": "k_attn_unit (ring append fused into decode attention), one launch per step",
+            "avg_us": round(bf16["ms_per_step"] * 1e3, 2),
+            "bytes_per_launch": int(bf16["bytes_per_step"]),
         },
         "cpu_baseline": cpu,
+        "two_launch_bf16": {"ms_per_step": round(bf16["unfused_ms_per_step"], 5),
+                            "gbs": round(bf16["unfused_gbs"], 1)},
         "f32_kv": None if f32 is None else {
             "value": round(f32["gbs"], 2), "unit": "GB/s",
             "ms_per_step": round(f32["ms_per_step"], 5),
-            "attn_gbs": round(f32["attn_gbs"], 1), "attn_us": round(f32["attn_us"], 2),
-            "frac": round(f32["attn_gbs"] / HBM_PEAK_GBS, 4)},
+            "frac": round(f32["gbs"] / HBM_PEAK_GBS, 4),
+            "two_launch_gbs": round(f32["unfused_gbs"], 1)},
         "hbm_copy": copy,
         "prefill_attention": c2,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},

@@ -151,6 +151,16 @@ int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float*
 int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int32_t* pos,
                         float* out);
 
+/* mb_ring_append followed by mb_decode_attention in one launch: the row of
+ * sequence b at pos[b] is appended (K = rope(k), V = v at slot pos mod C, the
+ * slot records pos) and its roped q attends the ring including that row;
+ * out[b][768] receives the attention output and q_out[b][768] (may be NULL)
+ * the roped q.  Results equal the two calls in sequence.  Replaces the
+ * ROPE_SPLIT_RING + ATTEND_RING pair of one decode layer
+ * (kernels-decode.ts:216-327, dispatched decode.ts:527-552). */
+int mb_append_attend(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_t* pos,
+                     float* q_out, float* out);
+
 /* Causal prefill attention: q [B][rows_max][768] (roped) for rows r < n_rows[b]
  * at positions pos0[b] + r, each attending the live slots of `layer` whose
  * position is <= its own; out [B][rows_max][768].  Replaces ATTENTION_SCORES /
@@ -171,6 +181,9 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
                             const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride);
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
                              int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out);
+int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
+                         int64_t qkv_stride, const int32_t* pos, int32_t max_pos, float* q_out,
+                         int64_t q_stride, float* out, int64_t out_stride);
 
 /* Kernel-level projection on device pointers (row a7):
  *   C[M][N] = epi(A[M][K] * W[K][N] + bias[N])

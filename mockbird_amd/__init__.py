@@ -31,7 +31,8 @@ EXPORTS = (
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
-    "mb_linear_dev", "mb_decode_frames_dev", "mb_decode_frames",
+    "mb_linear_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
+    "mb_append_attend_dev",
 )
 
 
@@ -110,6 +111,9 @@ def load():
                            C.c_int64, C.c_int], C.c_int),
         "mb_decode_frames_dev": ([_vp, C.c_int, C.c_int, _vp, _vp, _i32, _vp, _vp], C.c_int),
         "mb_decode_frames": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+        "mb_append_attend": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
+        "mb_append_attend_dev": ([_vp, C.c_int, C.c_int, _vp, C.c_int, _i64, _vp, _i32, _vp, _i64,
+                                  _vp, _i64], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -235,6 +239,16 @@ class Context:
                                                 pos.ctypes.data, out.ctypes.data))
         return out
 
+    def append_attend(self, layer: int, qkv: np.ndarray, pos, want_q: bool = True):
+        """Fused append + decode attention: returns (roped q or None, out)."""
+        qkv, pos = _f32c(qkv), _i32c(pos)
+        B = qkv.shape[0]
+        q = np.zeros((B, D), np.float32) if want_q else None
+        out = np.zeros((B, D), np.float32)
+        self.check(self.lib.mb_append_attend(self.h, layer, B, qkv.ctypes.data, pos.ctypes.data,
+                                             _ptr(q), out.ctypes.data))
+        return q, out
+
     def prefill_attention(self, layer: int, q: np.ndarray, pos0, n_rows) -> np.ndarray:
         q, pos0, n_rows = _f32c(q), _i32c(pos0), _i32c(n_rows)
         B, R = q.shape[0], q.shape[1]
@@ -259,6 +273,12 @@ class Context:
                              out_stride=D):
         self.check(self.lib.mb_decode_attention_dev(self.h, layer, B, q_ptr, q_stride, pos_ptr,
                                                     max_pos, out_ptr, out_stride))
+
+    def append_attend_dev(self, layer, B, qkv_ptr, pos_ptr, max_pos, out_ptr, q_ptr=None,
+                          qkv_dtype=MB_DT_F32, qkv_stride=QKV, q_stride=D, out_stride=D):
+        self.check(self.lib.mb_append_attend_dev(self.h, layer, B, qkv_ptr, qkv_dtype, qkv_stride,
+                                                 pos_ptr, max_pos, q_ptr, q_stride, out_ptr,
+                                                 out_stride))
 
     def prefill_attention_dev(self, layer, B, rows_max, q_ptr, pos0_ptr, n_ptr, out_ptr,
                               q_dtype=MB_DT_F32):

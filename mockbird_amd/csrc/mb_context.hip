@@ -378,6 +378,28 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
                      (int64_t)max_pos + 1, out, dense_rows(out_stride, 1));
 }
 
+int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
+                         int64_t qkv_stride, const int32_t* pos, int32_t max_pos, float* q_out,
+                         int64_t q_stride, float* out, int64_t out_stride) {
+  int rc = check_common(ctx, layer, B);
+  if (rc) return rc;
+  if (qkv_dtype != MB_DT_F32 && qkv_dtype != MB_DT_BF16)
+    return fail(ctx, MB_ERR_ARG, "unknown dtype");
+  if (qkv_stride < QKV || out_stride < D || (q_out && q_stride < D))
+    return fail(ctx, MB_ERR_ARG, "row stride too small");
+  if (max_pos < 0) return fail(ctx, MB_ERR_ARG, "max_pos %d is negative", max_pos);
+  if (!ctx->cfg.wrap && max_pos >= ctx->cfg.capacity)
+    return fail(ctx, MB_ERR_RANGE,
+                "decode position %d exceeds the KV ring (%d slots); it must be sized "
+                "prefill_rows + max_new_frames",
+                max_pos, ctx->cfg.capacity);
+  if (B == 0) return MB_OK;
+  if (!qkv || !pos || !out) return fail(ctx, MB_ERR_ARG, "null pointer");
+  return launch_append_attn(ctx, global_ring(ctx, layer), B, qkv, qkv_dtype,
+                            dense_rows(qkv_stride, 1), pos, (int64_t)max_pos + 1, q_out,
+                            dense_rows(q_stride, 1), out, dense_rows(out_stride, 1));
+}
+
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
                              int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out) {
   int rc = check_common(ctx, layer, B);
@@ -475,6 +497,33 @@ int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int
   rc = launch_attn(ctx, global_ring(ctx, layer), B, 1, d_q, dense_rows(D, 1), d_pos, nullptr,
                    (int64_t)max_pos + 1, d_out, dense_rows(D, 1));
   if (rc) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(out, d_out, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_append_attend(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_t* pos,
+                     float* q_out, float* out) {
+  int rc = check_common(ctx, layer, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!qkv || !pos || !out) return fail(ctx, MB_ERR_ARG, "null pointer");
+  rc = check_positions(ctx, B, pos, nullptr, 1);
+  if (rc) return rc;
+  int32_t max_pos = 0;
+  for (int b = 0; b < B; b++) max_pos = pos[b] > max_pos ? pos[b] : max_pos;
+  float* d_qkv = (float*)scratch(ctx, "qkv", (size_t)B * QKV * 4);
+  float* d_q = (float*)scratch(ctx, "q", (size_t)B * D * 4);
+  float* d_out = (float*)scratch(ctx, "out", (size_t)B * D * 4);
+  int32_t* d_pos = (int32_t*)scratch(ctx, "pos", (size_t)B * 8);
+  if (!d_qkv || !d_q || !d_out || !d_pos) return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_qkv, qkv, (size_t)B * QKV * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_pos, pos, (size_t)B * 4, hipMemcpyHostToDevice, ctx->stream));
+  rc = launch_append_attn(ctx, global_ring(ctx, layer), B, d_qkv, MB_DT_F32, dense_rows(QKV, 1),
+                          d_pos, (int64_t)max_pos + 1, q_out ? d_q : nullptr, dense_rows(D, 1),
+                          d_out, dense_rows(D, 1));
+  if (rc) return rc;
+  if (q_out) MB_HIP(ctx, hipMemcpyAsync(q_out, d_q, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipMemcpyAsync(out, d_out, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;

@@ -200,6 +200,11 @@ int launch_ring_write(mb_ctx* ctx, const RingView& ring, int B, int rows_max, co
 int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
                 const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
                 float* out, const Rows& out_rows);
+// Ring append fused into the decode attention: one row per sequence, qkv
+// [B] fused rows at pos[b]; q_out (roped q) may be null.
+int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv, int qkv_dtype,
+                       const Rows& qkv_rows, const int32_t* pos, int64_t max_valid, float* q_out,
+                       const Rows& qo_rows, float* out, const Rows& out_rows);
 int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
                              const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
                              const int32_t* n_rows, float* out, const Rows& out_rows);

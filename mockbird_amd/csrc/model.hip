@@ -129,14 +129,17 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
     qkv_rows = dense_rows(QKV, 1);
     q_rows = dense_rows(D, 1);
   }
-  if ((rc = launch_ring_write(ctx, ring, B, rows_max, a.qkv, MB_DT_F32, qkv_rows, pos0, n_rows,
-                              a.q, MB_DT_F32, q_rows)))
-    return rc;
-  if (prefill)
+  if (prefill) {
+    if ((rc = launch_ring_write(ctx, ring, B, rows_max, a.qkv, MB_DT_F32, qkv_rows, pos0, n_rows,
+                                a.q, MB_DT_F32, q_rows)))
+      return rc;
     rc = launch_prefill_attention(ctx, ring, B, rows_max, a.q, MB_DT_F32, q_rows, pos0, n_rows,
                                   a.att, q_rows);
-  else
-    rc = launch_attn(ctx, ring, B, 1, a.q, q_rows, pos0, nullptr, max_valid, a.att, q_rows);
+  } else {
+    // one launch appends this row's K/V and attends the ring including it
+    rc = launch_append_attn(ctx, ring, B, a.qkv, MB_DT_F32, qkv_rows, pos0, max_valid, nullptr,
+                            Rows{}, a.att, q_rows);
+  }
   if (rc) return rc;
   if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, w.proj_w, D, D, w.proj_b, a.x, D, (int)M))) return rc;
   if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln2_w, w.ln2_b, a.norm, D))) return rc;

@@ -6,6 +6,8 @@
 // so one (sequence, head) window is one contiguous run of C * 64 elements and
 // a wave streams it with 16-byte loads; the reference's [slot][head*64+dim]
 // order (prefill.ts:55-56) is produced only on read-back.
+#include <algorithm>
+
 #include "mb_internal.h"
 #include "kv_types.h"
 
@@ -215,50 +217,142 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* acc, floa
   m = mn;
 }
 
-// One wave per (query, head, split).  A query is row r of sequence b at
-// position cur = pos0[b] + r; it attends the slots of its ring whose stored
-// position p satisfies 0 <= cur - p < C (kernels-decode.ts:608-611), which
-// are all inside physical slots [0, min(cur + 1, C)).  Split `s` covers
-// slots [s * split_len, (s + 1) * split_len) of that range.
+// 16-byte streaming load (global_load_dwordx4 ... nt): the K/V window is read
+// once per launch, and the non-temporal hint lets the caches stream it.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const char* p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// VD (4 or 8) consecutive elements of an fp32 or bf16 row starting at `off`.
+template <bool IN_BF16, int VD>
+__device__ __forceinline__ void load_n(const void* base, int64_t off, float* out) {
+  if (VD == 8) {
+    load8<IN_BF16>(base, off, out);
+  } else if (IN_BF16) {
+    const uint2 v = *(const uint2*)((const uint16_t*)base + off);
+    out[0] = bf16_lo(v.x); out[1] = bf16_hi(v.x); out[2] = bf16_lo(v.y); out[3] = bf16_hi(v.y);
+  } else {
+    const float4 v = *(const float4*)((const float*)base + off);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  }
+}
+
+// 16 bytes of a ring row: 8 bf16 (round to nearest even) or 4 fp32 values.
+template <bool KV_BF16>
+__device__ __forceinline__ uint4 pack16(const float* x) {
+  if (KV_BF16)
+    return make_uint4(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]), pack_bf16(x[4], x[5]),
+                      pack_bf16(x[6], x[7]));
+  return make_uint4(__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]),
+                    __float_as_uint(x[3]));
+}
+
+// One block per (query, head): the live window [0, min(cur + 1, C)) of the
+// query at position cur = pos0[b] + r is cut into `nw` equal ranges (whole
+// load batches), one per wave; the waves fold their online-softmax partials
+// through LDS and wave 0 writes the normalised row.  A query attends the
+// slots whose stored position p satisfies 0 <= cur - p < C
+// (kernels-decode.ts:608-611); they all lie inside physical slots
+// [0, min(cur + 1, C)).
 //
 // Lane layout: LR = 64 / VD lanes hold one 64-dim row (VD dims each, one
 // 16-byte load), so a wave covers G = VD consecutive slots -- 1 KB of one
 // (sequence, head) run -- per load instruction; U loads of K and V are issued
 // before any is used.  Scores are reduced across the LR lanes with DPP; each
 // lane group keeps its own online-softmax state (max, sum, VD accumulators)
-// and the G groups are merged with cross-row shuffles at the end.
+// and the G groups merge with cross-row shuffles at the end of the range.
 //
 // Liveness: for each tile of 256 slots every lane loads the stored positions
 // of 4 slots and the wave turns them into four 64-bit ballot masks, so the
 // per-slot test in the hot loop is a bit lookup, not a memory access.
 //
-// With one split the normalised row is written directly; with several each
-// wave writes a partial (acc[64], max, sum) for k_attn_combine.
-template <bool KV_BF16, int U>
-__global__ __launch_bounds__(256) void k_attn_split(
-    const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
-    const int32_t* __restrict__ n_rows, int rows, const void* __restrict__ ring_k,
-    const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, int split_len, int nsplit, float* __restrict__ part,
+// No barrier is skipped: a block whose query row is beyond n_rows returns as
+// a whole before the only __syncthreads.
+//
+// With APPEND the kernel also does the ring append of ROPE_SPLIT_RING
+// (kernels-decode.ts:216-241) for its (sequence, head): `q` is then the fused
+// q | k | v row (IN_BF16: bf16 elements), q is roped in registers (and stored
+// to q_out when given), and the wave whose range holds slot cur mod C (cur in
+// a non-wrapping ring) ropes k, stores K and V there -- the head-0 block also
+// records the slot's position -- and feeds the new row to its own batch from
+// registers, so the attention sees it without reading it back.  Rows 1 only.
+template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16>
+__global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
+    const void* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, int rows, void* __restrict__ ring_k,
+    void* __restrict__ ring_v, int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C,
+    int wrap, const float2* __restrict__ rope_tab, float* __restrict__ q_out, Rows qo_rows,
     float* __restrict__ out, Rows out_rows) {
   constexpr int VD = KV_BF16 ? 8 : 4;
   constexpr int LR = 64 / VD;
   constexpr int G = VD;
+  constexpr int GU = G * U;
   constexpr int TILE = 256;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int head = blockIdx.y * 4 + wave;
-  const int qidx = blockIdx.x / nsplit, split = blockIdx.x % nsplit;
+  constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
+  __shared__ float fold[MAXNW][PART];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int qidx = blockIdx.x / H, head = blockIdx.x % H;
   const int b = qidx / rows, r = qidx % rows;
-  if (n_rows && r >= n_rows[b]) return;  // uniform per wave; no barriers in this kernel
+  if (n_rows && r >= n_rows[b]) return;  // uniform per block
   const int g = lane / LR, sub = lane % LR;
   const int64_t cur = (int64_t)pos0[b] + r;
   const int nvalid = cur < 0 ? 0 : (int)(cur + 1 < C ? cur + 1 : C);
-  const int s0 = split * split_len;
-  const int s1 = min(s0 + split_len, nvalid);
+  int per = (nvalid + nw - 1) / nw;
+  per = (per + GU - 1) / GU * GU;
+  const int s0 = wave * per;
+  const int s1 = min(s0 + per, nvalid);
+
+  const int64_t kv_off = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
+  const char* kbase = (const char*)ring_k + kv_off * (KV_BF16 ? 2 : 4);
+  const char* vbase = (const char*)ring_v + kv_off * (KV_BF16 ? 2 : 4);
+  const int32_t* sp = slot_pos + (int64_t)b * C;
 
   float qv[VD];
-  {
-    const float* qp = q + row_at(q_rows, b, r) + head * HD + sub * VD;
+  // the appended row: its slot, whether this wave's range holds it, and its
+  // K and V as stored (rounded to the ring's type)
+  int slot_new = -1;
+  bool owner = false;
+  uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+  if (APPEND) {
+    const int64_t roff = row_at(q_rows, b, r) + head * HD + sub * VD;
+    float qi[VD], qo[VD];
+    load_n<IN_BF16, VD>(q, roff, qi);
+    const bool have = cur >= 0 && cur <= INT32_MAX && (wrap || cur < C);
+    const int32_t pos = (int32_t)(have ? cur : 0);
+    float cs[VD / 2], sn[VD / 2];
+#pragma unroll
+    for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+#pragma unroll
+    for (int j = 0; j < VD / 2; j++) rope_pair(qi[2 * j], qi[2 * j + 1], cs[j], sn[j], qo[2 * j], qo[2 * j + 1]);
+    if (q_out && wave == 0 && g == 0) {
+      float* op = q_out + row_at(qo_rows, b, r) + head * HD + sub * VD;
+#pragma unroll
+      for (int i = 0; i < VD; i += 4) *(float4*)(op + i) = make_float4(qo[i], qo[i + 1], qo[i + 2], qo[i + 3]);
+    }
+#pragma unroll
+    for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
+    if (have) {
+      slot_new = wrap ? (int)(cur % C) : (int)cur;
+      owner = (slot_new >= s0 && slot_new < s1);
+    }
+    if (owner) {
+      float ki[VD], vi[VD], ko[VD];
+      load_n<IN_BF16, VD>(q, roff + D, ki);
+      load_n<IN_BF16, VD>(q, roff + 2 * D, vi);
+#pragma unroll
+      for (int j = 0; j < VD / 2; j++) rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
+      knew = pack16<KV_BF16>(ko);
+      vnew = pack16<KV_BF16>(vi);
+      if (g == 0) {
+        *(uint4*)((char*)ring_k + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = knew;
+        *(uint4*)((char*)ring_v + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = vnew;
+        if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
+      }
+    }
+  } else {
+    const float* qp = (const float*)q + row_at(q_rows, b, r) + head * HD + sub * VD;
 #pragma unroll
     for (int i = 0; i < VD; i += 4) {
       const float4 t = *(const float4*)(qp + i);
@@ -266,12 +360,6 @@ __global__ __launch_bounds__(256) void k_attn_split(
       qv[i] = t.x * 0.125f; qv[i + 1] = t.y * 0.125f; qv[i + 2] = t.z * 0.125f; qv[i + 3] = t.w * 0.125f;
     }
   }
-  const char* kbase = (const char*)ring_k +
-      ((int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD) * (KV_BF16 ? 2 : 4);
-  const char* vbase = (const char*)ring_v +
-      ((int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD) * (KV_BF16 ? 2 : 4);
-  constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
-  const int32_t* sp = slot_pos + (int64_t)b * C;
 
   float m = -INFINITY, l = 0.f, acc[VD];
 #pragma unroll
@@ -287,7 +375,7 @@ __global__ __launch_bounds__(256) void k_attn_split(
       const int64_t dlt = cur - p;
       live[c] = __ballot(p >= 0 && dlt >= 0 && dlt < C);
     }
-    for (int base = t0; base < t1; base += G * U) {
+    for (int base = t0; base < t1; base += GU) {
       uint4 kr[U], vr[U];
       bool ok[U];
 #pragma unroll
@@ -296,8 +384,21 @@ __global__ __launch_bounds__(256) void k_attn_split(
         const int i = slot - t0;
         ok[u] = slot < t1 && ((live[i & 3] >> (i >> 2)) & 1ull);
         const int sl = slot < t1 ? slot : t0;
-        kr[u] = *(const uint4*)(kbase + (int64_t)sl * ROWB);
-        vr[u] = *(const uint4*)(vbase + (int64_t)sl * ROWB);
+        kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
+        vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
+      }
+      // the new row joins the one batch (of the one tile) that covers its slot:
+      // a batch may reach past the tile end when GU does not divide TILE, and
+      // the slots beyond t1 belong to the next tile
+      if (APPEND && owner && slot_new >= base && slot_new < min(base + GU, t1)) {  // wave-uniform
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+          if (base + u * G + g == slot_new) {
+            kr[u] = knew;
+            vr[u] = vnew;
+            ok[u] = true;
+          }
+        }
       }
       float sc[U];
       float mx = m;
@@ -340,41 +441,20 @@ __global__ __launch_bounds__(256) void k_attn_split(
     for (int i = 0; i < VD; i++) ao[i] = __shfl_xor(acc[i], off);
     merge_state<VD>(m, l, acc, mo, lo, ao);
   }
-  if (g != 0) return;
-  if (nsplit == 1) {
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    float* op = out + row_at(out_rows, b, r) + head * HD + sub * VD;
+  if (g == 0) {
 #pragma unroll
-    for (int i = 0; i < VD; i += 4)
-      *(float4*)(op + i) = make_float4(acc[i] * inv, acc[i + 1] * inv, acc[i + 2] * inv, acc[i + 3] * inv);
-  } else {
-    float* pp = part + (((int64_t)qidx * H + head) * nsplit + split) * PART;
-#pragma unroll
-    for (int i = 0; i < VD; i += 4)
-      *(float4*)(pp + sub * VD + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+    for (int i = 0; i < VD; i++) fold[wave][sub * VD + i] = acc[i];
     if (sub == 0) {
-      pp[64] = m;
-      pp[65] = l;
+      fold[wave][64] = m;
+      fold[wave][65] = l;
     }
   }
-}
-
-// Fold the split partials of one (query, head) -- one wave, lane = dim.
-// Lane s first holds split s's (max, sum) (nsplit <= 64), the wave forms the
-// global max and each split's weight, then every lane sums its dim over the
-// splits with independent loads.
-__global__ __launch_bounds__(256) void k_attn_combine(
-    const float* __restrict__ part, int nsplit, const int32_t* __restrict__ n_rows, int rows,
-    int64_t units, float* __restrict__ out, Rows out_rows) {
-  const int lane = threadIdx.x & 63;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (query, head)
-  if (unit >= units) return;
-  const int qidx = (int)(unit / H), head = (int)(unit % H);
-  const int b = qidx / rows, r = qidx % rows;
-  if (n_rows && r >= n_rows[b]) return;
-  const float* pp = part + unit * nsplit * PART;
-  const float ms = lane < nsplit ? pp[lane * PART + 64] : -INFINITY;
-  const float ls = lane < nsplit ? pp[lane * PART + 65] : 0.f;
+  __syncthreads();
+  if (wave != 0) return;
+  // fold the waves: lane w first holds wave w's (max, sum), then every lane
+  // (= dim) sums its dim over the waves
+  const float ms = lane < nw ? fold[lane][64] : -INFINITY;
+  const float ls = lane < nw ? fold[lane][65] : 0.f;
   float M = ms;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
@@ -382,70 +462,59 @@ __global__ __launch_bounds__(256) void k_attn_combine(
   float L = ls * w;
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
-  float acc = 0.f;
-  for (int s = 0; s < nsplit; s++) acc = fmaf(__shfl(w, s), pp[s * PART + lane], acc);
-  out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? acc / L : 0.f;
+  float o = 0.f;
+  for (int s = 0; s < nw; s++) o = fmaf(__shfl(w, s), fold[s][lane], o);
+  out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? o / L : 0.f;
 }
 
-// Launch the split attention for nq = B * rows queries.  The split length is
-// chosen so that about `target` waves cover the chip (256 CUs) while each
-// split stays a whole number of U-deep load batches and there are at most 64
-// splits; MB_ATTN_WAVES and MB_ATTN_U override the defaults (tuning sweeps).
-template <bool BF16, int U>
-static void launch_split(mb_ctx* ctx, dim3 grid, const float* q, const Rows& q_rows,
-                         const int32_t* pos0, const int32_t* n_rows, int rows,
-                         const RingView& ring, int split_len, int nsplit, float* part, float* out,
-                         const Rows& out_rows) {
-  hipLaunchKernelGGL((k_attn_split<BF16, U>), grid, dim3(256), 0, ctx->stream, q, q_rows, pos0,
-                     n_rows, rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, split_len,
-                     nsplit, part, out, out_rows);
-}
-
-static int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
-
-int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
-                const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
-                float* out, const Rows& out_rows) {
-  static const int64_t target = env_int("MB_ATTN_WAVES", 8192);
-  static const int U = env_int("MB_ATTN_U", 16);
-  if (U != 4 && U != 8 && U != 16) return fail(ctx, MB_ERR_ARG, "MB_ATTN_U must be 4, 8 or 16");
-  const int gu = (ring.bf16 ? 8 : 4) * U;
+// Waves per block for a window of up to `max_valid` slots: about one wave
+// per 128 slots (bf16) or 256 slots (fp32), at most MAXNW; measured on the
+// B=64, C=2048 decode step, these keep every wave streaming whole load
+// batches and the chip at one to two rounds of resident waves.
+template <bool APPEND, bool IN_BF16>
+static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const void* q,
+                       const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
+                       int64_t max_valid, float* q_out, const Rows& qo_rows, float* out,
+                       const Rows& out_rows) {
   const int C = ring.C;
   if (max_valid > C) max_valid = C;
   if (max_valid < 1) max_valid = 1;
   const int64_t nq = (int64_t)B * rows;
   if (nq == 0) return MB_OK;
-  const int64_t units = nq * H;
-  const int64_t want = (target + units - 1) / units;
-  int64_t split_len = (max_valid + want - 1) / want;
-  if (split_len < (max_valid + 63) / 64) split_len = (max_valid + 63) / 64;
-  split_len = ((split_len + gu - 1) / gu) * gu;
-  const int nsplit = (int)((max_valid + split_len - 1) / split_len);
-  if (nq * nsplit > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
-  float* part = nullptr;
-  if (nsplit > 1) {
-    part = (float*)scratch(ctx, "attn_part", (size_t)units * nsplit * PART * 4);
-    if (!part) return fail(ctx, MB_ERR_NOMEM, "attention partials allocation failed");
-  }
-  dim3 grid((unsigned)(nq * nsplit), H / 4);
-#define MB_SPLIT(BF, UU) \
-  launch_split<BF, UU>(ctx, grid, q, q_rows, pos0, n_rows, rows, ring, (int)split_len, nsplit, part, out, out_rows)
+  if (nq * H > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
+  const dim3 grid((unsigned)(nq * H));
   if (ring.bf16) {
-    if (U == 4) MB_SPLIT(true, 4); else if (U == 8) MB_SPLIT(true, 8); else MB_SPLIT(true, 16);
+    constexpr int U = 8, MAXNW = 16;
+    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 127) / 128);
+    hipLaunchKernelGGL((k_attn_unit<true, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
+                       ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
+                       ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
   } else {
-    if (U == 4) MB_SPLIT(false, 4); else if (U == 8) MB_SPLIT(false, 8); else MB_SPLIT(false, 16);
+    constexpr int U = 12, MAXNW = 8;
+    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 255) / 256);
+    hipLaunchKernelGGL((k_attn_unit<false, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
+                       ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
+                       ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
   }
-#undef MB_SPLIT
   MB_HIP(ctx, hipGetLastError());
-  if (nsplit > 1) {
-    hipLaunchKernelGGL(k_attn_combine, dim3((unsigned)((units + 3) / 4)), dim3(256), 0, ctx->stream,
-                       part, nsplit, n_rows, rows, units, out, out_rows);
-    MB_HIP(ctx, hipGetLastError());
-  }
   return MB_OK;
+}
+
+int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
+                const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
+                float* out, const Rows& out_rows) {
+  return launch_unit<false, false>(ctx, ring, B, rows, q, q_rows, pos0, n_rows, max_valid, nullptr,
+                                   Rows{}, out, out_rows);
+}
+
+int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv, int qkv_dtype,
+                       const Rows& qkv_rows, const int32_t* pos, int64_t max_valid, float* q_out,
+                       const Rows& qo_rows, float* out, const Rows& out_rows) {
+  if (qkv_dtype == MB_DT_BF16)
+    return launch_unit<true, true>(ctx, ring, B, 1, qkv, qkv_rows, pos, nullptr, max_valid, q_out,
+                                   qo_rows, out, out_rows);
+  return launch_unit<true, false>(ctx, ring, B, 1, qkv, qkv_rows, pos, nullptr, max_valid, q_out,
+                                  qo_rows, out, out_rows);
 }
 
 }  // namespace mb

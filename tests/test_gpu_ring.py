@@ -205,3 +205,107 @@ def test_c4_eviction_stress():
                     assert np.array_equal(k, rings[b].K[0]) and np.array_equal(v, rings[b].V[0])
                     want = rings[b].attend(q[b][None], [p])[0]
                     assert np.abs(out[b] - want).max() < 1e-4, (p, b)
+
+
+@pytest.mark.parametrize("name,kv", KV)
+def test_append_attend_equals_append_then_attention(name, kv):
+    """The fused append + attention launch against the two calls in sequence
+    on a twin context (bit-exact: same stored rows, same fold order) and
+    against the oracle; rings that wrap, a ring holding only the new row, and
+    positions beyond the RoPE table."""
+    say(f"fused append+attention kv={name}")
+    B, C = 6, 96
+    rng = np.random.default_rng(21)
+    pos = np.array([0, 5, 95, 96, 300, 70_000], np.int32)
+    with mb.Context(n_layers=2, capacity=C, max_seqs=B, max_rows=C, kv_dtype=kv) as fused, \
+            mb.Context(n_layers=2, capacity=C, max_seqs=B, max_rows=C, kv_dtype=kv) as twin:
+        ring = _oracle_ring(B, C, kv)
+        start = np.maximum(0, pos - C + 1).astype(np.int32)
+        n = (pos - start).astype(np.int32)
+        fill = rng.standard_normal((B, C, 2304), dtype=np.float32)
+        for ctx in (fused, twin):
+            ctx.ring_write_rows(1, fill, start, n)
+        ring.write(fill, start, n)
+        for step in range(5):
+            qkv = rng.standard_normal((B, 2304), dtype=np.float32)
+            q_f, out_f = fused.append_attend(1, qkv, pos)
+            q_t = twin.ring_append(1, qkv, pos)
+            out_t = twin.decode_attention(1, q_t, pos)
+            assert np.array_equal(q_f, q_t), step
+            assert np.array_equal(out_f, out_t), step
+            q_or = ring.append(qkv, pos)
+            assert np.array_equal(q_f, q_or), step
+            assert np.abs(out_f - ring.attend(q_or, pos)).max() < 1e-4, step
+            pos = pos + 1
+        _check_ring(fused, ring, 1, range(B))
+        # without q_out the output is the same
+        qkv = rng.standard_normal((B, 2304), dtype=np.float32)
+        _, out_a = fused.append_attend(0, qkv, pos, want_q=False)
+        q_t = twin.ring_append(0, qkv, pos)
+        assert np.array_equal(out_a, twin.decode_attention(0, q_t, pos))
+
+
+def test_append_attend_range_error_on_a_non_wrapping_ring():
+    say("fused append+attention range error")
+    import torch
+
+    with mb.Context(n_layers=1, capacity=8, max_seqs=2, max_rows=8, wrap=False) as ctx:
+        qkv = np.zeros((2, 2304), np.float32)
+        with pytest.raises(mb.MbError) as e:
+            ctx.append_attend(0, qkv, [3, 8])
+        assert e.value.code == mb.MB_ERR_RANGE
+        d = torch.zeros((2, 2304), device="cuda")
+        p = torch.tensor([3, 7], dtype=torch.int32, device="cuda")
+        out = torch.empty((2, 768), device="cuda")
+        with pytest.raises(mb.MbError) as e:
+            ctx.append_attend_dev(0, 2, d.data_ptr(), p.data_ptr(), 8, out.data_ptr())
+        assert e.value.code == mb.MB_ERR_RANGE and "exceeds the KV ring" in str(e.value)
+        ctx.append_attend_dev(0, 2, d.data_ptr(), p.data_ptr(), 7, out.data_ptr())
+        ctx.synchronize()
+        assert torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("name,kv", KV)
+def test_c1_full_size_fused_matches_two_launches(name, kv):
+    """B=64, C=2048, positions U[1, 6144): two layers filled with the same
+    rows; layer 0 steps with append then attention, layer 1 with the fused
+    launch.  Outputs and ring contents must be identical, and the outputs
+    agree with the unfused path for three consecutive steps."""
+    torch = pytest.importorskip("torch")
+    say(f"C1 full size fused kv={name}")
+    B, C = 64, 2048
+    g = np.random.default_rng(20260101)
+    pos = g.integers(1, 6144, size=B).astype(np.int32)
+    start = np.maximum(0, pos - (C - 1)).astype(np.int32)
+    nfill = (pos - start).astype(np.int32)
+    dev = torch.device("cuda")
+    tg = torch.Generator(device=dev)
+    tg.manual_seed(9)
+    with mb.Context(n_layers=2, capacity=C, max_seqs=B, max_rows=256, kv_dtype=kv) as ctx:
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        chunk = 256
+        for c0 in range(0, int(nfill.max()), chunk):
+            qkv = torch.randn((B, chunk, 2304), generator=tg, device=dev, dtype=torch.float32)
+            n = torch.from_numpy(np.clip(nfill - c0, 0, chunk).astype(np.int32)).to(dev)
+            p0 = torch.from_numpy((start + c0).astype(np.int32)).to(dev)
+            for layer in (0, 1):
+                ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+        q0 = torch.empty((B, 768), device=dev)
+        q1 = torch.empty((B, 768), device=dev)
+        out0 = torch.empty((B, 768), device=dev)
+        out1 = torch.empty((B, 768), device=dev)
+        for s in range(3):
+            step = torch.randn((B, 2304), generator=tg, device=dev, dtype=torch.float32)
+            pos_d = torch.from_numpy(pos + s).to(dev)
+            mp = int(pos.max()) + s
+            ctx.ring_append_dev(0, B, step.data_ptr(), pos_d.data_ptr(), q0.data_ptr())
+            ctx.decode_attention_dev(0, B, q0.data_ptr(), pos_d.data_ptr(), mp, out0.data_ptr())
+            ctx.append_attend_dev(1, B, step.data_ptr(), pos_d.data_ptr(), mp, out1.data_ptr(),
+                                  q_ptr=q1.data_ptr())
+            torch.cuda.synchronize()
+            assert torch.equal(q0, q1), s
+            assert torch.equal(out0, out1), s
+        for b in range(0, B, 7):
+            k0, v0, sp0 = ctx.read_ring(0, b)
+            k1, v1, sp1 = ctx.read_ring(1, b)
+            assert np.array_equal(sp0, sp1) and np.array_equal(k0, k1) and np.array_equal(v0, v1), b
