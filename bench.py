@@ -169,6 +169,69 @@ def run_c1(args, kv_name):
     return res
 
 
+def run_voices_attention(args, B=256, C=1024, frames_in=150):
+    """The KV-attention kernel at the many-voice decode shape: 256 voices,
+    ring capacity 1024, bf16 KV, 12 layer rings stepped in turn; positions are
+    the many-voice prompt lengths U[64, 400) (seed 33) plus `frames_in`
+    decoded frames, so the live windows span 214-549 slots and grow by one
+    per pass over the layers.  Each step is one fused append + attention
+    launch, timed back to back with HIP events."""
+    import torch
+
+    import mockbird_amd as mb
+
+    L = 12
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=128, kv_dtype=mb.MB_KV_BF16)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    g = np.random.default_rng(33)
+    pos0 = (g.integers(64, 400, size=B) + frames_in).astype(np.int32)
+    tg = torch.Generator(device=dev)
+    tg.manual_seed(11)
+    chunk = 128
+    zeros = np.zeros(B, np.int32)
+    for layer in range(L):
+        for c0 in range(0, int(pos0.max()), chunk):
+            qkv = torch.randn((B, chunk, QKV), generator=tg, device=dev)
+            n = torch.from_numpy(np.clip(pos0 - c0, 0, chunk).astype(np.int32)).to(dev)
+            p0 = torch.from_numpy((zeros + c0).astype(np.int32)).to(dev)
+            ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+    torch.cuda.synchronize()
+    steps, warmup = args.steps, args.warmup
+    tokens = (warmup + steps) // L + 2
+    pos_all = torch.from_numpy((pos0[None, :] + np.arange(tokens)[:, None]).astype(np.int32)).to(dev)
+    qkv_l = [torch.randn((B, QKV), generator=tg, device=dev) for _ in range(L)]
+    out = torch.empty((B, D), device=dev)
+    max_pos = int(pos0.max()) + tokens
+    if max_pos >= C:
+        raise ValueError("positions exceed the ring")
+
+    def step(s):
+        layer, tok = s % L, s // L
+        ctx.append_attend_dev(layer, B, qkv_l[layer].data_ptr(), pos_all[tok].data_ptr(), max_pos,
+                              out.data_ptr())
+
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(warmup + i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / steps
+    nbytes = np.mean([fused_bytes(pos0 + (warmup + i) // L, C, 2) for i in range(steps)])
+    ctx.close()
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "fused ring append + decode attention, 256 voices, 12 x 64, ring 1024, "
+                        "bf16 KV, windows 214-549 slots, 12 layer rings in turn",
+            "avg_us": round(us, 2), "bytes_per_launch": int(nbytes), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def run_c2(args):
     """Causal prefill attention, B=16, S=512, 12 heads x 64, bf16 q/k/v with
     fp32 accumulation (bf16 MFMA), RoPE at pos = row, ring C=1024 from slot 0.
@@ -351,9 +414,10 @@ def main():
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
-    ap.add_argument("--legs", default="copy,c1,c2,frames",
+    ap.add_argument("--legs", default="copy,c1,voices,c2,frames",
                     help="comma list of copy (plain 2 GiB HBM copy), c1 (append + decode "
-                         "attention), c2 (prefill attention), frames (model decode frames/s); "
+                         "attention, 64 sequences, C=2048), voices (the same at 256 voices, "
+                         "C=1024), c2 (prefill attention), frames (model decode frames/s); "
                          "the JSON line needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     args = ap.parse_args()
@@ -368,6 +432,7 @@ def main():
     if args.no_frames:
         legs.discard("frames")
     copy = run_copy() if "copy" in legs else None
+    voices = run_voices_attention(args) if "voices" in legs else None
     c2 = run_c2(args) if "c2" in legs else None
     frames = None
     if "frames" in legs:
@@ -380,8 +445,8 @@ def main():
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
         frames = [run_frames(w, b, *plan[b]) for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
-        print(json.dumps({"hbm_copy": copy, "prefill_attention": c2, "frames_detail": frames}),
-              flush=True)
+        print(json.dumps({"hbm_copy": copy, "kv_attention_256_voices": voices,
+                          "prefill_attention": c2, "frames_detail": frames}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -425,6 +490,7 @@ def main():
             "frac": round(f32["gbs"] / HBM_PEAK_GBS, 4),
             "two_launch_gbs": round(f32["unfused_gbs"], 1)},
         "hbm_copy": copy,
+        "kv_attention_256_voices": voices,
         "prefill_attention": c2,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
         "frames_detail": frames,

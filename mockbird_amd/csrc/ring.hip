@@ -468,9 +468,10 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
 }
 
 // Waves per block for a window of up to `max_valid` slots: about one wave
-// per 128 slots (bf16) or 256 slots (fp32), at most MAXNW; measured on the
-// B=64, C=2048 decode step, these keep every wave streaming whole load
-// batches and the chip at one to two rounds of resident waves.
+// per 180 slots (bf16, 64-slot batches) or 256 slots (fp32, 48-slot
+// batches), at most MAXNW.  Measured on the 64-voice C=2048 step and the
+// 256-voice C=1024 step (windows 200-550), these per-wave lengths were the
+// fastest of the sweep on both shapes.
 template <bool APPEND, bool IN_BF16>
 static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const void* q,
                        const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
@@ -485,7 +486,7 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
   const dim3 grid((unsigned)(nq * H));
   if (ring.bf16) {
     constexpr int U = 8, MAXNW = 16;
-    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 127) / 128);
+    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 179) / 180);
     hipLaunchKernelGGL((k_attn_unit<true, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                        ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
                        ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
