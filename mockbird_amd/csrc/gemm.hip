@@ -157,13 +157,15 @@ static void gemm_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const
 //
 // A workgroup owns MT rows x 64 columns and a k range; its four waves take
 // four consecutive quarters of that range and add their sums through LDS in
-// wave order.  Across workgroups the k range is split S ways (gridDim.z):
+// wave order.  Each wave streams its quarter in 16-deep chunks through ST
+// register stages (chunk c in stage c % ST, ST - 1 chunks in flight ahead of
+// the MFMAs).  Across workgroups the k range may be split S ways (gridDim.z):
 // each split writes its sum to part[split][M][N] and k_gemm_reduce adds the
 // splits in split order, so every output is the same fixed-order sum on every
 // run.
 constexpr int kStreamMaxM = 1024;
-constexpr int kStreamChunk = 32;  // k rows per wave per pipeline stage
-constexpr int kStreamMaxSplit = 32;
+constexpr int kStreamChunk = 16;  // k rows per wave per pipeline stage
+constexpr int kStreamMaxSplit = 8;
 
 template <int EPI>
 __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ bias, int n,
@@ -182,7 +184,7 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
   return v;
 }
 
-template <int MT, int EPI>
+template <int MT, int ST, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int N, int kw,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
@@ -208,49 +210,44 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
 #pragma unroll
     for (int i = 0; i < MI; i++) Ap[i] = A + (int64_t)min(m0 + 16 * i + l16, M - 1) * lda + 4 * r;
     const float* Wp = W + (int64_t)4 * r * N + n;
-    float4 a[2][2][MI], w[2][2][4];  // [stage][16-deep half][...]
+    float4 a[ST][MI], w[ST][4];
     auto load = [&](int st, int k) {
 #pragma unroll
-      for (int h = 0; h < 2; h++) {
+      for (int t = 0; t < 4; t++) w[st][t] = *(const float4*)(Wp + (int64_t)(k + t) * N);
 #pragma unroll
-        for (int t = 0; t < 4; t++) w[st][h][t] = *(const float4*)(Wp + (int64_t)(k + 16 * h + t) * N);
-#pragma unroll
-        for (int i = 0; i < MI; i++) a[st][h][i] = *(const float4*)(Ap[i] + k + 16 * h);
-      }
+      for (int i = 0; i < MI; i++) a[st][i] = *(const float4*)(Ap[i] + k);
     };
     auto mma = [&](int st) {
 #pragma unroll
-      for (int h = 0; h < 2; h++)
+      for (int t = 0; t < 4; t++) {
+        const float4 wt = w[st][t];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const float4 wt = w[st][h][t];
-#pragma unroll
-          for (int i = 0; i < MI; i++) {
-            const float av = t == 0 ? a[st][h][i].x : t == 1 ? a[st][h][i].y : t == 2 ? a[st][h][i].z : a[st][h][i].w;
-            acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.x, acc[i][0], 0, 0, 0);
-            acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.y, acc[i][1], 0, 0, 0);
-            acc[i][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.z, acc[i][2], 0, 0, 0);
-            acc[i][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.w, acc[i][3], 0, 0, 0);
-          }
+        for (int i = 0; i < MI; i++) {
+          const float av = t == 0 ? a[st][i].x : t == 1 ? a[st][i].y : t == 2 ? a[st][i].z : a[st][i].w;
+          acc[i][0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.x, acc[i][0], 0, 0, 0);
+          acc[i][1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.y, acc[i][1], 0, 0, 0);
+          acc[i][2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.z, acc[i][2], 0, 0, 0);
+          acc[i][3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, wt.w, acc[i][3], 0, 0, 0);
         }
+      }
     };
-    // Two register stages, chunk c in stage c & 1.  The loop body has no
-    // branch, so each stage's MFMAs wait only for that stage's loads: the
-    // stage-0 prefetch is always issued, re-reading the last chunk (in
-    // bounds, unused) when there is no next one.
+    // Prefetch ST - 1 chunks, then per chunk: issue the load ST - 1 ahead and
+    // run the MFMAs of the oldest stage.  Past the end the last chunk is
+    // re-read (in bounds, unused), so the loop body has no load branch and
+    // each stage's MFMAs wait only for that stage's loads.
     const int k0 = (split * 4 + wave) * kw, k1 = k0 + kw, nc = kw / kStreamChunk;
-    load(0, k0);
-    int c = 0;
-    for (; c + 2 <= nc; c += 2) {
-      const int k = k0 + c * kStreamChunk;
-      load(1, k + kStreamChunk);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
-      mma(0);
-      load(0, min(k + 2 * kStreamChunk, k1 - kStreamChunk));
-      __builtin_amdgcn_sched_barrier(0);
-      mma(1);
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++) load(s, min(k0 + s * kStreamChunk, k1 - kStreamChunk));
+    for (int c = 0; c < nc; c += ST) {
+#pragma unroll
+      for (int s = 0; s < ST; s++) {
+        if (c + s < nc) {
+          load((s + ST - 1) % ST, min(k0 + (c + s + ST - 1) * kStreamChunk, k1 - kStreamChunk));
+          __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+          mma(s);
+        }
+      }
     }
-    if (c < nc) mma(0);
   }
 
   // the four waves' sums, added in wave order
@@ -326,20 +323,10 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
   *(float4*)cp = epilogue4<EPI>(sum, bias, col, cp);
 }
 
-template <int MT>
+template <int MT, int ST>
 static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
-                         int K, const float* bias, float* Cm, int64_t ldc, int M) {
-  const int tx = N / 64, ty = (M + MT - 1) / MT, tiles = tx * ty;
-  // Smallest split S (4 waves x S workgroups share K in whole 32-row chunks,
-  // S at most kStreamMaxSplit) that gives every CU a workgroup; else the
-  // largest allowed.
-  const int quarters = K / (4 * kStreamChunk);
-  int S = 1;
-  for (int s = 1; s <= kStreamMaxSplit && s <= quarters; s++) {
-    if (quarters % s) continue;
-    S = s;
-    if ((int64_t)tiles * s >= 256) break;
-  }
+                         int K, const float* bias, float* Cm, int64_t ldc, int M, int S) {
+  const int tx = N / 64, ty = (M + MT - 1) / MT;
   float* part = nullptr;
   if (S > 1) {
     part = (float*)scratch(ctx, "gemm_part", (size_t)S * M * N * 4);
@@ -348,14 +335,14 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
   const int kw = K / (4 * S);
   if (epi == EPI_GELU)
-    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_GELU>), grid, dim3(256), 0, ctx->stream, A, lda, W, N,
-                       kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_GELU>), grid, dim3(256), 0, ctx->stream, A, lda,
+                       W, N, kw, bias, Cm, ldc, M, part);
   else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_ADD>), grid, dim3(256), 0, ctx->stream, A, lda, W, N,
-                       kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_ADD>), grid, dim3(256), 0, ctx->stream, A, lda,
+                       W, N, kw, bias, Cm, ldc, M, part);
   else
-    hipLaunchKernelGGL((k_gemm_stream<MT, EPI_STORE>), grid, dim3(256), 0, ctx->stream, A, lda, W,
-                       N, kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_STORE>), grid, dim3(256), 0, ctx->stream, A, lda,
+                       W, N, kw, bias, Cm, ldc, M, part);
   if (S > 1) {
     const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
     if (epi == EPI_GELU)
@@ -372,21 +359,47 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   return MB_OK;
 }
 
-// M < kStreamMaxM: the streaming kernel, 16 rows per workgroup up to M = 16
-// and 32 above.  32 rows keep a wave at 3 per SIMD, and at M = 256 already
-// give most projections >= 256 workgroups without a split (a split's
-// partials cost a write and a read of M x N per extra split).
+// M < kStreamMaxM: the streaming kernel.  Its row tile is the smallest of
+// 16 / 32 / 48 / 64 rows that keeps the grid at most one workgroup per CU
+// (256 CUs), so the projection runs as one round; K = 3072 projections with
+// few tiles split K over up to 8 workgroups (fixed-order reduce).  Measured
+// on the decode projections (M = 1, 64, 256; N x K = 2304 x 768, 768 x 768,
+// 3072 x 768, 768 x 3072, 1024 x 768) these choices were the fastest of a
+// sweep over tile, pipeline depth and split; 16-deep chunks in 4 register
+// stages (3 for 48- and 64-row tiles, whose stages are wider).
 // Larger M: the LDS-tiled kernel with the largest tile that still gives the
 // chip (256 CUs) a block per CU, else the smallest tile.
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M) {
   if (M <= 0) return MB_OK;
-  if (N % 64 || K % (4 * kStreamChunk) || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
+  if (N % 64 || K % 128 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
   if (M < kStreamMaxM) {
-    if (M <= 16) return stream_launch<16>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
-    return stream_launch<32>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
+    const int tx = N / 64;
+    auto tiles = [&](int mt) { return (int64_t)tx * ((M + mt - 1) / mt); };
+    int mt = 64;
+    for (int cand : {16, 32, 48}) {
+      if (tiles(cand) <= 256) {
+        mt = cand;
+        break;
+      }
+    }
+    int S = 1;
+    if (K >= 2048) {
+      for (int s = kStreamMaxSplit; s > 1; s--) {
+        if (K % (4 * kStreamChunk * s) == 0 && tiles(mt) * s <= 256) {
+          S = s;
+          break;
+        }
+      }
+    }
+    switch (mt) {
+      case 16: return stream_launch<16, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
+      case 32: return stream_launch<32, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
+      case 48: return stream_launch<48, 3>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
+      default: return stream_launch<64, 3>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
+    }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };
   if (N % 128 == 0 && blocks(128, 128) >= 256)
