@@ -22,10 +22,14 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int GBK = 16;   // K slice
 constexpr int GPAD = 20;  // LDS row stride in floats (16 + 4)
 
+// GELU with the tanh approximation, 0.5 v (1 + tanh(u)) with
+// u = 0.7978845608 (v + 0.044715 v^3) (kernels-decode.ts:373-385), evaluated
+// as v / (1 + exp(-2u)): 0.5 (1 + tanh(u)) is the logistic function of 2u, so
+// the two forms are equal, and this one needs one exponential and no
+// cancellation (exp(-2u) overflowing to inf gives -0, the limit).
 __device__ __forceinline__ float gelu_tanh(float v) {
-  // 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))), kernels-decode.ts:373-385
-  const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
-  return 0.5f * v * (1.f + tanhf(inner));
+  const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+  return v / (1.f + __expf(-2.f * u));
 }
 
 template <int TM, int TN, int EPI>
@@ -184,13 +188,22 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
   return v;
 }
 
-template <int MT, int ST, int EPI>
+//
+// With LNF the A rows are the raw residual stream x and the LayerNorm in
+// front of the projection is folded in: W holds diag(gamma) * W, and
+//   LN(x) W = rstd (x W' - mean c) + d,   c = 1 W',  d = beta W
+// (c, d from k_fold_ln), so the kernel only needs each row's mean and rstd.
+// It accumulates them from the A values it streams anyway -- sums of
+// x - x0 and (x - x0)^2 with x0 = x[row][0], so the variance does not cancel
+// -- which requires the workgroup to see the whole row (S == 1, K == 768).
+template <int MT, int ST, int EPI, bool LNF>
 __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int N, int kw,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
-    float* __restrict__ part) {
+    float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd) {
   constexpr int MI = MT / 16;
   __shared__ f32x4_t red[3][MI][4][64];
+  __shared__ float4 stat[LNF ? 4 : 1][MI][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, r = lane >> 4;
   const int n = blockIdx.x * 64 + 4 * l16;
@@ -202,6 +215,7 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
   for (int i = 0; i < MI; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float x0[MI], sx[MI], sxx[MI];
 
   {
     // Rows past M read row M - 1 (in bounds, no branch); their sums are
@@ -209,6 +223,14 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* Ap[MI];
 #pragma unroll
     for (int i = 0; i < MI; i++) Ap[i] = A + (int64_t)min(m0 + 16 * i + l16, M - 1) * lda + 4 * r;
+    if (LNF) {
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        x0[i] = Ap[i][-4 * r];
+        sx[i] = 0.f;
+        sxx[i] = 0.f;
+      }
+    }
     const float* Wp = W + (int64_t)4 * r * N + n;
     float4 a[ST][MI], w[ST][4];
     auto load = [&](int st, int k) {
@@ -218,6 +240,15 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
       for (int i = 0; i < MI; i++) a[st][i] = *(const float4*)(Ap[i] + k);
     };
     auto mma = [&](int st) {
+      if (LNF) {
+#pragma unroll
+        for (int i = 0; i < MI; i++) {
+          const float e0 = a[st][i].x - x0[i], e1 = a[st][i].y - x0[i];
+          const float e2 = a[st][i].z - x0[i], e3 = a[st][i].w - x0[i];
+          sx[i] += (e0 + e1) + (e2 + e3);
+          sxx[i] = fmaf(e0, e0, fmaf(e1, e1, fmaf(e2, e2, fmaf(e3, e3, sxx[i]))));
+        }
+      }
 #pragma unroll
       for (int t = 0; t < 4; t++) {
         const float4 wt = w[st][t];
@@ -250,6 +281,18 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     }
   }
 
+  if (LNF) {
+    // a row's four k groups sit in lanes l16 + 16r: fold them, then lanes
+    // r = 0 publish the wave's quarter of the row sums
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+      sx[i] += __shfl_xor(sx[i], 16);
+      sx[i] += __shfl_xor(sx[i], 32);
+      sxx[i] += __shfl_xor(sxx[i], 16);
+      sxx[i] += __shfl_xor(sxx[i], 32);
+      if (lane < 16) stat[wave][i][lane] = make_float4(sx[i], sxx[i], x0[i], 0.f);
+    }
+  }
   // the four waves' sums, added in wave order
   if (wave > 0) {
 #pragma unroll
@@ -265,6 +308,30 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     for (int i = 0; i < MI; i++)
 #pragma unroll
       for (int j = 0; j < 4; j++) acc[i][j] += red[q][i][j][lane];
+
+  if (LNF) {
+    // rows 16i + 4r + v of this lane: mean and rstd from the four quarters,
+    // then out = rstd (acc - mean c) + d (+ bias and the epilogue below)
+    const float inv_k = 1.f / (float)(4 * kw);
+    const float4 cv = *(const float4*)(lnc + n), dv = *(const float4*)(lnd + n);
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+#pragma unroll
+      for (int v = 0; v < 4; v++) {
+        const int rl = 4 * r + v;
+        const float4 q0 = stat[0][i][rl], q1 = stat[1][i][rl], q2 = stat[2][i][rl], q3 = stat[3][i][rl];
+        const float s1 = ((q0.x + q1.x) + q2.x) + q3.x;
+        const float s2 = ((q0.y + q1.y) + q2.y) + q3.y;
+        const float ms = s1 * inv_k;  // mean of x - x0
+        const float var = fmaxf(s2 * inv_k - ms * ms, 0.f);
+        const float mean = q0.z + ms;
+        const float rstd = 1.f / sqrtf(var + 1e-5f);
+        acc[i][0][v] = rstd * (acc[i][0][v] - mean * cv.x) + dv.x;
+        acc[i][1][v] = rstd * (acc[i][1][v] - mean * cv.y) + dv.y;
+        acc[i][2][v] = rstd * (acc[i][2][v] - mean * cv.z) + dv.z;
+        acc[i][3][v] = rstd * (acc[i][3][v] - mean * cv.w) + dv.w;
+      }
+  }
 
   // lane holds C[m0 + 16i + 4r + v][n + j] in acc[i][j][v]
   if (S > 1) {
@@ -323,9 +390,10 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
   *(float4*)cp = epilogue4<EPI>(sum, bias, col, cp);
 }
 
-template <int MT, int ST>
+template <int MT, int ST, bool LNF>
 static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
-                         int K, const float* bias, float* Cm, int64_t ldc, int M, int S) {
+                         int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
+                         const float* lnc, const float* lnd) {
   const int tx = N / 64, ty = (M + MT - 1) / MT;
   float* part = nullptr;
   if (S > 1) {
@@ -335,14 +403,14 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
   const int kw = K / (4 * S);
   if (epi == EPI_GELU)
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_GELU>), grid, dim3(256), 0, ctx->stream, A, lda,
-                       W, N, kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_GELU, LNF>), grid, dim3(256), 0, ctx->stream, A,
+                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
   else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_ADD>), grid, dim3(256), 0, ctx->stream, A, lda,
-                       W, N, kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_ADD, LNF>), grid, dim3(256), 0, ctx->stream, A,
+                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
   else
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_STORE>), grid, dim3(256), 0, ctx->stream, A, lda,
-                       W, N, kw, bias, Cm, ldc, M, part);
+    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_STORE, LNF>), grid, dim3(256), 0, ctx->stream, A,
+                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
   if (S > 1) {
     const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
     if (epi == EPI_GELU)
@@ -357,6 +425,81 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   }
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
+}
+
+// Row tile and k split of the streaming kernel for an M x N x K projection
+// (see launch_gemm); `whole_rows` forbids a split (LayerNorm folding needs
+// every k of a row in one workgroup).
+static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) {
+  const int tx = N / 64;
+  auto tiles = [&](int m) { return (int64_t)tx * ((M + m - 1) / m); };
+  mt = 64;
+  for (int cand : {16, 32, 48}) {
+    if (tiles(cand) <= 256) {
+      mt = cand;
+      break;
+    }
+  }
+  S = 1;
+  if (K >= 2048 && !whole_rows) {
+    for (int s = kStreamMaxSplit; s > 1; s--) {
+      if (K % (4 * kStreamChunk * s) == 0 && tiles(mt) * s <= 256) {
+        S = s;
+        break;
+      }
+    }
+  }
+}
+
+// W' = diag(gamma) W, c = column sums of W', d = beta W: the folded form of
+// "LayerNorm, then x W" used by the LNF streaming kernel.  One thread per
+// column; c and d are summed in double in k order and rounded once.
+__global__ __launch_bounds__(256) void k_fold_ln(const float* __restrict__ W, int K, int N,
+                                                 const float* __restrict__ gamma,
+                                                 const float* __restrict__ beta,
+                                                 float* __restrict__ Wg, float* __restrict__ c,
+                                                 float* __restrict__ d) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  double sc = 0.0, sd = 0.0;
+  for (int k = 0; k < K; k++) {
+    const float w = W[(int64_t)k * N + n];
+    const float g = __fmul_rn(gamma[k], w);
+    Wg[(int64_t)k * N + n] = g;
+    sc += (double)g;
+    sd += (double)beta[k] * (double)w;
+  }
+  c[n] = (float)sc;
+  d[n] = (float)sd;
+}
+
+int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma,
+                   const float* beta, float* Wg, float* c, float* d) {
+  hipLaunchKernelGGL(k_fold_ln, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream, W, K,
+                     N, gamma, beta, Wg, c, d);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// out = epi(LN(x) W + bias) for decode-sized M with the LayerNorm folded in
+// (Wg, c, d from launch_fold_ln); K must be the row width 768.  Larger M
+// returns MB_ERR_STATE so the caller runs the LayerNorm and the GEMM apart.
+int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const float* Wg, int N,
+                   int K, const float* c, const float* d, const float* bias, float* Cm,
+                   int64_t ldc, int M) {
+  if (M <= 0) return MB_OK;
+  if (M >= kStreamMaxM) return MB_ERR_STATE;
+  if (K != D || N % 64 || ldx % 4 || ldc % 4 || ((uintptr_t)x & 15) || ((uintptr_t)Wg & 15) ||
+      ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) || ((uintptr_t)c & 15) || ((uintptr_t)d & 15))
+    return fail(ctx, MB_ERR_ARG, "folded gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  int mt, S;
+  stream_shape(M, N, K, true, mt, S);
+  switch (mt) {
+    case 16: return stream_launch<16, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
+    case 32: return stream_launch<32, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
+    case 48: return stream_launch<48, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
+    default: return stream_launch<64, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
+  }
 }
 
 // M < kStreamMaxM: the streaming kernel.  Its row tile is the smallest of
@@ -376,29 +519,13 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
   if (M < kStreamMaxM) {
-    const int tx = N / 64;
-    auto tiles = [&](int mt) { return (int64_t)tx * ((M + mt - 1) / mt); };
-    int mt = 64;
-    for (int cand : {16, 32, 48}) {
-      if (tiles(cand) <= 256) {
-        mt = cand;
-        break;
-      }
-    }
-    int S = 1;
-    if (K >= 2048) {
-      for (int s = kStreamMaxSplit; s > 1; s--) {
-        if (K % (4 * kStreamChunk * s) == 0 && tiles(mt) * s <= 256) {
-          S = s;
-          break;
-        }
-      }
-    }
+    int mt, S;
+    stream_shape(M, N, K, false, mt, S);
     switch (mt) {
-      case 16: return stream_launch<16, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
-      case 32: return stream_launch<32, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
-      case 48: return stream_launch<48, 3>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
-      default: return stream_launch<64, 3>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S);
+      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
     }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };

@@ -169,28 +169,42 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
 // kernels-decode.ts:428-478).  Strict '>' keeps the lowest id on ties and a
 // NaN never wins.  The winner goes to tokens[b][ch]; the seen bit is set only
 // for sequences that continue (the reference stops before drawing codes).
+// One wave per sequence.  Lane l takes ids 16l .. 16l+15: four 16-byte logit
+// loads and the one seen-mask word that holds their 16 bits, all issued up
+// front; the penalised values are compared in double (policy.ts:273-290 works
+// on JS numbers) with strict > so the lowest id wins a tie, within the lane
+// (ascending ids) and across lanes (the lower id on equal values).
 __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
                                                         int ch, float penalty,
                                                         uint32_t* __restrict__ seen,
                                                         const int32_t* __restrict__ cont,
                                                         int32_t* __restrict__ tokens) {
+  static_assert(CODES == 64 * 16, "one wave covers the codebook, 16 ids per lane");
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
   uint32_t* sm = seen + ((int64_t)b * NVQ + ch) * 32;
-  // the penalty applies once the channel has emitted anything (policy.ts:282)
-  uint32_t any = lane < 32 ? sm[lane] : 0u;
+  const float4* lp = (const float4*)(logits + (int64_t)b * CODES + 16 * lane);
+  float v[16];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) any |= __shfl_xor(any, off);
-  const bool apply = any != 0u && penalty != 1.f;
+  for (int q = 0; q < 4; q++) {
+    const float4 t = lp[q];
+    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
+  }
+  const uint32_t word = sm[lane >> 1];
+  const uint32_t bits = (word >> (16 * (lane & 1))) & 0xffffu;
+  // the penalty applies once the channel has emitted anything (policy.ts:282)
+  const bool any = __ballot(word != 0u) != 0ull;
+  const bool apply = any && penalty != 1.f;
   double best = -INFINITY;
   int idx = 0x7fffffff;
-  for (int i = lane; i < CODES; i += 64) {
-    double s = logits[(int64_t)b * CODES + i];
-    if (apply && ((sm[i >> 5] >> (i & 31)) & 1u)) s = s < 0 ? s * (double)penalty : s / (double)penalty;
+#pragma unroll
+  for (int j = 0; j < 16; j++) {
+    double s = v[j];
+    if (apply && ((bits >> j) & 1u)) s = s < 0 ? s * (double)penalty : s / (double)penalty;
     if (s > best) {
       best = s;
-      idx = i;
+      idx = 16 * lane + j;
     }
   }
 #pragma unroll

@@ -220,6 +220,8 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
   if (!ctx) return MB_ERR_ARG;
   if (!name || !data || !dims || ndims < 1 || ndims > 4)
     return fail(ctx, MB_ERR_ARG, "mb_upload_tensor: bad arguments");
+  if (name[0] == '#')  // the context's own derived tensors live under '#' names
+    return fail(ctx, MB_ERR_ARG, "mb_upload_tensor: names starting with '#' are reserved");
   int64_t numel = 1;
   for (int i = 0; i < ndims; i++) {
     if (dims[i] < 1) return fail(ctx, MB_ERR_ARG, "mb_upload_tensor(%s): dim %d is %lld", name, i,

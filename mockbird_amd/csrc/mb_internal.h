@@ -64,10 +64,13 @@ struct AudioTables {
   const float* t[NVQ];
 };
 
-// Device pointers of one d=768 transformer layer ([K, N] row-major matrices).
+// Device pointers of one d=768 transformer layer ([K, N] row-major matrices),
+// plus the LayerNorm-folded forms of the two projections that follow a
+// LayerNorm (W' = diag(gamma) W, c = column sums of W', d = beta W).
 struct LayerW {
   const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
   const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
+  const float *attn_wg, *attn_c, *attn_d, *fc_in_wg, *fc_in_c, *fc_in_d;
 };
 
 // Every weight a model call needs, resolved from the uploaded tensors.
@@ -78,7 +81,12 @@ struct ModelW {
   LayerW local;
   const float *local_lnf_w, *local_lnf_b, *text_head;
   AudioTables audio_heads;
+  // the audio heads with the local ln_f folded in
+  AudioTables head_wg, head_c, head_d;
 };
+
+// Projections with fewer rows than this run with their LayerNorm folded in.
+constexpr int kFoldMaxM = 1024;
 
 }  // namespace mb
 
@@ -215,6 +223,14 @@ int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value);
 enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2 };
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M);
+
+// LayerNorm folded into the projection after it (decode-sized M): Wg, c, d
+// from launch_fold_ln; launch_gemm_ln returns MB_ERR_STATE for M >= 1024.
+int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma,
+                   const float* beta, float* Wg, float* c, float* d);
+int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const float* Wg, int N,
+                   int K, const float* c, const float* d, const float* bias, float* Cm,
+                   int64_t ldc, int M);
 
 // layers.hip
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,

@@ -47,6 +47,50 @@ int resolve_layer(mb_ctx* ctx, const std::string& p, LayerW& w, std::string& mis
   return missing.empty() ? MB_OK : MB_ERR_STATE;
 }
 
+// A device tensor owned by the context under an internal name (freed with
+// the uploaded weights); reallocated only when its size changes.
+float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel) {
+  DeviceTensor& t = ctx->weights[name];
+  if (t.ptr && t.numel != numel) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(t.ptr);
+    ctx->device_bytes -= t.numel * 4;
+    t.ptr = nullptr;
+  }
+  if (!t.ptr) {
+    if (hipMalloc(&t.ptr, (size_t)numel * 4) != hipSuccess) {
+      ctx->weights.erase(name);
+      return nullptr;
+    }
+    ctx->device_bytes += numel * 4;
+    ctx->graph_gen++;
+  }
+  t.numel = numel;
+  t.dims = {numel};
+  return t.ptr;
+}
+
+// LayerNorm (gamma, beta) folded into the [K][N] projection W after it.
+int fold(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, const float* gamma,
+         const float* beta, const float*& wg, const float*& c, const float*& d) {
+  float* pw = internal_tensor(ctx, name + ".w", (int64_t)K * N);
+  float* pc = internal_tensor(ctx, name + ".c", N);
+  float* pd = internal_tensor(ctx, name + ".d", N);
+  if (!pw || !pc || !pd) return fail(ctx, MB_ERR_NOMEM, "folded weight allocation failed (%s)", name.c_str());
+  wg = pw;
+  c = pc;
+  d = pd;
+  return launch_fold_ln(ctx, W, K, N, gamma, beta, pw, pc, pd);
+}
+
+int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
+  int rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
+                w.attn_d);
+  if (rc) return rc;
+  return fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
+              w.fc_in_d);
+}
+
 // Resolve every weight once per upload (gpu.ts:339-343 throws "weight not
 // uploaded" the same way).  `local` selects the local-head half.
 int resolve(mb_ctx* ctx, bool global, bool local) {
@@ -78,7 +122,19 @@ int resolve(mb_ctx* ctx, bool global, bool local) {
       m.audio_heads.t[k] = get("model.audio_lm_heads." + std::to_string(k) + ".weight", {D, CODES});
   }
   if (!missing.empty()) return fail(ctx, MB_ERR_STATE, "%s", missing.c_str());
-  if (global && local) ctx->model_ok = true;
+  if (global && local) {
+    int rc;
+    for (size_t l = 0; l < m.layers.size(); l++)
+      if ((rc = fold_layer(ctx, "#fold/h" + std::to_string(l), m.layers[l]))) return rc;
+    if ((rc = fold_layer(ctx, "#fold/local", m.local))) return rc;
+    for (int k = 0; k < NVQ; k++) {
+      const std::string p = "#fold/head" + std::to_string(k);
+      if ((rc = fold(ctx, p, m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.local_lnf_b,
+                     m.head_wg.t[k], m.head_c.t[k], m.head_d.t[k])))
+        return rc;
+    }
+    ctx->model_ok = true;
+  }
   return MB_OK;
 }
 
@@ -116,9 +172,17 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
               const int32_t* pos0, const int32_t* n_rows, const int32_t* row_off, bool prefill,
               int64_t max_valid, Act& a) {
   int rc;
-  if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln1_w, w.ln1_b, a.norm, D))) return rc;
-  if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, w.attn_w, QKV, D, w.attn_b, a.qkv, QKV, (int)M)))
-    return rc;
+  // decode-sized M: each LayerNorm is folded into the projection after it
+  const bool folded = M < kFoldMaxM;
+  if (folded) {
+    if ((rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, w.attn_wg, QKV, D, w.attn_c, w.attn_d,
+                             w.attn_b, a.qkv, QKV, (int)M)))
+      return rc;
+  } else {
+    if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln1_w, w.ln1_b, a.norm, D))) return rc;
+    if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, w.attn_w, QKV, D, w.attn_b, a.qkv, QKV, (int)M)))
+      return rc;
+  }
   Rows qkv_rows, q_rows;
   if (prefill) {
     qkv_rows.row_stride = QKV;
@@ -142,9 +206,15 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   }
   if (rc) return rc;
   if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, w.proj_w, D, D, w.proj_b, a.x, D, (int)M))) return rc;
-  if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln2_w, w.ln2_b, a.norm, D))) return rc;
-  if ((rc = launch_gemm(ctx, EPI_GELU, a.norm, D, w.fc_in_w, FFN, D, w.fc_in_b, a.ffn, FFN, (int)M)))
-    return rc;
+  if (folded) {
+    if ((rc = launch_gemm_ln(ctx, EPI_GELU, a.x, D, w.fc_in_wg, FFN, D, w.fc_in_c, w.fc_in_d,
+                             w.fc_in_b, a.ffn, FFN, (int)M)))
+      return rc;
+  } else {
+    if ((rc = launch_layernorm(ctx, a.x, D, nullptr, (int)M, w.ln2_w, w.ln2_b, a.norm, D))) return rc;
+    if ((rc = launch_gemm(ctx, EPI_GELU, a.norm, D, w.fc_in_w, FFN, D, w.fc_in_b, a.ffn, FFN, (int)M)))
+      return rc;
+  }
   return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_w, D, FFN, w.fc_out_b, a.x, D, (int)M);
 }
 
@@ -239,7 +309,11 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
     if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
                         nullptr, false, step + 1, a)))
       return rc;
-    if ((rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
+    // the audio heads take ln_f folded in (decode-sized B); the text decision
+    // and the step probe read ln_f itself
+    const bool folded_head = pick && step > 0 && B < kFoldMaxM;
+    if (!folded_head &&
+        (rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
       return rc;
     if (!pick) continue;
     if (step == 0) {
@@ -247,9 +321,13 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
                               ctx->assistant_id, ctx->frame_alive, ctx->cont);
     } else {
       const int ch = step - 1;
-      if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr,
-                            a.logits, CODES, B)))
-        return rc;
+      if (folded_head)
+        rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, m.head_wg.t[ch], CODES, D, m.head_c.t[ch],
+                            m.head_d.t[ch], nullptr, a.logits, CODES, B);
+      else
+        rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr,
+                         a.logits, CODES, B);
+      if (rc) return rc;
       rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
                                  ctx->tokens);
     }
