@@ -420,6 +420,8 @@ def main():
                          "C=1024), c2 (prefill attention), frames (model decode frames/s); "
                          "the JSON line needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
+    ap.add_argument("--frames-n", type=int, default=0,
+                    help="frames per voice count (default: 60 at B=1, 300 otherwise)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); sequences are "
@@ -443,7 +445,8 @@ def main():
         w = synth.model_weights(n_layers=12, vocab=32000, seed=0)
         w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
-        frames = [run_frames(w, b, *plan[b]) for b in map(int, args.frames_b.split(","))]
+        frames = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1])
+                  for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "kv_attention_256_voices": voices,
                           "prefill_attention": c2, "frames_detail": frames}), flush=True)

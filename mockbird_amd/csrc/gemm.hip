@@ -202,7 +202,7 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd) {
   constexpr int MI = MT / 16;
-  __shared__ f32x4_t red[3][MI][4][64];
+  __shared__ float red[4][2][4][4][64];  // [wave][block][column block][element][lane]
   __shared__ float4 stat[LNF ? 4 : 1][MI][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, r = lane >> 4;
@@ -293,32 +293,46 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
       if (lane < 16) stat[wave][i][lane] = make_float4(sx[i], sxx[i], x0[i], 0.f);
     }
   }
-  // the four waves' sums, added in wave order
-  if (wave > 0) {
-#pragma unroll
-    for (int i = 0; i < MI; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) red[wave - 1][i][j][lane] = acc[i][j];
-  }
-  __syncthreads();
-  if (wave > 0) return;
-#pragma unroll
-  for (int q = 0; q < 3; q++)
-#pragma unroll
-    for (int i = 0; i < MI; i++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) acc[i][j] += red[q][i][j][lane];
 
+  // Add the four waves' sums and finish the tile on all four waves: the
+  // partial tiles go through LDS two 16-row blocks at a time, and wave w
+  // takes element w of every accumulator -- row 16i + 4r + w, columns
+  // n .. n+3 -- summing the waves in wave order (the same order on every run).
+  const float inv_k = 1.f / (float)(4 * kw);
+  float4 cv = make_float4(0.f, 0.f, 0.f, 0.f), dv = cv;
   if (LNF) {
-    // rows 16i + 4r + v of this lane: mean and rstd from the four quarters,
-    // then out = rstd (acc - mean c) + d (+ bias and the epilogue below)
-    const float inv_k = 1.f / (float)(4 * kw);
-    const float4 cv = *(const float4*)(lnc + n), dv = *(const float4*)(lnd + n);
+    cv = *(const float4*)(lnc + n);
+    dv = *(const float4*)(lnd + n);
+  }
+  const float4 bv = (bias && S == 1) ? *(const float4*)(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < MI; i++)
+  for (int i0 = 0; i0 < MI; i0 += 2) {
+    if (i0 > 0) __syncthreads();  // the previous group's reads are done
 #pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const int rl = 4 * r + v;
+    for (int ii = 0; ii < 2; ii++) {
+      if (i0 + ii >= MI) break;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[wave][ii][j][e][lane] = acc[i0 + ii][j][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++) {
+      const int i = i0 + ii;
+      if (i >= MI) break;
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float t = red[0][ii][j][wave][lane];
+        t += red[1][ii][j][wave][lane];
+        t += red[2][ii][j][wave][lane];
+        t += red[3][ii][j][wave][lane];
+        o[j] = t;
+      }
+      const int rl = 4 * r + wave;
+      const int row = m0 + 16 * i + rl;
+      if (LNF) {
         const float4 q0 = stat[0][i][rl], q1 = stat[1][i][rl], q2 = stat[2][i][rl], q3 = stat[3][i][rl];
         const float s1 = ((q0.x + q1.x) + q2.x) + q3.x;
         const float s2 = ((q0.y + q1.y) + q2.y) + q3.y;
@@ -326,38 +340,21 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
         const float var = fmaxf(s2 * inv_k - ms * ms, 0.f);
         const float mean = q0.z + ms;
         const float rstd = 1.f / sqrtf(var + 1e-5f);
-        acc[i][0][v] = rstd * (acc[i][0][v] - mean * cv.x) + dv.x;
-        acc[i][1][v] = rstd * (acc[i][1][v] - mean * cv.y) + dv.y;
-        acc[i][2][v] = rstd * (acc[i][2][v] - mean * cv.z) + dv.z;
-        acc[i][3][v] = rstd * (acc[i][3][v] - mean * cv.w) + dv.w;
+        o[0] = rstd * (o[0] - mean * cv.x) + dv.x;
+        o[1] = rstd * (o[1] - mean * cv.y) + dv.y;
+        o[2] = rstd * (o[2] - mean * cv.z) + dv.z;
+        o[3] = rstd * (o[3] - mean * cv.w) + dv.w;
       }
-  }
-
-  // lane holds C[m0 + 16i + 4r + v][n + j] in acc[i][j][v]
-  if (S > 1) {
-#pragma unroll
-    for (int i = 0; i < MI; i++)
-#pragma unroll
-      for (int v = 0; v < 4; v++) {
-        const int row = m0 + 16 * i + 4 * r + v;
-        if (row < M)
-          *(float4*)(part + ((int64_t)split * M + row) * N + n) =
-              make_float4(acc[i][0][v], acc[i][1][v], acc[i][2][v], acc[i][3][v]);
-      }
-    return;
-  }
-  const float4 bv = bias ? *(const float4*)(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-  for (int i = 0; i < MI; i++)
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int row = m0 + 16 * i + 4 * r + v;
       if (row >= M) continue;
-      float4 val = make_float4(acc[i][0][v] + bv.x, acc[i][1][v] + bv.y, acc[i][2][v] + bv.z,
-                               acc[i][3][v] + bv.w);
+      if (S > 1) {
+        *(float4*)(part + ((int64_t)split * M + row) * N + n) = make_float4(o[0], o[1], o[2], o[3]);
+        continue;
+      }
+      const float4 val = make_float4(o[0] + bv.x, o[1] + bv.y, o[2] + bv.z, o[3] + bv.w);
       float* cp = Cm + (int64_t)row * ldc + n;
       *(float4*)cp = epilogue4<EPI>(val, nullptr, n, cp);
     }
+  }
 }
 
 // C = epi(sum over splits of part, in split order, + bias); one float4 per thread.
