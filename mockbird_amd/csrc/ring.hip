@@ -310,18 +310,27 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
   float qv[VD];
-  // the appended row: its slot, whether this wave's range holds it, and its
-  // K and V as stored (rounded to the ring's type)
+  // The appended row: its slot and whether this wave's range holds it.  The
+  // owning wave issues its k and v loads here but ropes, rounds and stores
+  // them only in the batch that covers the slot, so the loads overlap the
+  // batches before it.
   int slot_new = -1;
   bool owner = false;
-  uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+  float ki[VD], vi[VD], cs[VD / 2], sn[VD / 2];
   if (APPEND) {
     const int64_t roff = row_at(q_rows, b, r) + head * HD + sub * VD;
     float qi[VD], qo[VD];
     load_n<IN_BF16, VD>(q, roff, qi);
     const bool have = cur >= 0 && cur <= INT32_MAX && (wrap || cur < C);
     const int32_t pos = (int32_t)(have ? cur : 0);
-    float cs[VD / 2], sn[VD / 2];
+    if (have) {
+      slot_new = wrap ? (int)(cur % C) : (int)cur;
+      owner = (slot_new >= s0 && slot_new < s1);
+    }
+    if (owner) {
+      load_n<IN_BF16, VD>(q, roff + D, ki);
+      load_n<IN_BF16, VD>(q, roff + 2 * D, vi);
+    }
 #pragma unroll
     for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
 #pragma unroll
@@ -333,24 +342,6 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
     }
 #pragma unroll
     for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
-    if (have) {
-      slot_new = wrap ? (int)(cur % C) : (int)cur;
-      owner = (slot_new >= s0 && slot_new < s1);
-    }
-    if (owner) {
-      float ki[VD], vi[VD], ko[VD];
-      load_n<IN_BF16, VD>(q, roff + D, ki);
-      load_n<IN_BF16, VD>(q, roff + 2 * D, vi);
-#pragma unroll
-      for (int j = 0; j < VD / 2; j++) rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
-      knew = pack16<KV_BF16>(ko);
-      vnew = pack16<KV_BF16>(vi);
-      if (g == 0) {
-        *(uint4*)((char*)ring_k + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = knew;
-        *(uint4*)((char*)ring_v + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = vnew;
-        if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
-      }
-    }
   } else {
     const float* qp = (const float*)q + row_at(q_rows, b, r) + head * HD + sub * VD;
 #pragma unroll
@@ -391,6 +382,16 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
       // a batch may reach past the tile end when GU does not divide TILE, and
       // the slots beyond t1 belong to the next tile
       if (APPEND && owner && slot_new >= base && slot_new < min(base + GU, t1)) {  // wave-uniform
+        float ko[VD];
+#pragma unroll
+        for (int j = 0; j < VD / 2; j++)
+          rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
+        const uint4 knew = pack16<KV_BF16>(ko), vnew = pack16<KV_BF16>(vi);
+        if (g == 0) {
+          *(uint4*)((char*)ring_k + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = knew;
+          *(uint4*)((char*)ring_v + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = vnew;
+          if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
           if (base + u * G + g == slot_new) {
