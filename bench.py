@@ -1,6 +1,6 @@
 """Benchmark of the MI355X decoder hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c1-f32]
+    python bench.py [--steps K] [--warmup W] [--legs copy,c1,voices,c4,c2,frames]
 
 Default workload (c1): the isolated KV ring append + decode attention step --
 B=64 independent sequences, 12 heads x 64, ring capacity 2048, bf16 KV
@@ -169,13 +169,13 @@ def run_c1(args, kv_name):
     return res
 
 
-def run_voices_attention(args, B=256, C=1024, frames_in=150):
-    """The KV-attention kernel at the many-voice decode shape: 256 voices,
-    ring capacity 1024, bf16 KV, 12 layer rings stepped in turn; positions are
-    the many-voice prompt lengths U[64, 400) (seed 33) plus `frames_in`
-    decoded frames, so the live windows span 214-549 slots and grow by one
-    per pass over the layers.  Each step is one fused append + attention
-    launch, timed back to back with HIP events."""
+def run_fused(args, B, C, pos0, seed, workload):
+    """Fused ring append + decode attention, bf16 KV, 12 layer rings stepped
+    in turn.  Each ring holds positions max(0, pos0 - C) .. pos0 - 1 of every
+    sequence (written through the rows append, so slots follow pos mod C); a
+    step is one mb_append_attend_dev launch at the next position, timed back
+    to back with HIP events on the stream the launches run on.  Every
+    sequence advances one position after each pass over the twelve layers."""
     import torch
 
     import mockbird_amd as mb
@@ -185,17 +185,16 @@ def run_voices_attention(args, B=256, C=1024, frames_in=150):
     ctx = mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=128, kv_dtype=mb.MB_KV_BF16)
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
-    g = np.random.default_rng(33)
-    pos0 = (g.integers(64, 400, size=B) + frames_in).astype(np.int32)
+    start = np.maximum(0, pos0 - C).astype(np.int32)
+    nfill = (pos0 - start).astype(np.int32)
     tg = torch.Generator(device=dev)
-    tg.manual_seed(11)
+    tg.manual_seed(seed)
     chunk = 128
-    zeros = np.zeros(B, np.int32)
     for layer in range(L):
-        for c0 in range(0, int(pos0.max()), chunk):
+        for c0 in range(0, int(nfill.max()), chunk):
             qkv = torch.randn((B, chunk, QKV), generator=tg, device=dev)
-            n = torch.from_numpy(np.clip(pos0 - c0, 0, chunk).astype(np.int32)).to(dev)
-            p0 = torch.from_numpy((zeros + c0).astype(np.int32)).to(dev)
+            n = torch.from_numpy(np.clip(nfill - c0, 0, chunk).astype(np.int32)).to(dev)
+            p0 = torch.from_numpy((start + c0).astype(np.int32)).to(dev)
             ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
     torch.cuda.synchronize()
     steps, warmup = args.steps, args.warmup
@@ -204,8 +203,6 @@ def run_voices_attention(args, B=256, C=1024, frames_in=150):
     qkv_l = [torch.randn((B, QKV), generator=tg, device=dev) for _ in range(L)]
     out = torch.empty((B, D), device=dev)
     max_pos = int(pos0.max()) + tokens
-    if max_pos >= C:
-        raise ValueError("positions exceed the ring")
 
     def step(s):
         layer, tok = s % L, s // L
@@ -226,10 +223,32 @@ def run_voices_attention(args, B=256, C=1024, frames_in=150):
     nbytes = np.mean([fused_bytes(pos0 + (warmup + i) // L, C, 2) for i in range(steps)])
     ctx.close()
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"workload": "fused ring append + decode attention, 256 voices, 12 x 64, ring 1024, "
-                        "bf16 KV, windows 214-549 slots, 12 layer rings in turn",
-            "avg_us": round(us, 2), "bytes_per_launch": int(nbytes), "gbs": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return {"workload": workload, "avg_us": round(us, 2), "bytes_per_launch": int(nbytes),
+            "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def run_voices_attention(args, B=256, C=1024, frames_in=150):
+    """The KV-attention kernel at the many-voice decode shape: 256 voices,
+    ring capacity 1024; positions are the many-voice prompt lengths
+    U[64, 400) (seed 33) plus `frames_in` decoded frames, so the live windows
+    span 214-549 slots and grow by one per pass over the layers."""
+    g = np.random.default_rng(33)
+    pos0 = (g.integers(64, 400, size=B) + frames_in).astype(np.int32)
+    if int(pos0.max()) + (args.warmup + args.steps) // 12 + 2 >= C:
+        raise ValueError("positions exceed the ring")
+    return run_fused(args, B, C, pos0, 11,
+                     "fused ring append + decode attention, 256 voices, 12 x 64, ring 1024, "
+                     "bf16 KV, windows 214-549 slots, 12 layer rings in turn")
+
+
+def run_c4(args, B=32, C=4096):
+    """The eviction-stress shape: 32 sequences, ring capacity 4096, every
+    ring full and wrapping (positions from 4096 on, so each append evicts the
+    position C older); every window is the full 4096 slots."""
+    pos0 = np.full(B, C, np.int32)
+    return run_fused(args, B, C, pos0, 13,
+                     "fused ring append + decode attention after wrap, 32 sequences, 12 x 64, "
+                     "ring 4096 (full windows, each append evicts), bf16 KV, 12 layer rings in turn")
 
 
 def run_c2(args):
@@ -414,11 +433,12 @@ def main():
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
-    ap.add_argument("--legs", default="copy,c1,voices,c2,frames",
+    ap.add_argument("--legs", default="copy,c1,voices,c4,c2,frames",
                     help="comma list of copy (plain 2 GiB HBM copy), c1 (append + decode "
                          "attention, 64 sequences, C=2048), voices (the same at 256 voices, "
-                         "C=1024), c2 (prefill attention), frames (model decode frames/s); "
-                         "the JSON line needs c1")
+                         "C=1024), c4 (the same at 32 sequences, C=4096, wrapped), c2 "
+                         "(prefill attention), frames (model decode frames/s); the JSON line "
+                         "needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     ap.add_argument("--frames-n", type=int, default=0,
                     help="frames per voice count (default: 60 at B=1, 300 otherwise)")
@@ -435,6 +455,7 @@ def main():
         legs.discard("frames")
     copy = run_copy() if "copy" in legs else None
     voices = run_voices_attention(args) if "voices" in legs else None
+    c4 = run_c4(args) if "c4" in legs else None
     c2 = run_c2(args) if "c2" in legs else None
     frames = None
     if "frames" in legs:
@@ -449,7 +470,8 @@ def main():
                   for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "kv_attention_256_voices": voices,
-                          "prefill_attention": c2, "frames_detail": frames}), flush=True)
+                          "kv_attention_c4_wrapped": c4, "prefill_attention": c2,
+                          "frames_detail": frames}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -494,6 +516,7 @@ def main():
             "two_launch_gbs": round(f32["unfused_gbs"], 1)},
         "hbm_copy": copy,
         "kv_attention_256_voices": voices,
+        "kv_attention_c4_wrapped": c4,
         "prefill_attention": c2,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
         "frames_detail": frames,

@@ -30,139 +30,299 @@ constexpr int QT = 64;    // query rows per workgroup
 constexpr int KPAD = 72;  // bf16 LDS row stride (144 B) to spread banks
 constexpr int FPAD = 68;  // fp32 LDS row stride (272 B)
 
+// Workgroup -> (sequence, head, query tile).  The dispatcher deals
+// consecutive workgroups round-robin to the 8 XCDs, so workgroup L lands on
+// XCD L % 8 and runs in the order L / 8 there.  Query tile t of a causal
+// prefill costs about t + 1 K/V tiles; numbering the work latest tile first,
+// all (sequence, head) pairs of one tile before the next, gives every XCD an
+// equal share of every tile length and starts the longest ones first.  (With
+// the tile index as the fastest grid coordinate, an 8-tile grid would send
+// all of tile t to one XCD.)
+__device__ __forceinline__ void work_item(int& b, int& h, int& qtile) {
+  const int64_t L = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
+  const int64_t pairs = (int64_t)gridDim.y * gridDim.z;
+  qtile = gridDim.x - 1 - (int)(L / pairs);
+  const int64_t hb = L % pairs;
+  h = (int)(hb % gridDim.y);
+  b = (int)(hb / gridDim.y);
+}
+
 __device__ __forceinline__ bool live_slot(int32_t p, int64_t cur, int C) {
   const int64_t d = cur - p;
   return p >= 0 && d >= 0 && d < C;
 }
 
-// Reduce over the four lane groups that share a query column (l%16).
+// Reduce over the four lane groups that share a query column (lanes i, i^16,
+// i^32, i^48) with the gfx950 cross-row swaps: v_permlane32_swap pairs lane
+// i with i^32 and v_permlane16_swap pairs i with i^16, both without an LDS
+// round trip.  Each step combines the two values of a pair in the same order
+// on both lanes, so all four lanes end with bit-identical results.
+template <class Op>
+__device__ __forceinline__ float col_reduce(float x, Op op) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
 __device__ __forceinline__ float col_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
+  return col_reduce(x, [](float u, float v) { return fmaxf(u, v); });
 }
 __device__ __forceinline__ float col_sum(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
+  return col_reduce(x, [](float u, float v) { return u + v; });
+}
+
+// Minimum / maximum over the 64 lanes of a wave: DPP within each row of 16
+// (quad swaps, half-row and row mirrors), then the two cross-row swaps.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+template <bool MAX>
+__device__ __forceinline__ int wave_extreme(int x) {
+  auto op = [](int u, int v) { return MAX ? max(u, v) : min(u, v); };
+  x = op(x, dpp_i<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = op(x, dpp_i<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = op(x, dpp_i<0x141>(x));  // row_half_mirror
+  x = op(x, dpp_i<0x140>(x));  // row_mirror
+  const auto a = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
+  x = op((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
+  return op((int)b[0], (int)b[1]);
 }
 
 // ---------------------------------------------------------------- bf16 MMA
 
 // Q bf16 [B][rows_max][768] (roped), K/V bf16 ring, fp32 output.
-__global__ __launch_bounds__(256) void k_flash_bf16(
+//
+// One workgroup = 128 query rows of one (sequence, head); each of its 4 waves
+// owns 32 of them as two 16-query column blocks, so every K or V^T fragment
+// read from LDS feeds two MFMAs.  Both products use v_mfma_f32_16x16x32_bf16:
+//  - scores: S^T[16 slots][16 queries] += K[16 slots][32 dims] Q^T[32 dims][16 queries];
+//  - P V:    O^T[16 dims][16 queries] += V^T[16 dims][32 slots] P^T[32 slots][16 queries].
+// For P V, lane l (g = l/16) must hold P^T for 8 slots of one query; the score
+// accumulators give it slots sb*16 + 4g + j (j < 4) of blocks sb = 2c and
+// 2c + 1, and the MFMA's k order is free, so those 8 slots are its k range.
+// V^T is stored in LDS with the slots of each 32-slot chunk c permuted the
+// same way (slot c*32 + h*16 + 4g + j at c*32 + 8g + 4h + j), so each A
+// fragment is one 16-byte LDS read.
+//
+// K/V tiles of 64 slots are double-buffered in LDS and the next tile's global
+// loads are issued before the current tile is computed; one barrier per
+// tile.  Per tile each wave classifies the slots against its 32 queries from
+// the tile's stored-position range: all in the future of every query (the
+// causal upper triangle: skipped), all live for every query (no per-slot
+// test), or mixed (the window rule per slot and query).
+constexpr int BQ = 128;  // query rows per workgroup of the bf16 kernel
+constexpr float kScoreLog2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
+constexpr int32_t kRelEmpty = 1 << 30;
+
+__device__ __forceinline__ int vt_col(int slot) {  // slot in a 64-slot tile -> V^T column
+  return (slot & 32) | ((slot & 12) << 1) | ((slot & 16) >> 2) | (slot & 3);
+}
+
+__global__ __launch_bounds__(256, 3) void k_flash_bf16(
     const uint16_t* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, const uint16_t* __restrict__ ring_k,
     const uint16_t* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
     int64_t ring_seq_stride, int C, float* __restrict__ out, Rows out_rows) {
-  __shared__ uint16_t Ks[KT * KPAD];   // [slot][dim]
-  __shared__ uint16_t Vt[HD * KPAD];   // [dim][slot]
-  __shared__ int32_t Ps[KT];
+  __shared__ __align__(16) uint16_t Ks[2][KT * KPAD];  // [slot][dim]
+  __shared__ __align__(16) uint16_t Vt[2][HD * KPAD];  // [dim][vt_col(slot)]
+  __shared__ __align__(16) int32_t Ps[2][KT];          // stored position per slot (-1: none)
+  __shared__ int32_t Pr[2][2];           // min and max of the tile's relative positions
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qcol = lane & 15, grp = lane >> 4;
-  const int b = blockIdx.z, h = blockIdx.y;
-  const int qtile = gridDim.x - 1 - blockIdx.x;  // longest (latest) tiles first
+  int b, h, qtile;
+  work_item(b, h, qtile);
   const int n = n_rows[b];
-  if (qtile * QT >= n) return;  // uniform per workgroup, before any barrier
-  const int r = qtile * QT + wave * 16 + qcol;
-  const bool qvalid = r < n;
-  const int64_t cur = qvalid ? (int64_t)pos0[b] + r : -1;
-  const int rlast = min(qtile * QT + QT, n) - 1;
-  const int64_t kv_end64 = (int64_t)pos0[b] + rlast + 1;
+  if (qtile * BQ >= n) return;  // uniform per workgroup, before any barrier
+  const int64_t p0 = pos0[b];
+  const int rw = qtile * BQ + wave * 32;  // this wave's first query row
+  const bool wave_rows = rw < n;
+  const int rlast = min(qtile * BQ + BQ, n) - 1;
+  const int64_t kv_end64 = p0 + rlast + 1;
   const int kv_end = kv_end64 < C ? (int)kv_end64 : C;
 
-  // B operand of the score MFMA: Q[r][32*kc + 8*grp + 0..7], scaled by 0.125 (exact)
-  bf16x8_t qb[2];
+  // B operands of the score MFMA: Q[row][32*kc + 8*grp + 0..7] as stored; the
+  // 1/sqrt(64) scale is applied with log2(e) in the softmax (a power of two,
+  // so the scores are the same as from a pre-scaled Q)
+  bf16x8_t qb[2][2];
 #pragma unroll
-  for (int kc = 0; kc < 2; kc++) {
-    uint4 raw = make_uint4(0, 0, 0, 0);
-    if (qvalid)
-      raw = *(const uint4*)(q + row_at(q_rows, b, r) + h * HD + kc * 32 + grp * 8);
-    float f[8];
-    unpack<true>(raw, f);
+  for (int qi = 0; qi < 2; qi++) {
+    const int r = rw + qi * 16 + qcol;
 #pragma unroll
-    for (int i = 0; i < 8; i++) qb[kc][i] = (__bf16)(f[i] * 0.125f);
+    for (int kc = 0; kc < 2; kc++) {
+      uint4 raw = make_uint4(0, 0, 0, 0);
+      if (r < n) raw = *(const uint4*)(q + row_at(q_rows, b, r) + h * HD + kc * 32 + grp * 8);
+      qb[qi][kc] = __builtin_bit_cast(bf16x8_t, raw);
+    }
   }
+  // Positions relative to the workgroup's first query, so the window test is
+  // one unsigned compare: slot positions are stored clamped to [-2^30, 2^30)
+  // and an empty slot as 2^30 (after every query); a query at relative
+  // position c sees the slot iff (unsigned)(c - rel) < C (mb_create keeps
+  // C <= 2^20, so a clamped position is outside every window, as it should be).
+  const int64_t base = p0 + (int64_t)qtile * BQ;
+  const int crel_lo = wave * 32, crel_hi = min(rw + 31, n - 1) - qtile * BQ;
+  int crel[2];
+#pragma unroll
+  for (int qi = 0; qi < 2; qi++) crel[qi] = crel_lo + qi * 16 + qcol;
   const uint16_t* kb = ring_k + (int64_t)b * ring_seq_stride + (int64_t)h * C * HD;
   const uint16_t* vb = ring_v + (int64_t)b * ring_seq_stride + (int64_t)h * C * HD;
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
-  f32x4_t acc[4];
+  // staging roles: threads 0-127 load V (4 consecutive slots x 8 dims each)
+  // and write it transposed; threads 128-255 load K (4 slots x 8 dims, rows
+  // 16 apart) in its natural layout; wave 0 also loads the slot positions
+  const bool v_role = tid < 128;
+  const int sg = tid & 15, vdc = (tid >> 4) & 7;           // V: slots 4sg.., dims 8vdc..
+  const int kt = tid - 128, ks = (kt >> 3) & 15, kdc = kt & 7;  // K: slots ks + 16i, dims 8kdc..
+  uint4 pre[4];
+  int32_t ppre = kRelEmpty;
+  auto fetch = [&](int t0) {
 #pragma unroll
-  for (int d = 0; d < 4; d++) acc[d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
-
-  for (int t0 = 0; t0 < kv_end; t0 += KT) {
-    __syncthreads();
-    // stage K [slot][dim] and V^T [dim][slot]; thread -> (slot, 8-dim chunk), 2 passes
-#pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-      const int sl = pass * 32 + (tid >> 3), dc = (tid & 7) * 8;
-      const int slot = t0 + sl;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (slot < kv_end) {
-        kv = *(const uint4*)(kb + (int64_t)slot * HD + dc);
-        vv = *(const uint4*)(vb + (int64_t)slot * HD + dc);
-      }
-      *(uint4*)(Ks + sl * KPAD + dc) = kv;
-      const uint16_t* ve = (const uint16_t*)&vv;
-#pragma unroll
-      for (int i = 0; i < 8; i++) Vt[(dc + i) * KPAD + sl] = ve[i];
+    for (int i = 0; i < 4; i++) {
+      const int slot = t0 + (v_role ? 4 * sg + i : ks + 16 * i);
+      const uint16_t* src = v_role ? vb + (int64_t)slot * HD + vdc * 8 : kb + (int64_t)slot * HD + kdc * 8;
+      pre[i] = slot < kv_end ? *(const uint4*)src : make_uint4(0, 0, 0, 0);
     }
-    if (tid < KT) Ps[tid] = (t0 + tid < kv_end) ? sp[t0 + tid] : -1;
-    __syncthreads();
+    if (wave == 0) {
+      const int32_t p = t0 + lane < kv_end ? sp[t0 + lane] : -1;
+      const int64_t d = (int64_t)p - base;
+      ppre = p < 0 ? kRelEmpty : (int32_t)(d < -kRelEmpty ? -kRelEmpty : d >= kRelEmpty ? kRelEmpty - 1 : d);
+    }
+  };
 
-    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = this lane's query
-    float s[4][4];
-    float mt = -INFINITY;
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int qi = 0; qi < 2; qi++)
+#pragma unroll
+    for (int d = 0; d < 4; d++) acc[qi][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t lsum[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+  float m[2] = {-INFINITY, -INFINITY};
+  bf16x8_t ones;
+#pragma unroll
+  for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.f;
+
+  fetch(0);
+  int buf = 0;
+  for (int t0 = 0; t0 < kv_end; t0 += KT, buf ^= 1) {
+    // the buffer written here was last read two tiles ago, before the
+    // previous barrier
+    if (v_role) {
+      const uint32_t* w = (const uint32_t*)pre;  // w[4 j + k]: slot 4sg + j, dims 2k, 2k + 1
+      uint16_t* dst = &Vt[buf][vdc * 8 * KPAD + vt_col(4 * sg)];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        // v_perm_b32 byte selectors: low halves of (a, b) -> b.lo | a.lo << 16,
+        // high halves -> b.hi | a.hi << 16
+        const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+        const int k = i >> 1;
+        *(uint2*)(dst + i * KPAD) = make_uint2(__builtin_amdgcn_perm(w[4 + k], w[k], sel),
+                                               __builtin_amdgcn_perm(w[12 + k], w[8 + k], sel));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) *(uint4*)&Ks[buf][(ks + 16 * i) * KPAD + kdc * 8] = pre[i];
+    }
+    if (wave == 0) {
+      Ps[buf][lane] = ppre;
+      const int lo = wave_extreme<false>(ppre);
+      const int hi = wave_extreme<true>(ppre);
+      if (lane == 0) {
+        Pr[buf][0] = lo;
+        Pr[buf][1] = hi;
+      }
+    }
+    __syncthreads();
+    if (t0 + KT < kv_end) fetch(t0 + KT);
+    if (!wave_rows) continue;
+    const int lo = Pr[buf][0], hi = Pr[buf][1];
+    if (lo > crel_hi) continue;  // every stored position is after every query here
+    const bool all_live = hi <= crel_lo && crel_hi - lo < C;
+
+    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
+    f32x4_t s[2][4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++) {
-      f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+      s[0][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      s[1][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 2; kc++) {
-        const bf16x8_t a = *(const bf16x8_t*)(Ks + (sb * 16 + qcol) * KPAD + kc * 32 + grp * 8);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[kc], c, 0, 0, 0);
-      }
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const bool ok = live_slot(Ps[sb * 16 + grp * 4 + j], cur, C);
-        s[sb][j] = ok ? c[j] : -INFINITY;
-        mt = fmaxf(mt, s[sb][j]);
+        const bf16x8_t a = *(const bf16x8_t*)&Ks[buf][(sb * 16 + qcol) * KPAD + kc * 32 + grp * 8];
+        s[0][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[0][kc], s[0][sb], 0, 0, 0);
+        s[1][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[1][kc], s[1][sb], 0, 0, 0);
       }
     }
-    mt = col_max(mt);
-    const float mn = fmaxf(m, mt);
-    const float mu = mn == -INFINITY ? 0.f : mn;
-    const float scale = __expf(m - mu);
-    float ls = 0.f;
-    i16x4_t pb[4];
+    if (!all_live) {
 #pragma unroll
-    for (int sb = 0; sb < 4; sb++)
+      for (int sb = 0; sb < 4; sb++) {
+        const int4 pv = *(const int4*)&Ps[buf][sb * 16 + grp * 4];
+        const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float p = __expf(s[sb][j] - mu);
-        const __bf16 pbf = (__bf16)p;
-        ls += (float)pbf;  // the sum uses the same rounded weights the MMA sees
-        pb[sb][j] = __builtin_bit_cast(short, pbf);
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int qi = 0; qi < 2; qi++)
+            if ((unsigned)(crel[qi] - pj[j]) >= (unsigned)C) s[qi][sb][j] = -INFINITY;
       }
-    l = l * scale + col_sum(ls);
-    m = mn;
+    }
+    // Online softmax in log2 units.  The running maximum m only moves when a
+    // tile's maximum exceeds it by more than 8 (the conditional rescaling of
+    // FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
+    // rescale of the accumulators, a wave-uniform branch, is rare after the
+    // first tiles.  The result is the same softmax: acc and the weight sum
+    // always share one m.
+    bf16x8_t pb[2][2];
 #pragma unroll
-    for (int d = 0; d < 4; d++) acc[d] *= scale;
-    // O^T[d-block] += V^T[d-block rows][slots] * P^T[slots][queries]
+    for (int qi = 0; qi < 2; qi++) {
+      float mt = -INFINITY;
 #pragma unroll
-    for (int sb = 0; sb < 4; sb++)
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) mt = fmaxf(mt, s[qi][sb][j]);
+      mt = col_max(mt) * kScoreLog2;
+      const bool grow = mt > m[qi] + 8.f;
+      if (__ballot(grow)) {
+        const float mn = grow ? mt : m[qi];
+        const float scale = grow ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
+        m[qi] = mn;
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
+        lsum[qi] *= scale;
+      }
+      const float mu = m[qi] == -INFINITY ? 0.f : m[qi];
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, -mu));
+    }
+    // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those slots][queries];
+    // the weight sum is one more MFMA with an all-ones A, so it adds the same
+    // rounded weights the products use
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        const i16x4_t a = *(const i16x4_t*)(Vt + (d * 16 + qcol) * KPAD + sb * 16 + grp * 4);
-        acc[d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, pb[sb], acc[d], 0, 0, 0);
+        const bf16x8_t a = *(const bf16x8_t*)&Vt[buf][(d * 16 + qcol) * KPAD + c * 32 + grp * 8];
+        acc[0][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][c], acc[0][d], 0, 0, 0);
+        acc[1][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][c], acc[1][d], 0, 0, 0);
       }
+      lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0][c], lsum[0], 0, 0, 0);
+      lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1][c], lsum[1], 0, 0, 0);
+    }
   }
-  if (!qvalid) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  float* op = out + row_at(out_rows, b, r) + h * HD;
 #pragma unroll
-  for (int d = 0; d < 4; d++)
-    *(float4*)(op + d * 16 + grp * 4) =
-        make_float4(acc[d][0] * inv, acc[d][1] * inv, acc[d][2] * inv, acc[d][3] * inv);
+  for (int qi = 0; qi < 2; qi++) {
+    const int r = rw + qi * 16 + qcol;
+    if (r >= n) continue;
+    const float l = lsum[qi][0];
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    float* op = out + row_at(out_rows, b, r) + h * HD;
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+      *(float4*)(op + d * 16 + grp * 4) = make_float4(acc[qi][d][0] * inv, acc[qi][d][1] * inv,
+                                                      acc[qi][d][2] * inv, acc[qi][d][3] * inv);
+  }
 }
 
 // ---------------------------------------------------------------- fp32 MMA
@@ -184,8 +344,8 @@ __global__ __launch_bounds__(256) void k_flash_f32(
   __shared__ int32_t Ps[KT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qcol = lane & 15, grp = lane >> 4;
-  const int b = blockIdx.z, h = blockIdx.y;
-  const int qtile = gridDim.x - 1 - blockIdx.x;
+  int b, h, qtile;
+  work_item(b, h, qtile);
   const int n = n_rows[b];
   if (qtile * QT >= n) return;
   const int r = qtile * QT + wave * 16 + qcol;
@@ -302,7 +462,8 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
   if (B == 0 || rows_max == 0) return MB_OK;
   dim3 grid((unsigned)((rows_max + QT - 1) / QT), H, (unsigned)B);
   if (q_dtype == MB_DT_BF16)
-    hipLaunchKernelGGL(k_flash_bf16, grid, dim3(256), 0, ctx->stream, (const uint16_t*)q, q_rows,
+    hipLaunchKernelGGL(k_flash_bf16, dim3((unsigned)((rows_max + BQ - 1) / BQ), H, (unsigned)B),
+                       dim3(256), 0, ctx->stream, (const uint16_t*)q, q_rows,
                        pos0, n_rows, (const uint16_t*)ring.k, (const uint16_t*)ring.v, ring.sp,
                        ring.seq_stride, ring.C, out, out_rows);
   else if (ring.bf16)
