@@ -56,7 +56,7 @@ enum {
 enum { MB_KV_F32 = 0, MB_KV_BF16 = 1 };
 enum { MB_DT_F32 = 0, MB_DT_BF16 = 1 };
 /* Epilogues of mb_linear_dev. */
-enum { MB_EPI_STORE = 0, MB_EPI_GELU = 1, MB_EPI_ADD = 2 };
+enum { MB_EPI_STORE = 0, MB_EPI_GELU = 1, MB_EPI_ADD = 2, MB_EPI_SCALE_ADD = 3, MB_EPI_GELU_ERF = 4 };
 
 typedef struct mb_config {
   int32_t n_layers;   /* global transformer layers (12) */
@@ -189,12 +189,15 @@ int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv
  *   C[M][N] = epi(A[M][K] * W[K][N] + bias[N])
  * W row-major [K, N] as the exported graph stores its MatMul initialisers;
  * bias may be NULL; epi MB_EPI_STORE writes, MB_EPI_GELU applies gelu-tanh,
- * MB_EPI_ADD adds into C (the residual).  fp32 products and accumulation.
- * Needs N % 64 == 0, K % 128 == 0, lda and ldc multiples of 4 and 16-byte
- * aligned pointers.  Replaces GEMM_NT (kernels-batch.ts:156-184, called
- * prefill.ts:404-422, :464-482) and GEMV (kernels-decode.ts:127-142, called
- * decode.ts:517-526, :553-562) with the GELU_TANH / ADD_RESIDUAL passes
- * that follow them (kernels-decode.ts:330-340, :373-385) fused in. */
+ * MB_EPI_ADD adds into C (the residual), MB_EPI_GELU_ERF applies the exact
+ * (erf) GELU, and MB_EPI_SCALE_ADD reads `bias` as a per-column scale s and
+ * stores C + s * (A W) (the codec's layer scale).  fp32 products and
+ * accumulation.  Needs N % 64 == 0, K % 64 == 0, lda and ldc multiples of 4
+ * and 16-byte aligned pointers.  Replaces GEMM_NT (kernels-batch.ts:156-184,
+ * called prefill.ts:404-422, :464-482), GEMV / GEMV_NOB (kernels-decode.ts:
+ * 127-166, called decode.ts:517-526, :553-562, codec.ts:536-735) with the
+ * GELU_TANH / GELU_ERF / ADD_RESIDUAL / LAYER_SCALE_ADD passes that follow
+ * them (kernels-decode.ts:330-415) fused in. */
 int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda, const float* W,
                   const float* bias, float* C, int64_t ldc, int epi);
 
@@ -286,6 +289,75 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
  * decodeStep at prompt_rows + step) for many voices in one call. */
 int mb_decode_frames(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
                      int32_t* codes, int32_t* cont);
+
+/* ------------------------------------------------------------ the codec
+ *
+ * The streaming codec decoder (codec.ts:1-30): 16 RVQ codes per 12.5 Hz
+ * frame -> 3840 stereo samples at 48 kHz, for up to max_voices independent
+ * voices per call.  Per frame: the RVQ front (16 codebook gathers through
+ * the per-quantiser 1x1 convolutions, then the [768,512] output projection,
+ * interleaved x4 into 4 positions of 192), four transformer stages of
+ * d = 256 (4 heads of 64) over 4, 8, 16, 32 positions, each with its own
+ * wrapping ring per layer keyed by absolute position (the window rule of
+ * ATTEND_RING_CODEC, kernels-decode.ts:590-667), an x2 sub-pixel upsample
+ * between stages, and the head that lays the 240-wide latent out as PCM.
+ *
+ * Weights are uploaded with mb_upload_tensor under these names ([K, N]
+ * row-major as the graph's MatMul initialisers hold them, which the
+ * reference finds by shape and offset order, decodeWeights.ts:69-156):
+ *   model.quantizer.quantizers.{k}.out_proj.weight   [512, 8] (or [512, 8, 1])
+ *   model.quantizer.quantizers.{k}.out_proj.bias     [512]
+ *   model.quantizer.quantizers.{k}.codebook.weight   [1024, 8]
+ *   model.quantizer.output_proj.weight               [768, 512] (or [768, 512, 1])
+ *   model.quantizer.output_proj.bias                 [768]
+ * and for stage s = 0..3, ds = 1, 3, 5, 7, layer i:
+ *   model.decoder.{ds}.input_proj.weight             [192 | 384, 256]
+ *   model.decoder.{ds}.output_proj.weight            [256, 768] (s < 3) | [256, 240]
+ *   model.decoder.{ds}.transformer.layers.{i}.self_attn.in_proj.weight   [256, 768]
+ *   model.decoder.{ds}.transformer.layers.{i}.self_attn.out_proj.weight  [256, 256]
+ *   model.decoder.{ds}.transformer.layers.{i}.ffn.0.weight               [256, 1024]
+ *   model.decoder.{ds}.transformer.layers.{i}.ffn.2.weight               [1024, 256]
+ *   model.decoder.{ds}.transformer.layers.{i}.norm1.weight / .bias        [256]
+ *   model.decoder.{ds}.transformer.layers.{i}.norm2.weight / .bias        [256]
+ *   model.decoder.{ds}.transformer.layers.{i}.layer_scale_1.scale         [256]
+ *   model.decoder.{ds}.transformer.layers.{i}.layer_scale_2.scale         [256]
+ */
+typedef struct mb_codec_config {
+  int32_t max_voices; /* voices decoded together (rings and buffers sized for them) */
+  int32_t kv_dtype;   /* MB_KV_F32 or MB_KV_BF16 for the codec rings */
+  int32_t layers[4];  /* transformer layers per stage: 4, 2, 2, 4 */
+  int32_t context[4]; /* ring window per stage in positions: 500, 1696, 2480, 3248 */
+} mb_codec_config;
+
+/* Allocate the codec's rings and buffers on this context (again: frees the
+ * previous ones).  Every voice starts empty at position 0 of every stage.
+ * Replaces the CodecRunner constructor (codec.ts:198-262). */
+int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg);
+
+/* A fresh utterance for `n` voices (n < 0: all): every ring slot reads as
+ * empty and every stage restarts at position 0 (CodecRunner.resetRings,
+ * codec.ts:265-269). */
+int mb_codec_reset(mb_ctx* ctx, int n, const int32_t* voices);
+
+/* Decode n_frames frames for voices b < B, continuing each voice's rings:
+ * codes [n_frames][B][16] in [0, 1024) -> pcm [B][2][n_frames * 3840]
+ * (per voice, left channel then right, frames in order).  Host pointers;
+ * synchronises before returning.  Replaces CodecRunner.decodeFrames
+ * (codec.ts:766-813) for many voices at once. */
+int mb_codec_decode(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm);
+
+/* Device-pointer form of mb_codec_decode (codes and pcm in device memory;
+ * a code outside [0, 1024) contributes no codebook row).  Enqueue only. */
+int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm);
+
+/* Parity read-back of one codec layer's ring for one voice (layers numbered
+ * across stages, 0 .. sum(layers) - 1): k and v [slots][256] in the
+ * reference's [slot][head * 64 + dim] order, slot_pos [slots]; *slots
+ * receives the ring's slot count (its window plus the stage's positions per
+ * frame, so that a frame's positions are appended before they are
+ * attended).  Any output may be NULL.  Synchronises. */
+int mb_codec_read_ring(mb_ctx* ctx, int layer, int voice, float* k, float* v, int32_t* slot_pos,
+                       int32_t* slots);
 
 #ifdef __cplusplus
 }

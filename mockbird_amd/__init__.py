@@ -19,7 +19,9 @@ LIB_PATH = os.path.join(PKG, "libmockbird_hip.so")
 MB_OK, MB_ERR_ARG, MB_ERR_RANGE, MB_ERR_HIP, MB_ERR_STATE, MB_ERR_CANCELLED, MB_ERR_NOMEM = range(7)
 MB_KV_F32, MB_KV_BF16 = 0, 1
 MB_DT_F32, MB_DT_BF16 = 0, 1
-MB_EPI_STORE, MB_EPI_GELU, MB_EPI_ADD = 0, 1, 2
+MB_EPI_STORE, MB_EPI_GELU, MB_EPI_ADD, MB_EPI_SCALE_ADD, MB_EPI_GELU_ERF = 0, 1, 2, 3, 4
+#: the codec decoder's shape (codec.ts:1-30)
+CODEC_LAYERS, CODEC_CONTEXT, CODEC_SAMPLES = (4, 2, 2, 4), (500, 1696, 2480, 3248), 3840
 D, H, HD, QKV, FFN, NVQ, ROW, PAD, CODES = 768, 12, 64, 2304, 3072, 16, 17, 1024, 1024
 
 #: every symbol include/mockbird_hip.h declares (checked by the CPU tests)
@@ -32,7 +34,8 @@ EXPORTS = (
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
     "mb_linear_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
-    "mb_append_attend_dev",
+    "mb_append_attend_dev", "mb_codec_init", "mb_codec_reset", "mb_codec_decode",
+    "mb_codec_decode_dev", "mb_codec_read_ring",
 )
 
 
@@ -48,6 +51,11 @@ class Config(C.Structure):
         ("max_seqs", C.c_int32), ("max_rows", C.c_int32), ("kv_dtype", C.c_int32),
         ("wrap", C.c_int32), ("device", C.c_int32),
     ]
+
+
+class CodecConfig(C.Structure):
+    _fields_ = [("max_voices", C.c_int32), ("kv_dtype", C.c_int32),
+                ("layers", C.c_int32 * 4), ("context", C.c_int32 * 4)]
 
 
 _lib = None
@@ -114,6 +122,11 @@ def load():
         "mb_append_attend": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
         "mb_append_attend_dev": ([_vp, C.c_int, C.c_int, _vp, C.c_int, _i64, _vp, _i32, _vp, _i64,
                                   _vp, _i64], C.c_int),
+        "mb_codec_init": ([_vp, C.POINTER(CodecConfig)], C.c_int),
+        "mb_codec_reset": ([_vp, C.c_int, _vp], C.c_int),
+        "mb_codec_decode": ([_vp, C.c_int, C.c_int, _vp, _vp], C.c_int),
+        "mb_codec_decode_dev": ([_vp, C.c_int, C.c_int, _vp, _vp], C.c_int),
+        "mb_codec_read_ring": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -284,6 +297,43 @@ class Context:
                               q_dtype=MB_DT_F32):
         self.check(self.lib.mb_prefill_attention_dev(self.h, layer, B, rows_max, q_ptr, q_dtype,
                                                      pos0_ptr, n_ptr, out_ptr))
+
+    # -- the codec decoder
+    def codec_init(self, max_voices: int, layers=CODEC_LAYERS, context=CODEC_CONTEXT,
+                   kv_dtype: int = MB_KV_F32):
+        cfg = CodecConfig(max_voices, kv_dtype, (C.c_int32 * 4)(*layers),
+                          (C.c_int32 * 4)(*context))
+        self.check(self.lib.mb_codec_init(self.h, C.byref(cfg)))
+        self.codec_layers, self.codec_context = tuple(layers), tuple(context)
+
+    def codec_reset(self, voices=None):
+        if voices is None:
+            self.check(self.lib.mb_codec_reset(self.h, -1, None))
+        else:
+            v = _i32c(voices)
+            self.check(self.lib.mb_codec_reset(self.h, v.size, _ptr(v)))
+
+    def codec_decode(self, codes: np.ndarray) -> np.ndarray:
+        """codes [n_frames][B][16] -> pcm [B][2][n_frames * 3840]."""
+        codes = _i32c(codes)
+        n, B = codes.shape[0], codes.shape[1]
+        pcm = np.zeros((B, 2, n * CODEC_SAMPLES), np.float32)
+        self.check(self.lib.mb_codec_decode(self.h, B, n, _ptr(codes), _ptr(pcm)))
+        return pcm
+
+    def codec_decode_dev(self, B, n_frames, codes_ptr, pcm_ptr):
+        self.check(self.lib.mb_codec_decode_dev(self.h, B, n_frames, codes_ptr, pcm_ptr))
+
+    def codec_read_ring(self, layer: int, voice: int):
+        """(k [slots][256], v [slots][256], slot_pos [slots]) of one codec layer and voice."""
+        n = C.c_int32(0)
+        self.check(self.lib.mb_codec_read_ring(self.h, layer, voice, None, None, None, C.byref(n)))
+        k = np.zeros((n.value, 256), np.float32)
+        v = np.zeros((n.value, 256), np.float32)
+        sp = np.zeros(n.value, np.int32)
+        self.check(self.lib.mb_codec_read_ring(self.h, layer, voice, _ptr(k), _ptr(v), _ptr(sp),
+                                               None))
+        return k, v, sp
 
     def decode_frames_dev(self, B, n_frames, hidden_ptr, pos_ptr, max_pos, codes_ptr, cont_ptr):
         self.check(self.lib.mb_decode_frames_dev(self.h, B, n_frames, hidden_ptr, pos_ptr, max_pos,

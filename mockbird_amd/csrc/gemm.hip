@@ -13,6 +13,8 @@
 // covers k = 4g .. 4g+3 of the slice; the sum over the slice is the same
 // product in a different order).  The next slice's global loads are issued
 // before the current slice's MFMAs.
+#include <type_traits>
+
 #include "mb_internal.h"
 
 namespace mb {
@@ -30,6 +32,34 @@ constexpr int GPAD = 20;  // LDS row stride in floats (16 + 4)
 __device__ __forceinline__ float gelu_tanh(float v) {
   const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
   return v / (1.f + __expf(-2.f * u));
+}
+
+// Exact GELU 0.5 v (1 + erf(v / sqrt 2)), the codec decoder's activation,
+// with erf from Abramowitz & Stegun 7.1.26 (|error| <= 1.5e-7), the form
+// GELU_ERF evaluates (kernels-decode.ts:392-415).
+__device__ __forceinline__ float erf_as(float x) {
+  const float sgn = x >= 0.f ? 1.f : -1.f;
+  const float ax = fabsf(x);
+  const float t = 1.f / (1.f + 0.3275911f * ax);
+  const float poly =
+      ((((1.061405429f * t + -1.453152027f) * t + 1.421413741f) * t + -0.284496736f) * t +
+       0.254829592f) * t;
+  return sgn * (1.f - poly * expf(-ax * ax));
+}
+__device__ __forceinline__ float gelu_erf(float v) {
+  return 0.5f * v * (1.f + erf_as(v * 0.7071067811865476f));
+}
+
+// Compile-time epilogue dispatch: f(std::integral_constant<int, EPI>{}).
+template <class F>
+static void with_epi(int epi, F f) {
+  switch (epi) {
+    case EPI_GELU: f(std::integral_constant<int, EPI_GELU>{}); break;
+    case EPI_ADD: f(std::integral_constant<int, EPI_ADD>{}); break;
+    case EPI_SCALE_ADD: f(std::integral_constant<int, EPI_SCALE_ADD>{}); break;
+    case EPI_GELU_ERF: f(std::integral_constant<int, EPI_GELU_ERF>{}); break;
+    default: f(std::integral_constant<int, EPI_STORE>{}); break;
+  }
 }
 
 template <int TM, int TN, int EPI>
@@ -119,15 +149,21 @@ __global__ __launch_bounds__(256) void k_gemm(const float* __restrict__ A, int64
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int col = n0 + (wn * TN + j) * 16 + col16;
-      const float bv = bias ? bias[col] : 0.f;
+      const float bv = bias ? bias[col] : 0.f;  // the scale for EPI_SCALE_ADD
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int row = m0 + (wm * TM + i) * 16 + g * 4 + r;
         if (row >= M) continue;
-        float v = acc[i][j][r] + bv;
         float* cp = Cm + (int64_t)row * ldc + col;
-        if (EPI == EPI_GELU) v = gelu_tanh(v);
-        if (EPI == EPI_ADD) v = *cp + v;
+        float v;
+        if (EPI == EPI_SCALE_ADD) {
+          v = *cp + bv * acc[i][j][r];
+        } else {
+          v = acc[i][j][r] + bv;
+          if (EPI == EPI_GELU) v = gelu_tanh(v);
+          if (EPI == EPI_GELU_ERF) v = gelu_erf(v);
+          if (EPI == EPI_ADD) v = *cp + v;
+        }
         *cp = v;
       }
     }
@@ -138,15 +174,10 @@ static void gemm_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const
                         int K, const float* bias, float* Cm, int64_t ldc, int M) {
   constexpr int BM = 2 * TM * 16, BN = 2 * TN * 16;
   dim3 grid((unsigned)(N / BN), (unsigned)((M + BM - 1) / BM));
-  if (epi == EPI_GELU)
-    hipLaunchKernelGGL((k_gemm<TM, TN, EPI_GELU>), grid, dim3(256), 0, ctx->stream, A, lda, W, N, K,
-                       bias, Cm, ldc, M);
-  else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemm<TM, TN, EPI_ADD>), grid, dim3(256), 0, ctx->stream, A, lda, W, N, K,
-                       bias, Cm, ldc, M);
-  else
-    hipLaunchKernelGGL((k_gemm<TM, TN, EPI_STORE>), grid, dim3(256), 0, ctx->stream, A, lda, W, N,
-                       K, bias, Cm, ldc, M);
+  with_epi(epi, [&](auto e) {
+    hipLaunchKernelGGL((k_gemm<TM, TN, decltype(e)::value>), grid, dim3(256), 0, ctx->stream, A,
+                       lda, W, N, K, bias, Cm, ldc, M);
+  });
 }
 
 // ---------------------------------------------------------------------------
@@ -174,12 +205,19 @@ constexpr int kStreamMaxSplit = 8;
 template <int EPI>
 __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ bias, int n,
                                             const float* cp) {
+  if (EPI == EPI_SCALE_ADD) {  // bias holds the per-column scale
+    const float4 c = *(const float4*)cp, sc = *(const float4*)(bias + n);
+    return make_float4(c.x + sc.x * v.x, c.y + sc.y * v.y, c.z + sc.z * v.z, c.w + sc.w * v.w);
+  }
   if (bias) {
     const float4 b = *(const float4*)(bias + n);
     v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
   }
   if (EPI == EPI_GELU) {
     v.x = gelu_tanh(v.x); v.y = gelu_tanh(v.y); v.z = gelu_tanh(v.z); v.w = gelu_tanh(v.w);
+  }
+  if (EPI == EPI_GELU_ERF) {
+    v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
   }
   if (EPI == EPI_ADD) {
     const float4 c = *(const float4*)cp;
@@ -304,7 +342,6 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     cv = *(const float4*)(lnc + n);
     dv = *(const float4*)(lnd + n);
   }
-  const float4 bv = (bias && S == 1) ? *(const float4*)(bias + n) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int i0 = 0; i0 < MI; i0 += 2) {
     if (i0 > 0) __syncthreads();  // the previous group's reads are done
@@ -350,9 +387,8 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
         *(float4*)(part + ((int64_t)split * M + row) * N + n) = make_float4(o[0], o[1], o[2], o[3]);
         continue;
       }
-      const float4 val = make_float4(o[0] + bv.x, o[1] + bv.y, o[2] + bv.z, o[3] + bv.w);
       float* cp = Cm + (int64_t)row * ldc + n;
-      *(float4*)cp = epilogue4<EPI>(val, nullptr, n, cp);
+      *(float4*)cp = epilogue4<EPI>(make_float4(o[0], o[1], o[2], o[3]), bias, n, cp);
     }
   }
 }
@@ -399,26 +435,20 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   }
   dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
   const int kw = K / (4 * S);
-  if (epi == EPI_GELU)
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_GELU, LNF>), grid, dim3(256), 0, ctx->stream, A,
-                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
-  else if (epi == EPI_ADD)
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_ADD, LNF>), grid, dim3(256), 0, ctx->stream, A,
-                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
-  else
-    hipLaunchKernelGGL((k_gemm_stream<MT, ST, EPI_STORE, LNF>), grid, dim3(256), 0, ctx->stream, A,
-                       lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+  if (LNF && epi != EPI_STORE && epi != EPI_GELU)
+    return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    if constexpr (!LNF || E == EPI_STORE || E == EPI_GELU)
+      hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, LNF>), grid, dim3(256), 0, ctx->stream, A, lda,
+                         W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+  });
   if (S > 1) {
     const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
-    if (epi == EPI_GELU)
-      hipLaunchKernelGGL(k_gemm_reduce<EPI_GELU>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M,
-                         N, bias, Cm, ldc);
-    else if (epi == EPI_ADD)
-      hipLaunchKernelGGL(k_gemm_reduce<EPI_ADD>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M, N,
-                         bias, Cm, ldc);
-    else
-      hipLaunchKernelGGL(k_gemm_reduce<EPI_STORE>, dim3(rb), dim3(256), 0, ctx->stream, part, S, M,
-                         N, bias, Cm, ldc);
+    with_epi(epi, [&](auto e) {
+      hipLaunchKernelGGL(k_gemm_reduce<decltype(e)::value>, dim3(rb), dim3(256), 0, ctx->stream,
+                         part, S, M, N, bias, Cm, ldc);
+    });
   }
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
@@ -512,7 +542,7 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M) {
   if (M <= 0) return MB_OK;
-  if (N % 64 || K % 128 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
+  if (N % 64 || K % 64 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
   if (M < kStreamMaxM) {

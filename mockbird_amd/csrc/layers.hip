@@ -7,43 +7,46 @@ namespace mb {
 
 // ---------------------------------------------------------------- LayerNorm
 
-// One wave per row of 768 (12 values per lane): mean, then the centred
-// second moment, eps 1e-5, y = (x - mean) * rsqrt * w + b
-// (LAYERNORM_ROWS, kernels-batch.ts:99-147; ref-decode.mjs:85-99).
+// One wave per row of WIDTH = 256 * NV (the model's 768, the codec's 256;
+// 4 NV values per lane): mean, then the centred second moment, eps 1e-5,
+// y = (x - mean) * rsqrt * w + b (LAYERNORM_ROWS, kernels-batch.ts:99-147;
+// LAYERNORM_1, kernels-decode.ts:168-202; ref-decode.mjs:85-99).
 // src_row (optional) maps output row i to input row src_row[i].
+template <int NV>
 __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, int64_t ldx,
                                                    const int32_t* __restrict__ src_row, int M,
                                                    const float* __restrict__ w,
                                                    const float* __restrict__ bb,
                                                    float* __restrict__ y, int64_t ldy) {
+  constexpr float kInvW = 1.f / (256.f * NV);
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= M) return;
   const float* xr = x + (int64_t)(src_row ? src_row[row] : row) * ldx;
-  float v[12];
+  float v[4 * NV];
 #pragma unroll
-  for (int i = 0; i < 3; i++) {
+  for (int i = 0; i < NV; i++) {
     const float4 t = *(const float4*)(xr + i * 256 + lane * 4);
     v[i * 4] = t.x; v[i * 4 + 1] = t.y; v[i * 4 + 2] = t.z; v[i * 4 + 3] = t.w;
   }
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 12; i++) s += v[i];
+  for (int i = 0; i < 4 * NV; i++) s += v[i];
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
-  const float mean = s * (1.f / 768.f);
+  const float mean = s * kInvW;
   float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < 12; i++) {
+  for (int i = 0; i < 4 * NV; i++) {
     const float d = v[i] - mean;
     q = fmaf(d, d, q);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
-  const float inv = 1.f / sqrtf(q * (1.f / 768.f) + 1e-5f);
+  const float inv = 1.f / sqrtf(q * kInvW + 1e-5f);
   float* yr = y + (int64_t)row * ldy;
 #pragma unroll
-  for (int i = 0; i < 3; i++) {
+  for (int i = 0; i < NV; i++) {
     const int c = i * 256 + lane * 4;
     const float4 ww = *(const float4*)(w + c), bv = *(const float4*)(bb + c);
     *(float4*)(yr + c) = make_float4((v[i * 4] - mean) * inv * ww.x + bv.x,
@@ -54,10 +57,17 @@ __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ x, 
 }
 
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,
-                     const float* w, const float* b, float* y, int64_t ldy) {
+                     const float* w, const float* b, float* y, int64_t ldy, int width) {
   if (M <= 0) return MB_OK;
-  hipLaunchKernelGGL(k_layernorm, dim3((unsigned)((M + 3) / 4)), dim3(256), 0, ctx->stream, x, ldx,
-                     src_row, M, w, b, y, ldy);
+  const dim3 grid((unsigned)((M + 3) / 4));
+  if (width == D)
+    hipLaunchKernelGGL(k_layernorm<3>, grid, dim3(256), 0, ctx->stream, x, ldx, src_row, M, w, b,
+                       y, ldy);
+  else if (width == 256)
+    hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(256), 0, ctx->stream, x, ldx, src_row, M, w, b,
+                       y, ldy);
+  else
+    return fail(ctx, MB_ERR_ARG, "LayerNorm over rows of %d is not built", width);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

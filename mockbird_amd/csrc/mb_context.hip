@@ -1,12 +1,52 @@
 // Context lifetime, errors, weights, ring bookkeeping and the host-pointer
 // entry points of the C ABI (include/mockbird_hip.h).  Kernels live in
 // ring.hip; this file only allocates, validates, stages and launches.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
 #include "mb_internal.h"
 
 namespace mb {
+
+const DeviceTensor* find(mb_ctx* ctx, const std::string& name, std::initializer_list<int64_t> dims,
+                         std::string& missing) {
+  auto it = ctx->weights.find(name);
+  if (it == ctx->weights.end()) {
+    if (missing.empty()) missing = "weight not uploaded: " + name;
+    return nullptr;
+  }
+  const DeviceTensor& t = it->second;
+  if (t.dims.size() != dims.size() || !std::equal(dims.begin(), dims.end(), t.dims.begin())) {
+    if (missing.empty()) missing = "weight has the wrong shape: " + name;
+    return nullptr;
+  }
+  return &t;
+}
+
+// A device tensor owned by the context under an internal name (freed with
+// the uploaded weights); reallocated only when its size changes.
+float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel) {
+  DeviceTensor& t = ctx->weights[name];
+  if (t.ptr && t.numel != numel) {
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipFree(t.ptr);
+    ctx->device_bytes -= t.numel * 4;
+    t.ptr = nullptr;
+  }
+  if (!t.ptr) {
+    if (hipMalloc(&t.ptr, (size_t)numel * 4) != hipSuccess) {
+      ctx->weights.erase(name);
+      return nullptr;
+    }
+    ctx->device_bytes += numel * 4;
+    ctx->graph_gen++;
+  }
+  t.numel = numel;
+  t.dims = {numel};
+  return t.ptr;
+}
+
 
 int fail(mb_ctx* ctx, int code, const char* fmt, ...) {
   if (ctx) {
@@ -176,6 +216,7 @@ void mb_destroy(mb_ctx* ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  mb::codec_free(ctx);
   for (auto& kv : ctx->weights) (void)hipFree(kv.second.ptr);
   for (auto& kv : ctx->scratch) (void)hipFree(kv.second.ptr);
   (void)hipFree(ctx->ring_k);
@@ -246,6 +287,7 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
   t.numel = numel;
   t.dims.assign(dims, dims + ndims);
   ctx->model_ok = false;
+  ctx->codec_ok = false;
   ctx->graph_gen++;
   MB_HIP(ctx, hipMemcpyAsync(t.ptr, data, (size_t)numel * 4, hipMemcpyHostToDevice, ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -420,8 +462,9 @@ int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
                   const float* bias, float* C, int64_t ldc, int epi) {
   if (!ctx) return MB_ERR_ARG;
   if (M < 0 || N < 1 || K < 1) return fail(ctx, MB_ERR_ARG, "linear shape M %d N %d K %d", M, N, K);
-  if (epi != EPI_STORE && epi != EPI_GELU && epi != EPI_ADD)
-    return fail(ctx, MB_ERR_ARG, "unknown epilogue %d", epi);
+  if (epi < EPI_STORE || epi > EPI_GELU_ERF) return fail(ctx, MB_ERR_ARG, "unknown epilogue %d", epi);
+  if (epi == EPI_SCALE_ADD && !bias)
+    return fail(ctx, MB_ERR_ARG, "MB_EPI_SCALE_ADD needs the scale vector in `bias`");
   if (M == 0) return MB_OK;
   if (!A || !W || !C) return fail(ctx, MB_ERR_ARG, "null pointer");
   if (lda < K || ldc < N) return fail(ctx, MB_ERR_ARG, "leading dimension below the row width");

@@ -59,6 +59,9 @@ struct Scratch {
 
 namespace mb {
 
+struct CodecState;
+void codec_free(mb_ctx* ctx);
+
 // The 16 audio-embedding tables (or heads), passed by value to kernels.
 struct AudioTables {
   const float* t[NVQ];
@@ -140,6 +143,10 @@ struct mb_ctx {
   int32_t* frame_alive = nullptr;
   int64_t device_bytes = 0;
   std::atomic<int> cancel{0};
+  // The codec decoder's rings, buffers and resolved weights (codec.hip);
+  // codec_ok is cleared by every upload.
+  mb::CodecState* codec = nullptr;
+  bool codec_ok = false;
 };
 
 namespace mb {
@@ -159,6 +166,14 @@ int hip_fail(mb_ctx* ctx, hipError_t e, const char* what);
 // Device scratch named `name` of at least `bytes`, kept between calls.
 void* scratch(mb_ctx* ctx, const char* name, size_t bytes);
 
+// The uploaded tensor `name` if its dims are `dims`; otherwise null, and the
+// first problem is recorded in `missing` ("weight not uploaded: ...").
+const DeviceTensor* find(mb_ctx* ctx, const std::string& name, std::initializer_list<int64_t> dims,
+                         std::string& missing);
+// A device tensor owned by the context under an internal ('#') name, freed
+// with the uploaded weights; reallocated only when its size changes.
+float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel);
+
 inline size_t kv_elem_bytes(const mb_ctx* ctx) { return ctx->cfg.kv_dtype == MB_KV_BF16 ? 2 : 4; }
 
 // Element offset of (layer, seq, head=0, slot=0, dim=0) in ring_k / ring_v.
@@ -171,12 +186,19 @@ inline int64_t slot_base(const mb_ctx* ctx, int layer, int seq) {
 
 // A ring as the kernels see it: sequence 0's K/V/slot positions for one
 // layer (or for the local head's 17-slot cache).
+// C is the slot count (slot = pos mod C); `window` is how far back a query
+// sees: slot p is live for a query at cur iff 0 <= cur - p < window.  The
+// model's rings use window = C.  The codec's rings add slack slots beyond
+// their window so that appending a chunk of positions before attending to
+// it never overwrites a position an earlier query of the chunk still sees.
 struct RingView {
   void* k = nullptr;
   void* v = nullptr;
   int32_t* sp = nullptr;
   int64_t seq_stride = 0;  // K/V elements between consecutive sequences
   int C = 0;
+  int window = 0;
+  int heads = H;
   int wrap = 1;
   bool bf16 = false;
 };
@@ -219,8 +241,10 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
 int launch_fill_i32(mb_ctx* ctx, int32_t* p, int64_t n, int32_t value);
 int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value);
 
-// gemm.hip
-enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2 };
+// gemm.hip.  EPI_SCALE_ADD (the codec's layer scale) reads the `bias`
+// argument as a per-column scale s and stores C + s * (A W); EPI_GELU_ERF
+// applies the exact (erf) GELU after the bias.
+enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2, EPI_SCALE_ADD = 3, EPI_GELU_ERF = 4 };
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M);
 
@@ -234,7 +258,7 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 
 // layers.hip
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,
-                     const float* w, const float* b, float* y, int64_t ldy);
+                     const float* w, const float* b, float* y, int64_t ldy, int width = D);
 int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, int vocab,
                       const AudioTables& audio, float* x);
 int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,

@@ -12,21 +12,6 @@ namespace mb {
 
 namespace {
 
-const DeviceTensor* find(mb_ctx* ctx, const std::string& name, std::initializer_list<int64_t> dims,
-                         std::string& missing) {
-  auto it = ctx->weights.find(name);
-  if (it == ctx->weights.end()) {
-    if (missing.empty()) missing = "weight not uploaded: " + name;
-    return nullptr;
-  }
-  const DeviceTensor& t = it->second;
-  if (t.dims.size() != dims.size() || !std::equal(dims.begin(), dims.end(), t.dims.begin())) {
-    if (missing.empty()) missing = "weight has the wrong shape: " + name;
-    return nullptr;
-  }
-  return &t;
-}
-
 int resolve_layer(mb_ctx* ctx, const std::string& p, LayerW& w, std::string& missing) {
   auto get = [&](const char* n, std::initializer_list<int64_t> d) {
     const DeviceTensor* t = find(ctx, p + n, d, missing);
@@ -45,29 +30,6 @@ int resolve_layer(mb_ctx* ctx, const std::string& p, LayerW& w, std::string& mis
   w.fc_out_w = get("mlp.fc_out.weight", {FFN, D});
   w.fc_out_b = get("mlp.fc_out.bias", {D});
   return missing.empty() ? MB_OK : MB_ERR_STATE;
-}
-
-// A device tensor owned by the context under an internal name (freed with
-// the uploaded weights); reallocated only when its size changes.
-float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel) {
-  DeviceTensor& t = ctx->weights[name];
-  if (t.ptr && t.numel != numel) {
-    (void)hipStreamSynchronize(ctx->stream);
-    (void)hipFree(t.ptr);
-    ctx->device_bytes -= t.numel * 4;
-    t.ptr = nullptr;
-  }
-  if (!t.ptr) {
-    if (hipMalloc(&t.ptr, (size_t)numel * 4) != hipSuccess) {
-      ctx->weights.erase(name);
-      return nullptr;
-    }
-    ctx->device_bytes += numel * 4;
-    ctx->graph_gen++;
-  }
-  t.numel = numel;
-  t.dims = {numel};
-  return t.ptr;
 }
 
 // LayerNorm (gamma, beta) folded into the [K][N] projection W after it.
@@ -252,6 +214,7 @@ RingView local_ring(mb_ctx* ctx) {
   v.sp = ctx->local_sp;
   v.seq_stride = (int64_t)H * ROW * HD;
   v.C = ROW;
+  v.window = ROW;
   v.wrap = 0;
   v.bf16 = false;
   return v;

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
     const uint16_t* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, const uint16_t* __restrict__ ring_k,
     const uint16_t* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, float* __restrict__ out, Rows out_rows) {
+    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
   __shared__ __align__(16) uint16_t Ks[2][KT * KPAD];  // [slot][dim]
   __shared__ __align__(16) uint16_t Vt[2][HD * KPAD];  // [dim][vt_col(slot)]
   __shared__ __align__(16) int32_t Ps[2][KT];          // stored position per slot (-1: none)
@@ -159,8 +159,9 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
   // Positions relative to the workgroup's first query, so the window test is
   // one unsigned compare: slot positions are stored clamped to [-2^30, 2^30)
   // and an empty slot as 2^30 (after every query); a query at relative
-  // position c sees the slot iff (unsigned)(c - rel) < C (mb_create keeps
-  // C <= 2^20, so a clamped position is outside every window, as it should be).
+  // position c sees the slot iff (unsigned)(c - rel) < W, the window (rings
+  // hold at most 2^20 slots, so a clamped position is outside every window,
+  // as it should be).
   const int64_t base = p0 + (int64_t)qtile * BQ;
   const int crel_lo = wave * 32, crel_hi = min(rw + 31, n - 1) - qtile * BQ;
   int crel[2];
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
     if (!wave_rows) continue;
     const int lo = Pr[buf][0], hi = Pr[buf][1];
     if (lo > crel_hi) continue;  // every stored position is after every query here
-    const bool all_live = hi <= crel_lo && crel_hi - lo < C;
+    const bool all_live = hi <= crel_lo && crel_hi - lo < W;
 
     // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
     f32x4_t s[2][4];
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
         for (int j = 0; j < 4; j++)
 #pragma unroll
           for (int qi = 0; qi < 2; qi++)
-            if ((unsigned)(crel[qi] - pj[j]) >= (unsigned)C) s[qi][sb][j] = -INFINITY;
+            if ((unsigned)(crel[qi] - pj[j]) >= (unsigned)W) s[qi][sb][j] = -INFINITY;
       }
     }
     // Online softmax in log2 units.  The running maximum m only moves when a
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(256) void k_flash_f32(
     const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, const void* __restrict__ ring_k,
     const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, float* __restrict__ out, Rows out_rows) {
+    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
   __shared__ float Ks[KT * FPAD];  // [slot][dim]
   __shared__ float Vs[KT * FPAD];  // [slot][dim]
   __shared__ int32_t Ps[KT];
@@ -413,7 +414,7 @@ __global__ __launch_bounds__(256) void k_flash_f32(
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const bool ok = live_slot(Ps[sb * 16 + grp * 4 + j], cur, C);
+        const bool ok = live_slot(Ps[sb * 16 + grp * 4 + j], cur, W);
         s[sb][j] = ok ? c[j] : -INFINITY;
         mt = fmaxf(mt, s[sb][j]);
       }
@@ -460,19 +461,21 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
     return fail(ctx, MB_ERR_ARG, "bf16 queries need a bf16 ring (the bf16 MFMA path)");
   if (B > 65535) return fail(ctx, MB_ERR_ARG, "at most 65535 sequences per prefill call");
   if (B == 0 || rows_max == 0) return MB_OK;
-  dim3 grid((unsigned)((rows_max + QT - 1) / QT), H, (unsigned)B);
+  const unsigned nh = (unsigned)ring.heads;
+  dim3 grid((unsigned)((rows_max + QT - 1) / QT), nh, (unsigned)B);
   if (q_dtype == MB_DT_BF16)
-    hipLaunchKernelGGL(k_flash_bf16, dim3((unsigned)((rows_max + BQ - 1) / BQ), H, (unsigned)B),
+    hipLaunchKernelGGL(k_flash_bf16, dim3((unsigned)((rows_max + BQ - 1) / BQ), nh, (unsigned)B),
                        dim3(256), 0, ctx->stream, (const uint16_t*)q, q_rows,
                        pos0, n_rows, (const uint16_t*)ring.k, (const uint16_t*)ring.v, ring.sp,
-                       ring.seq_stride, ring.C, out, out_rows);
+                       ring.seq_stride, ring.C, ring.window, out, out_rows);
   else if (ring.bf16)
     hipLaunchKernelGGL(k_flash_f32<true>, grid, dim3(256), 0, ctx->stream, (const float*)q, q_rows,
-                       pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, out, out_rows);
+                       pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.window,
+                       out, out_rows);
   else
     hipLaunchKernelGGL(k_flash_f32<false>, grid, dim3(256), 0, ctx->stream, (const float*)q,
-                       q_rows, pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, out,
-                       out_rows);
+                       q_rows, pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C,
+                       ring.window, out, out_rows);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

@@ -104,17 +104,18 @@ __device__ __forceinline__ void rope_pair(float x0, float x1, float c, float s, 
 // records the slot's position.  Rows with r >= n_rows[b], negative positions
 // or (non-wrapping ring) pos >= C are skipped; the host rejects them first.
 // With more than C rows in one call only the last C reach the ring.
-template <bool IN_BF16, bool KV_BF16, bool Q_BF16>
+template <bool IN_BF16, bool KV_BF16, bool Q_BF16, int NH>
 __global__ __launch_bounds__(256) void k_ring_write(
     const void* __restrict__ qkv, Rows qkv_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, int rows_max, int B, void* __restrict__ q_out,
     Rows q_rows, void* __restrict__ ring_k, void* __restrict__ ring_v,
     int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, int wrap,
     const float2* __restrict__ rope_tab) {
+  constexpr int D = NH * HD;  // width of each of q, k, v in the fused row
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t row_id = t / 96;
+  const int64_t row_id = t / (NH * 8);
   if (row_id >= (int64_t)B * rows_max) return;
-  const int part = (int)(t % 96), head = part >> 3, d0 = (part & 7) * 8;
+  const int part = (int)(t % (NH * 8)), head = part >> 3, d0 = (part & 7) * 8;
   const int b = (int)(row_id / rows_max), r = (int)(row_id % rows_max);
   const int n = n_rows ? n_rows[b] : 1;
   if (r >= n) return;
@@ -155,6 +156,7 @@ RingView global_ring(const mb_ctx* ctx, int layer) {
   v.sp = ctx->slot_pos + slot_base(ctx, layer, 0);
   v.seq_stride = (int64_t)H * ctx->cfg.capacity * HD;
   v.C = ctx->cfg.capacity;
+  v.window = ctx->cfg.capacity;
   v.wrap = ctx->cfg.wrap;
   v.bf16 = ctx->cfg.kv_dtype == MB_KV_BF16;
   return v;
@@ -163,15 +165,24 @@ RingView global_ring(const mb_ctx* ctx, int layer) {
 int launch_ring_write(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const void* qkv,
                       int qkv_dtype, const Rows& qkv_rows, const int32_t* pos0,
                       const int32_t* n_rows, void* q_out, int q_dtype, const Rows& q_rows) {
-  const int64_t threads = (int64_t)B * rows_max * 96;
+  if (ring.heads != H && ring.heads != 4)
+    return fail(ctx, MB_ERR_ARG, "rings of %d heads are not built", ring.heads);
+  const int64_t threads = (int64_t)B * rows_max * ring.heads * 8;
   const int64_t blocks = (threads + 255) / 256;
   if (blocks > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many rows in one call");
   if (blocks == 0) return MB_OK;
   const bool in_bf16 = qkv_dtype == MB_DT_BF16, kv_bf16 = ring.bf16, q_bf16 = q_dtype == MB_DT_BF16;
-#define MB_RW(A, Bq, Cq)                                                                        \
-  hipLaunchKernelGGL((k_ring_write<A, Bq, Cq>), dim3((unsigned)blocks), dim3(256), 0, ctx->stream, \
-                     qkv, qkv_rows, pos0, n_rows, rows_max, B, q_out, q_rows, ring.k, ring.v,     \
-                     ring.sp, ring.seq_stride, ring.C, ring.wrap, ctx->rope_tab)
+#define MB_RW(A, Bq, Cq)                                                                          \
+  do {                                                                                             \
+    if (ring.heads == H)                                                                           \
+      hipLaunchKernelGGL((k_ring_write<A, Bq, Cq, H>), dim3((unsigned)blocks), dim3(256), 0,       \
+                         ctx->stream, qkv, qkv_rows, pos0, n_rows, rows_max, B, q_out, q_rows,     \
+                         ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.wrap, ctx->rope_tab); \
+    else                                                                                           \
+      hipLaunchKernelGGL((k_ring_write<A, Bq, Cq, 4>), dim3((unsigned)blocks), dim3(256), 0,       \
+                         ctx->stream, qkv, qkv_rows, pos0, n_rows, rows_max, B, q_out, q_rows,     \
+                         ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.wrap, ctx->rope_tab); \
+  } while (0)
   if (in_bf16) {
     if (kv_bf16) { if (q_bf16) MB_RW(true, true, true); else MB_RW(true, true, false); }
     else { if (q_bf16) MB_RW(true, false, true); else MB_RW(true, false, false); }
@@ -478,6 +489,8 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
                        const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
                        int64_t max_valid, float* q_out, const Rows& qo_rows, float* out,
                        const Rows& out_rows) {
+  if (ring.heads != H || ring.window != ring.C)
+    return fail(ctx, MB_ERR_ARG, "single-query decode attention runs on the model's 12-head rings");
   const int C = ring.C;
   if (max_valid > C) max_valid = C;
   if (max_valid < 1) max_valid = 1;

@@ -103,3 +103,65 @@ def qkv_rows(seed, shape) -> np.ndarray:
     """q | k | v rows ~ N(0, 1), float32."""
     g = np.random.default_rng(seed)
     return g.standard_normal(tuple(shape) + (QKV,), dtype=np.float32)
+
+
+# ------------------------------------------------------------------ the codec
+CODEC_D, CODEC_FFN = 256, 1024
+CODEC_DECODER_INDEX = (1, 3, 5, 7)
+
+
+def codec_specs(layers=(4, 2, 2, 4)):
+    """(name, shape, kind, scale) of every codec tensor, in a fixed order.  The
+    names are the ones include/mockbird_hip.h lists for mb_codec_*; the
+    matrices are [K, N] as the graph's MatMul initialisers hold them, except
+    the two output-major 1x1 convolutions of the RVQ front."""
+    d, f = CODEC_D, CODEC_FFN
+    specs = []
+    for k in range(NVQ):
+        p = f"model.quantizer.quantizers.{k}."
+        specs += [(p + "out_proj.weight", (512, 8), "mat", 0.35),
+                  (p + "out_proj.bias", (512,), "vec", 0.02),
+                  (p + "codebook.weight", (CODES, 8), "mat", 1.0)]
+    specs += [("model.quantizer.output_proj.weight", (768, 512), "mat", 512 ** -0.5),
+              ("model.quantizer.output_proj.bias", (768,), "vec", 0.02)]
+    for s, n_layers in enumerate(layers):
+        p = f"model.decoder.{CODEC_DECODER_INDEX[s]}."
+        w_in = 192 if s == 0 else 384
+        specs.append((p + "input_proj.weight", (w_in, d), "mat", w_in ** -0.5))
+        for i in range(n_layers):
+            q = p + f"transformer.layers.{i}."
+            specs += [(q + "self_attn.in_proj.weight", (d, 3 * d), "mat", d ** -0.5),
+                      (q + "self_attn.out_proj.weight", (d, d), "mat", d ** -0.5),
+                      (q + "ffn.0.weight", (d, f), "mat", d ** -0.5),
+                      (q + "ffn.2.weight", (f, d), "mat", f ** -0.5),
+                      (q + "norm1.weight", (d,), "ln_w", 0.1), (q + "norm1.bias", (d,), "vec", 0.05),
+                      (q + "norm2.weight", (d,), "ln_w", 0.1), (q + "norm2.bias", (d,), "vec", 0.05),
+                      (q + "layer_scale_1.scale", (d,), "scale", 0.2),
+                      (q + "layer_scale_2.scale", (d,), "scale", 0.2)]
+        specs.append((p + "output_proj.weight", (d, 240 if s == len(layers) - 1 else 768), "mat",
+                      d ** -0.5))
+    return specs
+
+
+def codec_weights(layers=(4, 2, 2, 4), seed: int = 0) -> dict[str, np.ndarray]:
+    """Seeded random codec weights at the real shapes: matrices N(0, scale),
+    LayerNorm scales 1 + N(0, 0.1), shifts and biases small normals, layer
+    scales 0.2 (1 + N(0, 0.25)); one stream per tensor from (seed, index)."""
+    out = {}
+    for idx, (name, shape, kind, sc) in enumerate(codec_specs(layers)):
+        g = np.random.default_rng([seed, 0xC0DEC, idx])
+        a = g.standard_normal(shape, dtype=np.float32)
+        if kind == "ln_w":
+            a = np.float32(1) + a * np.float32(sc)
+        elif kind == "scale":
+            a = np.float32(sc) * (np.float32(1) + a * np.float32(0.25))
+        else:
+            a = a * np.float32(sc)
+        out[name] = np.ascontiguousarray(a, dtype=np.float32)
+    return out
+
+
+def codec_codes(seed: int, n_frames: int, B: int) -> np.ndarray:
+    """Seeded code frames [n_frames][B][16] in [0, 1024)."""
+    g = np.random.default_rng([seed, 0xC0DE5])
+    return g.integers(0, CODES, size=(n_frames, B, NVQ), dtype=np.int32)

@@ -73,6 +73,16 @@ def lib():
                                                  _i32p, _i32p, _f32p, _f32p, _i32p, _f32p]
         L.or_local_frame_batch.argtypes = [C.c_void_p, C.c_int, _f32p, _u32p, _i32p, _i32p,
                                            C.c_void_p]
+        L.or_erf_as.argtypes = [C.c_double]
+        L.or_erf_as.restype = C.c_double
+        L.or_gelu_erf.argtypes = [C.c_float]
+        L.or_gelu_erf.restype = C.c_float
+        L.or_codec_slots.argtypes = [C.c_void_p]
+        L.or_codec_slots.restype = C.c_int64
+        L.or_codec_rvq.argtypes = [C.c_void_p, _i32p, _f32p]
+        L.or_codec_decode_batch.argtypes = [C.c_void_p, C.c_int, _f32p, _f32p, _i32p, _i32p,
+                                            C.c_int, _i32p, _f32p]
+        L.or_codec_decode_batch.restype = C.c_int
         _lib = L
     return _lib
 
@@ -335,3 +345,103 @@ class ModelState:
         lib().or_local_frame_batch(self.m.ptr, self.B, _c(hidden, np.float32), self.seen, codes,
                                    cont, margins.ctypes.data)
         return codes, cont.astype(bool), margins
+
+
+# ------------------------------------------------------------------ the codec
+class _CodecLayer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in
+                ("qkv", "o", "f1", "f2", "ln1_w", "ln1_b", "ln2_w", "ln2_b", "s1", "s2")]
+
+
+class _Codec(C.Structure):
+    _fields_ = [("rvq_w", C.c_void_p * 16), ("rvq_b", C.c_void_p * 16),
+                ("rvq_book", C.c_void_p * 16), ("rvq_out", C.c_void_p), ("rvq_out_b", C.c_void_p),
+                ("layers", C.c_int * 4), ("context", C.c_int * 4), ("in_proj", C.c_void_p * 4),
+                ("out_proj", C.c_void_p * 4), ("layer", C.POINTER(_CodecLayer)),
+                ("kv_bf16", C.c_int)]
+
+
+def erf_as(x: float) -> float:
+    """erf by Abramowitz & Stegun 7.1.26 (the reference's GELU_ERF form)."""
+    return lib().or_erf_as(float(x))
+
+
+def gelu_erf(x: float) -> float:
+    return lib().or_gelu_erf(float(x))
+
+
+class CodecOracle:
+    """The codec decoder (codec_oracle.c) for B voices with their own rings:
+    the reference's per-position order, rings of exactly `context` slots."""
+
+    def __init__(self, weights: dict, B: int, layers=(4, 2, 2, 4),
+                 context=(500, 1696, 2480, 3248), kv_bf16: bool = False):
+        self.B, self.layers, self.context = B, tuple(layers), tuple(context)
+        self._keep = {k: _c(v, np.float32) for k, v in weights.items()}
+        w = self._keep
+        st = _Codec()
+        for k in range(16):
+            p = f"model.quantizer.quantizers.{k}."
+            st.rvq_w[k] = w[p + "out_proj.weight"].ctypes.data
+            st.rvq_b[k] = w[p + "out_proj.bias"].ctypes.data
+            st.rvq_book[k] = w[p + "codebook.weight"].ctypes.data
+        st.rvq_out = w["model.quantizer.output_proj.weight"].ctypes.data
+        st.rvq_out_b = w["model.quantizer.output_proj.bias"].ctypes.data
+        layer_structs = []
+        for s in range(4):
+            p = f"model.decoder.{(1, 3, 5, 7)[s]}."
+            st.layers[s] = self.layers[s]
+            st.context[s] = self.context[s]
+            st.in_proj[s] = w[p + "input_proj.weight"].ctypes.data
+            st.out_proj[s] = w[p + "output_proj.weight"].ctypes.data
+            for i in range(self.layers[s]):
+                q = p + f"transformer.layers.{i}."
+                layer_structs.append(_CodecLayer(
+                    w[q + "self_attn.in_proj.weight"].ctypes.data,
+                    w[q + "self_attn.out_proj.weight"].ctypes.data,
+                    w[q + "ffn.0.weight"].ctypes.data, w[q + "ffn.2.weight"].ctypes.data,
+                    w[q + "norm1.weight"].ctypes.data, w[q + "norm1.bias"].ctypes.data,
+                    w[q + "norm2.weight"].ctypes.data, w[q + "norm2.bias"].ctypes.data,
+                    w[q + "layer_scale_1.scale"].ctypes.data,
+                    w[q + "layer_scale_2.scale"].ctypes.data))
+        self._layers = (_CodecLayer * len(layer_structs))(*layer_structs)
+        st.layer = C.cast(self._layers, C.POINTER(_CodecLayer))
+        st.kv_bf16 = int(kv_bf16)
+        self._st = st
+        self.slots = int(lib().or_codec_slots(C.byref(st)))
+        self.K = np.zeros((B, self.slots, 256), np.float32)
+        self.V = np.zeros((B, self.slots, 256), np.float32)
+        self.slot_pos = np.full((B, self.slots), -1, np.int32)
+        self.pos = np.zeros((B, 4), np.int32)
+
+    def reset(self, voices=None):
+        for b in (range(self.B) if voices is None else voices):
+            self.slot_pos[b] = -1
+            self.pos[b] = 0
+
+    def rvq(self, codes) -> np.ndarray:
+        """One frame's RVQ front for one voice: codes[16] -> [4][192]."""
+        out = np.zeros((4, 192), np.float32)
+        lib().or_codec_rvq(C.byref(self._st), _c(codes, np.int32), out)
+        return out
+
+    def decode(self, codes: np.ndarray) -> np.ndarray:
+        """codes [n][B][16] -> pcm [B][2][n * 3840], continuing every voice."""
+        codes = _c(codes, np.int32)
+        n = codes.shape[0]
+        pcm = np.zeros((self.B, 2, n * 3840), np.float32)
+        rc = lib().or_codec_decode_batch(C.byref(self._st), self.B, self.K, self.V, self.slot_pos,
+                                         self.pos, n, codes, pcm)
+        if rc != 0:
+            raise MemoryError("codec oracle allocation failed")
+        return pcm
+
+    def layer_ring(self, layer: int, voice: int):
+        """(K [context][256], V, slot_pos [context]) of one layer's ring."""
+        start, s_of = 0, []
+        for s in range(4):
+            for _ in range(self.layers[s]):
+                s_of.append((start, self.context[s]))
+                start += self.context[s]
+        a, c = s_of[layer]
+        return (self.K[voice, a:a + c], self.V[voice, a:a + c], self.slot_pos[voice, a:a + c])

@@ -93,3 +93,46 @@ def test_linear_rejects_bad_shapes(ctx):
     assert e.value.code == mb.MB_ERR_ARG
     with pytest.raises(mb.MbError):
         ctx.linear_dev(4, 64, 768, 16, 700, 16, None, 16, 64)  # lda < K
+
+
+CODEC_SHAPES = [  # (M, N, K): the codec's projections at 1-256 voices
+    (4, 256, 192), (16, 768, 256), (64, 256, 256), (128, 1024, 256), (256, 256, 1024),
+    (512, 768, 384), (1024, 256, 1024), (2048, 1024, 256), (8192, 256, 256),
+]
+
+
+@pytest.mark.parametrize("M,N,K", CODEC_SHAPES)
+def test_linear_codec_epilogues(ctx, M, N, K):
+    """MB_EPI_SCALE_ADD (C + s * A W, the codec's layer scale, LAYER_SCALE_ADD
+    kernels-decode.ts:360-371) and MB_EPI_GELU_ERF (the exact GELU after the
+    bias, GELU_ERF :392-415) on both GEMM kernels.  Expected: the oracle's
+    GEMM, then the epilogue in float64 with scipy's erf (A&S 7.1.26, which
+    the kernels use, is within 1.5e-7 of it).  Bar 1e-4 (outputs are O(1))."""
+    torch = pytest.importorskip("torch")
+    from scipy.special import erf
+    say(f"linear codec epilogues M={M} N={N} K={K}")
+    g = np.random.default_rng([M, N, K, 7])
+    A = g.standard_normal((M, K), dtype=np.float32)
+    W = g.standard_normal((K, N), dtype=np.float32) * np.float32(K ** -0.5)
+    vec = g.standard_normal(N, dtype=np.float32) * np.float32(0.3)
+    C0 = g.standard_normal((M, N), dtype=np.float32)
+    dev = torch.device("cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    tA, tW, tv = (torch.from_numpy(x).to(dev) for x in (A, W, vec))
+    lin = oracle.gemm(A, W).astype(np.float64)
+    cases = {
+        mb.MB_EPI_SCALE_ADD: C0.astype(np.float64) + vec.astype(np.float64) * lin,
+        mb.MB_EPI_GELU_ERF: (lambda u: 0.5 * u * (1.0 + erf(u / np.sqrt(2.0))))(lin + vec),
+    }
+    for epi, want in cases.items():
+        tC = torch.from_numpy(C0).to(dev)
+        ctx.linear_dev(M, N, K, tA.data_ptr(), K, tW.data_ptr(), tv.data_ptr(), tC.data_ptr(), N, epi)
+        torch.cuda.synchronize()
+        err = float(np.abs(tC.cpu().numpy() - want).max())
+        assert err < 1e-4, (epi, err)
+
+
+def test_linear_scale_add_needs_the_scale(ctx):
+    with pytest.raises(mb.MbError) as e:
+        ctx.linear_dev(4, 256, 256, 16, 256, 16, None, 16, 256, mb.MB_EPI_SCALE_ADD)
+    assert e.value.code == mb.MB_ERR_ARG
