@@ -1,6 +1,6 @@
 """Benchmark of the MI355X decoder hot path (one GPU).
 
-    python bench.py [--steps K] [--warmup W] [--legs copy,c1,voices,c4,c2,frames]
+    python bench.py [--steps K] [--warmup W] [--legs copy,c1,voices,c4,c2,codec,frames]
 
 Default workload (c1): the isolated KV ring append + decode attention step --
 B=64 independent sequences, 12 heads x 64, ring capacity 2048, bf16 KV
@@ -251,6 +251,54 @@ def run_c4(args, B=32, C=4096):
                      "ring 4096 (full windows, each append evicts), bf16 KV, 12 layer rings in turn")
 
 
+def run_codec(args, B, kv_name, warm=216, frames=24):
+    """The codec decoder at steady state: B voices, the real stage shapes
+    (4/2/2/4 layers of d=256, windows 500/1696/2480/3248 positions), every
+    ring full after `warm` frames (stage 2, the slowest, fills after 212).  One
+    mb_codec_decode_dev call decodes `frames` frames; frames/s counts voice
+    frames (B x frames / time).  The attention's algorithmic bytes per frame
+    are every layer's full window of K and V read once per frame (the stage's
+    positions attend to it in one pass) plus the frame's new K/V rows."""
+    import torch
+
+    import mockbird_amd as mb
+    from mockbird_amd import synth
+
+    kv = mb.MB_KV_BF16 if kv_name == "bf16" else mb.MB_KV_F32
+    e = 2 if kv == mb.MB_KV_BF16 else 4
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=1, capacity=16, max_seqs=1, max_rows=16)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    ctx.upload_all(synth.codec_weights(mb.CODEC_LAYERS, seed=21))
+    ctx.codec_init(B, kv_dtype=kv)
+    codes = torch.from_numpy(synth.codec_codes(22, warm + frames, B)).to(dev)
+    chunk = 8
+    pcm = torch.empty((B, 2, max(chunk, frames) * mb.CODEC_SAMPLES), device=dev)
+    for f in range(0, warm, chunk):
+        n = min(chunk, warm - f)
+        ctx.codec_decode_dev(B, n, codes[f].data_ptr(), pcm.data_ptr())
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    ctx.codec_decode_dev(B, frames, codes[warm].data_ptr(), pcm.data_ptr())
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / frames
+    ctx.close()
+    window = sum(l * c for l, c in zip(mb.CODEC_LAYERS, mb.CODEC_CONTEXT))
+    new_rows = sum(l * (4 << s) for s, l in enumerate(mb.CODEC_LAYERS))
+    attn_bytes = B * (window + new_rows) * 256 * 2 * e
+    return {"workload": f"codec decoder, {B} voices, rings full (4/2/2/4 layers, windows "
+                        f"500/1696/2480/3248), {kv_name} rings, {frames} frames per call",
+            "B": B, "kv": kv_name, "ms_per_frame": round(ms, 4),
+            "voice_frames_per_sec": round(B / (ms * 1e-3), 1),
+            "realtime_factor": round(B * 80.0 / ms, 1),
+            "ring_bytes_per_frame": int(attn_bytes),
+            "ring_gbs": round(attn_bytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def run_c2(args):
     """Causal prefill attention, B=16, S=512, 12 heads x 64, bf16 q/k/v with
     fp32 accumulation (bf16 MFMA), RoPE at pos = row, ring C=1024 from slot 0.
@@ -433,12 +481,12 @@ def main():
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
-    ap.add_argument("--legs", default="copy,c1,voices,c4,c2,frames",
+    ap.add_argument("--legs", default="copy,c1,voices,c4,c2,codec,frames",
                     help="comma list of copy (plain 2 GiB HBM copy), c1 (append + decode "
                          "attention, 64 sequences, C=2048), voices (the same at 256 voices, "
                          "C=1024), c4 (the same at 32 sequences, C=4096, wrapped), c2 "
-                         "(prefill attention), frames (model decode frames/s); the JSON line "
-                         "needs c1")
+                         "(prefill attention), codec (codec decoder frames/s at 64 and 256 "
+                         "voices), frames (model decode frames/s); the JSON line needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     ap.add_argument("--frames-n", type=int, default=0,
                     help="frames per voice count (default: 60 at B=1, 300 otherwise)")
@@ -456,6 +504,8 @@ def main():
     copy = run_copy() if "copy" in legs else None
     voices = run_voices_attention(args) if "voices" in legs else None
     c4 = run_c4(args) if "c4" in legs else None
+    codec = ([run_codec(args, 64, "f32"), run_codec(args, 256, "bf16")]
+             if "codec" in legs else None)
     c2 = run_c2(args) if "c2" in legs else None
     frames = None
     if "frames" in legs:
@@ -471,7 +521,7 @@ def main():
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "kv_attention_256_voices": voices,
                           "kv_attention_c4_wrapped": c4, "prefill_attention": c2,
-                          "frames_detail": frames}), flush=True)
+                          "codec": codec, "frames_detail": frames}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -518,6 +568,7 @@ def main():
         "kv_attention_256_voices": voices,
         "kv_attention_c4_wrapped": c4,
         "prefill_attention": c2,
+        "codec": codec,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
         "frames_detail": frames,
     }

@@ -10,7 +10,9 @@
 //  - the projections are one GEMM each over B x positions rows, with the
 //    layer-scale residual add and the GELU fused into their epilogues;
 //  - a layer appends the frame's positions to its ring and then attends to
-//    them with the causal windowed flash kernel.  Position i of the chunk
+//    them in one pass over the window (k_attn_window: the window split
+//    across the waves of a workgroup, all of the chunk's queries per wave).
+//    Position i of the chunk
 //    must not see i + 1 ..; the window rule (stored position <= cur) gives
 //    that, and each ring holds its window plus one frame of positions, so an
 //    append never overwrites a position that an earlier query of the same
@@ -330,8 +332,8 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T,
           (rc = launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M)) ||
           (rc = launch_ring_write(ctx, ring, B, n, cs.qkv, MB_DT_F32, dense_rows(3 * kD, n), pos,
                                   nrow, cs.q, MB_DT_F32, dense_rows(kD, n))) ||
-          (rc = launch_prefill_attention(ctx, ring, B, n, cs.q, MB_DT_F32, dense_rows(kD, n), pos,
-                                         nrow, cs.att, dense_rows(kD, n))) ||
+          (rc = launch_window_attention(ctx, ring, B, n, cs.q, dense_rows(kD, n), pos, nrow,
+                                        cs.att, dense_rows(kD, n))) ||
           (rc = launch_gemm(ctx, EPI_SCALE_ADD, cs.att, kD, w.o, kD, kD, w.s1, cs.x, kD, M)) ||
           (rc = launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln2_w, w.ln2_b, cs.h, kD, kD)) ||
           (rc = launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M)) ||

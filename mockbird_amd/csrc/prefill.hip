@@ -454,6 +454,208 @@ __global__ __launch_bounds__(256) void k_flash_f32(
         make_float4(acc[d][0] * inv, acc[d][1] * inv, acc[d][2] * inv, acc[d][3] * inv);
 }
 
+// ------------------------------------------------ short chunks, long windows
+
+// Attention of a short chunk of consecutive queries (up to 16 * QB rows per
+// sequence, fp32) against a long window: the codec's stages append 4..32
+// positions per frame and attend over windows of 500..3248.  A workgroup is
+// one (sequence, head); its NW waves split the slot range into contiguous
+// runs of 16-slot groups, and each wave computes every query of the chunk
+// against its run, reading K and V straight from HBM into MFMA operands
+// (no LDS staging), with v_mfma_f32_16x16x4f32:
+//  - scores S^T[16 slots][16 queries]: lane l feeds K[slot l%16][16g + kc]
+//    and Q[query l%16][16g + kc] (g = l/16) in step kc, so it loads 16
+//    contiguous dims of one K row;
+//  - P V: output block d row i is dim 4i + d, so in step j lane l feeds
+//    V[slot (l/16)*4 + j][4(l%16) + d] -- 4 contiguous dims -- and its own
+//    score element j as P^T.
+// Partials (max, sum, 64 dims per query) fold across the waves through LDS.
+// Liveness is the window rule: slot position p (empty slots never live) is
+// visible to a query at cur iff 0 <= cur - p < W.
+template <bool KV_BF16, int QB, int NW>
+__global__ __launch_bounds__(64 * NW) void k_attn_window(
+    const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, const void* __restrict__ ring_k,
+    const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
+  constexpr int NQ = 16 * QB;
+  __shared__ float red_ml[NW][2][NQ];        // per wave: max (log2 units), sum
+  __shared__ float red_acc[NW][NQ][HD + 1];  // per wave: unnormalised output
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qc = lane & 15, g = lane >> 4;
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int n = n_rows[b];
+  const int64_t p0 = pos0[b];
+  const int64_t end64 = p0 + n;
+  const int kv_end = end64 < C ? (int)end64 : C;
+  const int groups = (kv_end + 15) >> 4;
+  const int per = (groups + NW - 1) / NW;
+  const int g0 = wave * per, g1 = min(g0 + per, groups);
+
+  // Positions relative to the sequence's first query, clamped so the window
+  // test is one unsigned compare; an empty slot and a query past n are
+  // outside every window.
+  constexpr int32_t kFar = 1 << 30;
+  int32_t crel[QB];
+  float qv[QB][16];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    const int r = qb * 16 + qc;
+    crel[qb] = r < n ? r : -kFar;
+    const float* qp = q + (r < n ? row_at(q_rows, b, r) : 0) + h * HD + g * 16;
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 t = r < n ? *(const float4*)(qp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qv[qb][i] = t.x; qv[qb][i + 1] = t.y; qv[qb][i + 2] = t.z; qv[qb][i + 3] = t.w;
+    }
+  }
+  constexpr int E = KV_BF16 ? 2 : 4;
+  const char* kb = (const char*)ring_k + ((int64_t)b * ring_seq_stride + (int64_t)h * C * HD) * E;
+  const char* vb = (const char*)ring_v + ((int64_t)b * ring_seq_stride + (int64_t)h * C * HD) * E;
+  const int32_t* sp = slot_pos + (int64_t)b * C;
+
+  f32x4_t acc[QB][4];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++)
+#pragma unroll
+    for (int d = 0; d < 4; d++) acc[qb][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m[QB], l[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    m[qb] = -INFINITY;
+    l[qb] = 0.f;
+  }
+
+  for (int gi = g0; gi < g1; gi++) {
+    const int s0 = gi * 16;
+    // K: 16 contiguous dims of slot s0 + qc; V: 4 dims of slots s0 + 4g + j
+    float kf[16], vf[4][4];
+    const int ks = min(s0 + qc, kv_end - 1);
+    if (KV_BF16) {
+      const uint4 a = *(const uint4*)(kb + ((int64_t)ks * HD + g * 16) * 2);
+      const uint4 c = *(const uint4*)(kb + ((int64_t)ks * HD + g * 16 + 8) * 2);
+      unpack<true>(a, kf);
+      unpack<true>(c, kf + 8);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; i += 4) {
+        const float4 t = *(const float4*)(kb + ((int64_t)ks * HD + g * 16 + i) * 4);
+        kf[i] = t.x; kf[i + 1] = t.y; kf[i + 2] = t.z; kf[i + 3] = t.w;
+      }
+    }
+    int32_t pj[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int sl = s0 + 4 * g + j;
+      const int vs = min(sl, kv_end - 1);
+      if (KV_BF16) {
+        const uint2 t = *(const uint2*)(vb + ((int64_t)vs * HD + 4 * qc) * 2);
+        vf[j][0] = bf16_lo(t.x); vf[j][1] = bf16_hi(t.x);
+        vf[j][2] = bf16_lo(t.y); vf[j][3] = bf16_hi(t.y);
+      } else {
+        const float4 t = *(const float4*)(vb + ((int64_t)vs * HD + 4 * qc) * 4);
+        vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
+      }
+      const int32_t p = sl < kv_end ? sp[sl] : -1;
+      const int64_t d = (int64_t)p - p0;
+      pj[j] = p < 0 ? kFar : (int32_t)(d < -kFar ? -kFar : d > kFar ? kFar : d);
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++) {
+      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < 16; kc++)
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kc], qv[qb][kc], sc, 0, 0, 0);
+      float t[4];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        t[j] = (unsigned)(crel[qb] - pj[j]) < (unsigned)W ? sc[j] * kScoreLog2 : -INFINITY;
+        mt = fmaxf(mt, t[j]);
+      }
+      mt = col_max(mt);
+      // conditional rescale (the running max moves only by more than 8)
+      const bool grow = mt > m[qb] + 8.f;
+      if (__ballot(grow)) {
+        const float mn = grow ? mt : m[qb];
+        const float scale = grow ? __builtin_amdgcn_exp2f(m[qb] - mn) : 1.f;
+        m[qb] = mn;
+        l[qb] *= scale;
+#pragma unroll
+        for (int d = 0; d < 4; d++) acc[qb][d] *= scale;
+      }
+      const float mu = m[qb] == -INFINITY ? 0.f : m[qb];
+      float pw[4], ls = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        pw[j] = __builtin_amdgcn_exp2f(t[j] - mu);
+        ls += pw[j];
+      }
+      l[qb] += col_sum(ls);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int d = 0; d < 4; d++)
+          acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j][d], pw[j], acc[qb][d], 0, 0, 0);
+    }
+  }
+
+  // fold the waves: lane (qc, g) holds dims 4((g*4) + r) + d of query qb*16 + qc
+#pragma unroll
+  for (int qb = 0; qb < QB; qb++) {
+    if (g == 0) {
+      red_ml[wave][0][qb * 16 + qc] = m[qb];
+      red_ml[wave][1][qb * 16 + qc] = l[qb];
+    }
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) red_acc[wave][qb * 16 + qc][4 * (4 * g + r) + d] = acc[qb][d][r];
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < NQ * HD; t += 64 * NW) {
+    const int qi = t / HD, dim = t % HD;
+    if (qi >= n) continue;
+    float M = -INFINITY;
+    for (int w = 0; w < NW; w++) M = fmaxf(M, red_ml[w][0][qi]);
+    float L = 0.f, o = 0.f;
+    if (M != -INFINITY) {
+      for (int w = 0; w < NW; w++) {
+        const float mw = red_ml[w][0][qi];
+        const float wt = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+        L += wt * red_ml[w][1][qi];
+        o += wt * red_acc[w][qi][dim];
+      }
+    }
+    out[row_at(out_rows, b, qi) + h * HD + dim] = L > 0.f ? o / L : 0.f;
+  }
+}
+
+// Chunks of up to 32 consecutive fp32 queries per sequence against a ring
+// (the codec's stages); rows_max bounds n_rows.
+int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const float* q,
+                            const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
+                            float* out, const Rows& out_rows) {
+  if (rows_max < 1 || rows_max > 32)
+    return fail(ctx, MB_ERR_ARG, "window attention takes 1..32 rows per sequence, not %d", rows_max);
+  if (B > 65535) return fail(ctx, MB_ERR_ARG, "at most 65535 sequences per call");
+  if (B == 0) return MB_OK;
+  constexpr int NW = 8;
+  const dim3 grid((unsigned)ring.heads, (unsigned)B);
+#define MB_WIN(BF, QB)                                                                            \
+  hipLaunchKernelGGL((k_attn_window<BF, QB, NW>), grid, dim3(64 * NW), 0, ctx->stream, q, q_rows, \
+                     pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.window, \
+                     out, out_rows)
+  if (ring.bf16) {
+    if (rows_max <= 16) MB_WIN(true, 1); else MB_WIN(true, 2);
+  } else {
+    if (rows_max <= 16) MB_WIN(false, 1); else MB_WIN(false, 2);
+  }
+#undef MB_WIN
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
 int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
                              const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
                              const int32_t* n_rows, float* out, const Rows& out_rows) {
