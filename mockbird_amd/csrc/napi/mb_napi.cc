@@ -596,6 +596,73 @@ napi_value DecodeFrames(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// A 4-element array field of a config object (each entry an integer).
+bool read_config_quad(napi_env env, napi_value obj, const char* key, int32_t* out) {
+  bool has = false;
+  napi_has_named_property(env, obj, key, &has);
+  if (!has) return true;  // keep the default
+  napi_value v;
+  napi_get_named_property(env, obj, key, &v);
+  bool is_array = false;
+  napi_is_array(env, v, &is_array);
+  uint32_t len = 0;
+  if (is_array) napi_get_array_length(env, v, &len);
+  if (!is_array || len != 4) {
+    throw_type(env, std::string(key) + " must be an array of 4 integers");
+    return false;
+  }
+  for (uint32_t i = 0; i < 4; i++) {
+    napi_value e;
+    napi_get_element(env, v, i, &e);
+    int x;
+    if (!get_int(env, e, &x, key)) return false;
+    out[i] = x;
+  }
+  return true;
+}
+
+// codecInit(h, {maxVoices, kvDtype, layers: [4], context: [4]})
+//   (the codec's shape defaults: layers 4/2/2/4, windows 500/1696/2480/3248)
+napi_value CodecInit(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  mb_codec_config cfg{1, MB_KV_F32, {4, 2, 2, 4}, {500, 1696, 2480, 3248}};
+  napi_valuetype t;
+  napi_typeof(env, a.at(1), &t);
+  if (t != napi_undefined) {
+    if (t != napi_object) return throw_type(env, "codecInit() takes a config object");
+    napi_value o = a.at(1);
+    if (!read_config_field(env, o, "maxVoices", &cfg.max_voices) ||
+        !read_config_field(env, o, "kvDtype", &cfg.kv_dtype) ||
+        !read_config_quad(env, o, "layers", cfg.layers) ||
+        !read_config_quad(env, o, "context", cfg.context))
+      return nullptr;
+  }
+  int rc = mb_codec_init(ctx, &cfg);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+// codecDecode(h, B, nFrames, codes Int32Array[nFrames*B*16])
+//   -> pcm Float32Array[B*2*nFrames*3840] (per voice: left, then right)
+napi_value CodecDecode(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int B, nf;
+  if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &nf, "nFrames")) return nullptr;
+  if (B < 0 || nf < 0) return throw_range(env, "B and nFrames must be >= 0");
+  int32_t* codes;
+  if (!get_array(env, a.at(3), napi_int32_array, (int64_t)nf * B * kNvq, &codes, nullptr, "codes"))
+    return nullptr;
+  float* pcm;
+  napi_value P = new_f32(env, (int64_t)B * 2 * nf * 3840, &pcm);
+  int rc = mb_codec_decode(ctx, B, nf, codes, pcm);
+  if (rc) return throw_status(env, ctx, rc);
+  return P;
+}
+
 napi_value LastError(napi_env env, napi_callback_info info) {
   Args a(env, info);
   mb_ctx* ctx = get_ctx(env, a.at(0));
@@ -630,6 +697,9 @@ napi_value Init(napi_env env, napi_value exports) {
       {"localFrame", LocalFrame},
       {"localSteps", LocalSteps},
       {"decodeFrames", DecodeFrames},
+      {"codecInit", CodecInit},
+      {"codecReset", SeqListCall<mb_codec_reset>},
+      {"codecDecode", CodecDecode},
       {"lastError", LastError},
   };
   for (const Fn& f : fns) {

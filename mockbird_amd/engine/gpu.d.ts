@@ -1,4 +1,4 @@
-import type { WeightTable } from "./weights";
+import type { CodecShape, WeightTable } from "./weights";
 
 export class EngineNotImplemented extends Error {
   constructor(step: string);
@@ -38,6 +38,9 @@ export type EngineOptions = {
   /** false (default): the reference's non-wrapping global ring */
   wrap?: boolean;
   device?: number;
+  /** the codec's layers and ring windows per stage (4/2/2/4, 500/1696/2480/3248) */
+  codecShape?: CodecShape;
+  codecKvDtype?: "f32" | "bf16";
 };
 
 export function createGpuEngineFor(

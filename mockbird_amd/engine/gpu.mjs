@@ -3,13 +3,14 @@
 // and error behaviour follow gpu.ts so WgpuTtsRuntime (runtime.ts:357-561)
 // can drive it unchanged: prefill -> nextFrame -> decodeStep -> ... -> reset.
 //
-// The codec (decodeFrames) and the clone encoder (encodeWaveform) are not
-// part of this library; both throw EngineNotImplemented, which is how the
-// reference itself reports a missing stage (gpu.ts:28-36, :279-281).
-import { HIDDEN, kvDtypeCode, loadNative, orDefault, ROW_WIDTH } from "./native.mjs";
+// The codec (decodeFrames) runs when the engine is created with a codec
+// weight table; the clone encoder (encodeWaveform) is not part of this
+// library.  A missing stage throws EngineNotImplemented, which is how the
+// reference itself reports one (gpu.ts:28-36, :279-281).
+import { HIDDEN, kvDtypeCode, loadNative, N_VQ, orDefault, ROW_WIDTH } from "./native.mjs";
 import { DecodeRunner } from "./decode.mjs";
 import { PrefillRunner, stageRows } from "./prefill.mjs";
-import { resolveEngineTensors } from "./weights.mjs";
+import { CODEC_SHAPE, resolveCodecTensors, resolveEngineTensors } from "./weights.mjs";
 
 export class EngineNotImplemented extends Error {
   constructor(step) {
@@ -45,6 +46,7 @@ class HipTtsEngineImpl {
     /** rows currently in the global KV cache (== the next sequence position) */
     this.pastValidLength = 0;
     this.lastHidden = null;
+    this.hasCodec = false;
     this.disposed = false;
   }
 
@@ -108,6 +110,7 @@ class HipTtsEngineImpl {
     this.lastHidden = null;
     this.decoder.clearSeen();
     this.native.ringReset(this.handle, null);
+    if (this.hasCodec) this.native.codecReset(this.handle, null);
   }
 
   async decodeStep(input) {
@@ -125,9 +128,22 @@ class HipTtsEngineImpl {
     return frame;
   }
 
+  /**
+   * Codes -> 48 kHz stereo, continuing the codec rings
+   * (CodecRunner.decodeFrames, codec.ts:766-813): one Float32Array per
+   * channel, 3840 samples per frame.  A missing code reads as 0, as there.
+   */
   async decodeFrames(frames) {
     if (!frames.length) return [];
-    throw new EngineNotImplemented("codec decoder (codec.ts streaming rings)");
+    if (!this.hasCodec) throw new EngineNotImplemented("codec decoder (no codec weights given)");
+    const n = frames.length;
+    const codes = new Int32Array(n * N_VQ);
+    for (let f = 0; f < n; f += 1) {
+      for (let k = 0; k < N_VQ; k += 1) codes[f * N_VQ + k] = orDefault(frames[f][k], 0);
+    }
+    const pcm = this.native.codecDecode(this.handle, 1, n, codes);
+    const T = n * SAMPLES_PER_FRAME;
+    return [pcm.slice(0, T), pcm.slice(T, 2 * T)];
   }
 
   encodeWaveform(_waveform, _length) {
@@ -148,7 +164,10 @@ class HipTtsEngineImpl {
  * (createGpuEngineFor, gpu.ts:316-388).  `tables` = {global, local[, codec]}
  * WeightTables; options: {localHead, maxSlots (570), maxRows (= maxSlots),
  * layers (12: the count the model must resolve to), kvDtype ("f32" | "bf16"),
- * wrap (false: the reference's non-wrapping ring), device (0)}.
+ * wrap (false: the reference's non-wrapping ring), device (0), codecShape
+ * ({layersPerStage, contextPerStage}, the real shape by default),
+ * codecKvDtype ("f32")}.  With a codec table the codec decoder is set up
+ * for one voice (decodeFrames).
  */
 export async function createGpuEngineFor(tables, log, options) {
   const native = loadNative();
@@ -176,8 +195,22 @@ export async function createGpuEngineFor(tables, log, options) {
       bytes += t.data.byteLength;
     }
     log(`weights: ${tensors.length} tensors (${(bytes / 1e6).toFixed(0)} MB of GPU memory)`);
+    let codecShape = null;
+    if (tables.codec) {
+      codecShape = orDefault(options.codecShape, CODEC_SHAPE);
+      const codecTensors = resolveCodecTensors(tables.codec, codecShape);
+      for (const t of codecTensors) native.uploadTensor(handle, t.name, t.data, t.dims);
+      native.codecInit(handle, {
+        maxVoices: 1,
+        kvDtype: kvDtypeCode(native, options.codecKvDtype),
+        layers: codecShape.layersPerStage,
+        context: codecShape.contextPerStage,
+      });
+      log(`codec: ${codecTensors.length} tensors, stages ${codecShape.layersPerStage.join("/")}`);
+    }
     const info = { adapterName: "MI355X (gfx950, HIP)", deviceBytes: native.deviceBytes(handle) };
     const engine = new HipTtsEngineImpl(native, handle, info, options.localHead, maxSlots, maxRows, layers);
+    engine.hasCodec = codecShape !== null;
     log(`engine ready: ${layers} layers, KV ring ${maxSlots} slots, vocab ${vocab}`);
     const warm = await engine.warmup();
     log(`warmup: 1 prefill over ${warm.rows} rows in ${warm.prefillMs} ms`);

@@ -1,4 +1,5 @@
 import type { EngineWeights, LocalHeadSettings } from "./gpu";
+import type { CodecShape } from "./weights";
 
 export class MultiVoiceEngine {
   readonly maxVoices: number;
@@ -7,6 +8,8 @@ export class MultiVoiceEngine {
   generate(nFrames: number): Promise<{ frames: number[][][]; stopped: boolean[] }>;
   nextFrames(hidden: Float32Array[]): Promise<(number[] | null)[]>;
   decodeSteps(rows: Int32Array[], positions: number[]): Promise<Float32Array[]>;
+  /** codes[f][b] = 16 codes of voice b's frame f -> per voice [left, right] */
+  decodeAudio(codes: number[][][]): Promise<Float32Array[][]>;
   reset(voices?: number[]): void;
   dispose(): void;
 }
@@ -19,6 +22,8 @@ export type MultiVoiceOptions = {
   kvDtype?: "f32" | "bf16";
   wrap?: boolean;
   device?: number;
+  codecShape?: CodecShape;
+  codecKvDtype?: "f32" | "bf16";
 };
 
 export function createMultiVoiceEngine(

@@ -4,7 +4,9 @@
 // FIFO eviction), the codec ring's rule (kernels-decode.ts:590-714).
 import { HIDDEN, kvDtypeCode, loadNative, N_VQ, orDefault, ROW_WIDTH } from "./native.mjs";
 import { stageRows } from "./prefill.mjs";
-import { resolveEngineTensors } from "./weights.mjs";
+import { CODEC_SHAPE, resolveCodecTensors, resolveEngineTensors } from "./weights.mjs";
+
+const SAMPLES_PER_FRAME = 3840;
 
 export class MultiVoiceEngine {
   constructor(native, handle, maxVoices, capacity, maxRows) {
@@ -17,6 +19,7 @@ export class MultiVoiceEngine {
     this.hidden = null;
     this.positions = null;
     this.stopped = null;
+    this.hasCodec = false;
     this.disposed = false;
   }
 
@@ -85,11 +88,36 @@ export class MultiVoiceEngine {
     return Array.from({ length: B }, (_, b) => out.slice(b * HIDDEN, (b + 1) * HIDDEN));
   }
 
+  /**
+   * Codec: n frames for voices 0 .. B-1 at once, codes[f][b] = 16 codes of
+   * voice b's frame f; returns per voice [left, right] Float32Arrays of
+   * n * 3840 samples, continuing each voice's codec rings.
+   */
+  async decodeAudio(codes) {
+    if (!this.hasCodec) throw new Error("decodeAudio: the engine was created without codec weights");
+    const n = codes.length;
+    if (!n) return [];
+    const B = codes[0].length;
+    if (B < 1 || B > this.maxVoices) throw new Error(`decodeAudio of ${B} voices (max ${this.maxVoices})`);
+    const flat = new Int32Array(n * B * N_VQ);
+    for (let f = 0; f < n; f += 1) {
+      if (codes[f].length !== B) throw new Error(`frame ${f} has ${codes[f].length} voices, expected ${B}`);
+      for (let b = 0; b < B; b += 1) flat.set(codes[f][b].slice(0, N_VQ), (f * B + b) * N_VQ);
+    }
+    const pcm = this.native.codecDecode(this.handle, B, n, flat);
+    const T = n * SAMPLES_PER_FRAME;
+    return Array.from({ length: B }, (_, b) => [
+      pcm.slice((2 * b) * T, (2 * b + 1) * T),
+      pcm.slice((2 * b + 1) * T, (2 * b + 2) * T),
+    ]);
+  }
+
   /** Empty the rings and repetition history of some voices (all when omitted). */
   reset(voices) {
     const ids = voices ? Int32Array.from(voices) : null;
     this.native.ringReset(this.handle, ids);
     this.native.clearSeen(this.handle, ids);
+    if (this.hasCodec) this.native.codecReset(this.handle, ids);
   }
 
   dispose() {
@@ -101,7 +129,9 @@ export class MultiVoiceEngine {
 
 /**
  * A context for `maxVoices` voices: options {localHead, maxVoices, capacity
- * (1024), maxRows (capacity), kvDtype ("bf16"), wrap (true), device (0)}.
+ * (1024), maxRows (capacity), kvDtype ("bf16"), wrap (true), device (0),
+ * codecShape, codecKvDtype ("bf16")}; a `codec` table sets up the codec for
+ * every voice (decodeAudio).
  */
 export async function createMultiVoiceEngine(tables, log, options) {
   const native = loadNative();
@@ -122,8 +152,24 @@ export async function createMultiVoiceEngine(tables, log, options) {
     for (const t of tensors) native.uploadTensor(handle, t.name, t.data, t.dims);
     const s = options.localHead;
     native.setLocalHead(handle, s.audioEndTokenId, s.audioAssistantSlotTokenId, s.repetitionPenalty);
+    let hasCodec = false;
+    if (tables.codec) {
+      const shape = orDefault(options.codecShape, CODEC_SHAPE);
+      for (const t of resolveCodecTensors(tables.codec, shape)) {
+        native.uploadTensor(handle, t.name, t.data, t.dims);
+      }
+      native.codecInit(handle, {
+        maxVoices: options.maxVoices,
+        kvDtype: kvDtypeCode(native, orDefault(options.codecKvDtype, "bf16")),
+        layers: shape.layersPerStage,
+        context: shape.contextPerStage,
+      });
+      hasCodec = true;
+    }
     if (log) log(`multi-voice engine: ${options.maxVoices} voices, ${layers} layers, ring ${capacity}`);
-    return new MultiVoiceEngine(native, handle, options.maxVoices, capacity, maxRows);
+    const engine = new MultiVoiceEngine(native, handle, options.maxVoices, capacity, maxRows);
+    engine.hasCodec = hasCodec;
+    return engine;
   } catch (error) {
     native.destroy(handle);
     throw error;

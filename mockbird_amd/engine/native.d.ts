@@ -76,6 +76,13 @@ export interface Native {
     hidden: Float32Array,
     pos: Int32Array,
   ): { codes: Int32Array; cont: Int32Array };
+  codecInit(
+    h: NativeHandle,
+    config?: { maxVoices?: number; kvDtype?: number; layers?: number[]; context?: number[] },
+  ): void;
+  codecReset(h: NativeHandle, voices: Int32Array | null): void;
+  /** codes [nFrames][B][16] -> pcm [B][2][nFrames * 3840] */
+  codecDecode(h: NativeHandle, B: number, nFrames: number, codes: Int32Array): Float32Array;
   lastError(h: NativeHandle): string;
 }
 

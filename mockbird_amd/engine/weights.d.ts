@@ -23,3 +23,11 @@ export function resolveEngineTensors(tables: { global: WeightTable; local: Weigh
   vocab: number;
   layers: number;
 };
+
+/** Layers and ring windows (positions) per codec stage. */
+export type CodecShape = { layersPerStage: number[]; contextPerStage: number[] };
+export const CODEC_SHAPE: CodecShape;
+export function resolveCodecTensors(
+  table: WeightTable,
+  shape?: CodecShape,
+): { name: string; dims: number[]; data: Float32Array }[];

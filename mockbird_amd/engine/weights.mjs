@@ -150,3 +150,89 @@ export function resolveEngineTensors(tables) {
   }
   return { tensors: out, vocab, layers };
 }
+
+/** The codec's default shape (codec.ts:1-30): layers and ring windows per stage. */
+export const CODEC_SHAPE = { layersPerStage: [4, 2, 2, 4], contextPerStage: [500, 1696, 2480, 3248] };
+
+const CODEC_D = 256;
+const CODEC_DECODER = [1, 3, 5, 7];
+
+/**
+ * The codec's tensors under the names mb_codec_* uploads by, from the codec
+ * WeightTable, resolved as resolveCodecWeights does (decodeWeights.ts:69-156):
+ * a matrix by name when the table has it, else by shape and offset order --
+ * the [256,768] run holds, stage by stage, each layer's attention input and
+ * then the stage's output projection (the last stage's is [256,240]); the
+ * [256,256], [256,1024] and [1024,256] runs hold one block per layer; stage 1
+ * reads [192,256], the others [384,256] in order; the 16 RVQ convolutions are
+ * the [512,8,1] run and the output projection the [768,512,1] block.
+ * Norms, layer scales, quantiser biases and codebooks are taken by name.
+ */
+export function resolveCodecTensors(table, shape) {
+  const layersPerStage = (shape || CODEC_SHAPE).layersPerStage;
+  const out = [];
+  const pick = (name, dims, list, index) => {
+    const key = dims.join("x");
+    if (table.has(name)) {
+      const t = table.get(name);
+      if (t.dims.join("x") !== key && !(t.dims.length === dims.length + 1 && t.dims[dims.length] === 1 &&
+          t.dims.slice(0, dims.length).join("x") === key)) {
+        throw new Error(`codec weight has the wrong shape: ${name} is ${t.dims.join("x")}, expected ${key}`);
+      }
+      return t.data;
+    }
+    if (!list[index]) throw new Error(`codec: no ${key} block at index ${index} for ${name}`);
+    return list[index];
+  };
+  const named = (name, dims) => out.push({ name, dims, data: table.get(name).data });
+  const wide = table.byShape(`${CODEC_D}x768`);
+  const convs = table.byShape("512x8x1");
+  for (let k = 0; k < N_VQ; k += 1) {
+    const p = `model.quantizer.quantizers.${k}.`;
+    out.push({ name: p + "out_proj.weight", dims: [512, 8], data: pick(p + "out_proj.weight", [512, 8], convs, k) });
+    named(p + "out_proj.bias", [512]);
+    named(p + "codebook.weight", [CODEBOOK, 8]);
+  }
+  out.push({
+    name: "model.quantizer.output_proj.weight",
+    dims: [768, 512],
+    data: pick("model.quantizer.output_proj.weight", [768, 512], table.byShape("768x512x1"), 0),
+  });
+  named("model.quantizer.output_proj.bias", [768]);
+  let cursor = 0;
+  let layer = 0;
+  const last = layersPerStage.length - 1;
+  for (let s = 0; s < layersPerStage.length; s += 1) {
+    const p = `model.decoder.${CODEC_DECODER[s]}.`;
+    const inW = s === 0 ? 192 : 384;
+    out.push({
+      name: p + "input_proj.weight",
+      dims: [inW, CODEC_D],
+      data: pick(p + "input_proj.weight", [inW, CODEC_D], table.byShape(`${inW}x${CODEC_D}`), s === 0 ? 0 : s - 1),
+    });
+    for (let i = 0; i < layersPerStage[s]; i += 1, layer += 1) {
+      const q = `${p}transformer.layers.${i}.`;
+      const mats = [
+        ["self_attn.in_proj.weight", [CODEC_D, 3 * CODEC_D], wide, cursor],
+        ["self_attn.out_proj.weight", [CODEC_D, CODEC_D], table.byShape(`${CODEC_D}x${CODEC_D}`), layer],
+        ["ffn.0.weight", [CODEC_D, 1024], table.byShape(`${CODEC_D}x1024`), layer],
+        ["ffn.2.weight", [1024, CODEC_D], table.byShape(`1024x${CODEC_D}`), layer],
+      ];
+      for (const [suffix, dims, list, index] of mats) {
+        out.push({ name: q + suffix, dims, data: pick(q + suffix, dims, list, index) });
+      }
+      cursor += 1;
+      for (const n of ["norm1.weight", "norm1.bias", "norm2.weight", "norm2.bias",
+                       "layer_scale_1.scale", "layer_scale_2.scale"]) named(q + n, [CODEC_D]);
+    }
+    const outW = s === last ? 240 : 768;
+    const list = s === last ? table.byShape(`${CODEC_D}x240`) : wide;
+    out.push({
+      name: p + "output_proj.weight",
+      dims: [CODEC_D, outW],
+      data: pick(p + "output_proj.weight", [CODEC_D, outW], list, s === last ? 0 : cursor),
+    });
+    if (s !== last) cursor += 1;
+  }
+  return out;
+}

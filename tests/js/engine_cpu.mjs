@@ -5,7 +5,7 @@
 // before any device call.  Prints one JSON object.
 import { loadNative } from "../../mockbird_amd/engine/native.mjs";
 import { createGpuEngine, EngineNotImplemented, frameRowFrom } from "../../mockbird_amd/engine/gpu.mjs";
-import { resolveEngineTensors, tableOf } from "../../mockbird_amd/engine/weights.mjs";
+import { resolveCodecTensors, resolveEngineTensors, tableOf } from "../../mockbird_amd/engine/weights.mjs";
 import { stageRows } from "../../mockbird_amd/engine/prefill.mjs";
 
 const out = {};
@@ -59,6 +59,37 @@ const r = resolveEngineTensors({ global, local });
 out.vocab = r.vocab;
 out.layers = r.layers;
 out.resolved = r.tensors.map((x) => [x.name, x.dims, x.data[0]]);
+
+// a codec table in the sidecar's order, every projection anonymous: per
+// stage the input projection, then per layer in_proj, out_proj, ffn.0, ffn.2
+// and the named norms / scales, then the stage output; the RVQ front's 16
+// convolutions and output projection are anonymous too
+const c = new Map();
+offset = 0;
+const dec = [1, 3, 5, 7];
+const codecLayers = [2, 1, 1, 2];
+for (let k = 0; k < 16; k += 1) {
+  add(c, `onnx::Conv_rvq_${k}`, [512, 8, 1]);
+  add(c, `model.quantizer.quantizers.${k}.out_proj.bias`, [512]);
+  add(c, `model.quantizer.quantizers.${k}.codebook.weight`, [1024, 8]);
+}
+add(c, "onnx::Conv_rvq_out", [768, 512, 1]);
+add(c, "model.quantizer.output_proj.bias", [768]);
+for (let s = 0; s < 4; s += 1) {
+  add(c, `onnx::MatMul_in_${s}`, [s === 0 ? 192 : 384, 256]);
+  for (let i = 0; i < codecLayers[s]; i += 1) {
+    const p = `model.decoder.${dec[s]}.transformer.layers.${i}.`;
+    add(c, `onnx::MatMul_qkv_${s}_${i}`, [256, 768]);
+    add(c, `onnx::MatMul_o_${s}_${i}`, [256, 256]);
+    add(c, `onnx::MatMul_f0_${s}_${i}`, [256, 1024]);
+    add(c, `onnx::MatMul_f2_${s}_${i}`, [1024, 256]);
+    for (const n of ["norm1.weight", "norm1.bias", "norm2.weight", "norm2.bias",
+                     "layer_scale_1.scale", "layer_scale_2.scale"]) add(c, p + n, [256]);
+  }
+  add(c, `onnx::MatMul_out_${s}`, [256, s === 3 ? 240 : 768]);
+}
+out.codec = resolveCodecTensors(tableOf(c), { layersPerStage: codecLayers, contextPerStage: [6, 12, 20, 40] })
+  .map((x) => [x.name, x.dims, x.data[0]]);
 
 // staging and frame rows
 out.staged = Array.from(stageRows([[6], [8, 1, 2, 3]]));

@@ -16,7 +16,9 @@ const spec = JSON.parse(fs.readFileSync(path.join(dir, "case.json"), "utf8"));
 const tables = {
   global: loadSidecarTable(path.join(dir, "global.json")),
   local: loadSidecarTable(path.join(dir, "local.json")),
+  codec: loadSidecarTable(path.join(dir, "codec.json")),
 };
+const codecShape = { layersPerStage: spec.codec.layers, contextPerStage: spec.codec.context };
 const localHead = { audioEndTokenId: 7, audioAssistantSlotTokenId: 9, repetitionPenalty: 1.2 };
 const out = { log: [] };
 const log = (m) => {
@@ -29,6 +31,7 @@ async function single() {
     localHead,
     maxSlots: spec.maxSlots,
     layers: spec.layers,
+    codecShape,
   });
   const prompt = spec.prompts[0];
   engine.reset();
@@ -47,6 +50,11 @@ async function single() {
     res.hiddens.push(Array.from(hidden));
   }
   res.position = engine.position;
+  // the codec: the voice's code frames over two calls (the rings carry over)
+  const codes = spec.codec.single;
+  const a = await engine.decodeFrames(codes.slice(0, 2));
+  const b = await engine.decodeFrames(codes.slice(2));
+  res.pcm = [0, 1].map((c) => Array.from(a[c]).concat(Array.from(b[c])));
   // the reference's ring never wraps: a position past it throws (decode.ts:719-724)
   try {
     await engine.decodeStep({ row: frameRowFrom(9, res.frames[0]), position: spec.maxSlots });
@@ -71,11 +79,19 @@ async function multi() {
     maxVoices: spec.prompts.length,
     capacity: spec.maxSlots,
     kvDtype: "f32",
+    codecShape,
+    codecKvDtype: "f32",
   });
   const hidden = await engine.prefill(spec.prompts);
   const gen = await engine.generate(spec.frames);
+  const audio = await engine.decodeAudio(spec.codec.multi);
   engine.dispose();
-  return { prefillHidden: hidden.map((h) => Array.from(h)), frames: gen.frames, stopped: gen.stopped };
+  return {
+    prefillHidden: hidden.map((h) => Array.from(h)),
+    frames: gen.frames,
+    stopped: gen.stopped,
+    pcm: audio.map((ch) => ch.map((x) => Array.from(x))),
+  };
 }
 
 // Node 12 has no top-level await

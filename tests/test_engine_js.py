@@ -15,7 +15,7 @@ BINDINGS = {
     "KV", "abiVersion", "cancel", "clearSeen", "create", "decodeAttention", "decodeFrames",
     "decodeStep", "destroy", "deviceBytes", "lastError", "localFrame", "localSteps", "prefill",
     "prefillAttention", "readRing", "ringAppend", "ringPoison", "ringReset", "ringWriteRows",
-    "setLocalHead", "uploadTensor",
+    "setLocalHead", "uploadTensor", "codecInit", "codecReset", "codecDecode",
 }
 
 
@@ -72,3 +72,30 @@ def test_errors_throw_before_device_calls(report):
     assert e["badConfig"][0] == "MB_ERR_ARG"
     assert e["badHandle"][0] == "TypeError"
     assert e["notImplemented"] == [True, "EngineNotImplemented"]
+
+
+def test_codec_table_resolves_by_shape_and_order(report):
+    """resolveCodecTensors follows resolveCodecWeights (decodeWeights.ts:69-156):
+    the [256,768] run alternates layer inputs and stage outputs, the per-layer
+    runs go by layer, the RVQ convolutions by quantiser."""
+    tags = report["tags"]
+    got = {name: (dims, tag) for name, dims, tag in report["codec"]}
+    dec = (1, 3, 5, 7)
+    layers = (2, 1, 1, 2)
+    for k in range(16):
+        assert got[f"model.quantizer.quantizers.{k}.out_proj.weight"] == ([512, 8], tags[f"onnx::Conv_rvq_{k}"])
+        assert got[f"model.quantizer.quantizers.{k}.codebook.weight"][1] == \
+            tags[f"model.quantizer.quantizers.{k}.codebook.weight"]
+    assert got["model.quantizer.output_proj.weight"] == ([768, 512], tags["onnx::Conv_rvq_out"])
+    for s in range(4):
+        p = f"model.decoder.{dec[s]}."
+        assert got[p + "input_proj.weight"][1] == tags[f"onnx::MatMul_in_{s}"]
+        assert got[p + "output_proj.weight"] == ([256, 240 if s == 3 else 768], tags[f"onnx::MatMul_out_{s}"])
+        for i in range(layers[s]):
+            q = p + f"transformer.layers.{i}."
+            assert got[q + "self_attn.in_proj.weight"][1] == tags[f"onnx::MatMul_qkv_{s}_{i}"]
+            assert got[q + "self_attn.out_proj.weight"][1] == tags[f"onnx::MatMul_o_{s}_{i}"]
+            assert got[q + "ffn.0.weight"][1] == tags[f"onnx::MatMul_f0_{s}_{i}"]
+            assert got[q + "ffn.2.weight"][1] == tags[f"onnx::MatMul_f2_{s}_{i}"]
+            assert got[q + "layer_scale_2.scale"][1] == tags[q + "layer_scale_2.scale"]
+    assert len(got) == 16 * 3 + 2 + 4 * 2 + sum(layers) * 10

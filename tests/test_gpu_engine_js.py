@@ -26,6 +26,7 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 L, V, C, FRAMES = 2, 64, 128, 6
 NEAR_TIE = 2e-5
+CODEC_LAYERS, CODEC_CONTEXT = (1, 1, 1, 2), (6, 12, 20, 40)
 
 
 def _tables(w, tmp):
@@ -38,6 +39,21 @@ def _tables(w, tmp):
         (loc if name.startswith("model.") else glob).append((key, arr))
     write_sidecar(os.path.join(tmp, "global.json"), glob)
     write_sidecar(os.path.join(tmp, "local.json"), loc)
+
+
+def _codec_table(cw, tmp):
+    """The codec weights in the sidecar's order with every projection under an
+    anonymous name and the 1x1 convolutions in their graph shape [., ., 1]."""
+    entries = []
+    for i, (name, arr) in enumerate(cw.items()):
+        if name.endswith("out_proj.weight") and name.startswith("model.quantizer") or \
+                name == "model.quantizer.output_proj.weight":
+            entries.append((f"onnx::Conv_{i}", arr.reshape(arr.shape + (1,))))
+        elif arr.ndim == 2 and "codebook" not in name:
+            entries.append((f"onnx::MatMul_c{i}", arr))
+        else:
+            entries.append((name, arr))
+    write_sidecar(os.path.join(tmp, "codec.json"), entries)
 
 
 def _oracle_frames(m, prompt, frames):
@@ -78,7 +94,13 @@ def test_engine_runtime_loop_and_multivoice_match_oracle(tmp_path):
     w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]  # never stops
     prompts = [synth.prompt(40 + b, n_frames=4 + 5 * b, n_text=6 + b, vocab=V) for b in range(3)]
     _tables(w, str(tmp_path))
-    spec = {"layers": L, "maxSlots": C, "frames": FRAMES, "prompts": [p.tolist() for p in prompts]}
+    cw = synth.codec_weights(CODEC_LAYERS, seed=12)
+    _codec_table(cw, str(tmp_path))
+    codes1 = synth.codec_codes(31, 4, 1)
+    codes3 = synth.codec_codes(32, 3, 3)
+    spec = {"layers": L, "maxSlots": C, "frames": FRAMES, "prompts": [p.tolist() for p in prompts],
+            "codec": {"layers": list(CODEC_LAYERS), "context": list(CODEC_CONTEXT),
+                      "single": codes1[:, 0].tolist(), "multi": codes3.tolist()}}
     (tmp_path / "case.json").write_text(json.dumps(spec))
     say("JS engine: single-voice runtime loop + 3-voice MultiVoiceEngine")
     r = subprocess.run(["node", os.path.join(ROOT, "tests", "js", "engine_run.mjs"), str(tmp_path)],
@@ -110,3 +132,17 @@ def test_engine_runtime_loop_and_multivoice_match_oracle(tmp_path):
         assert not mv["stopped"][b]
         n = _check_codes(mv["frames"][b], ref, f"voice {b}")
         say(f"  multi-voice {b}: {n} of {FRAMES} frames bit-exact")
+
+    # the codec through GpuTtsEngine.decodeFrames (one voice, two calls) and
+    # MultiVoiceEngine.decodeAudio (3 voices), fp32 rings: within 2e-5 of scale
+    ora = oracle.CodecOracle(cw, 1, CODEC_LAYERS, CODEC_CONTEXT)
+    want = ora.decode(codes1)[0]
+    got = np.array(s["pcm"], np.float32)
+    assert got.shape == want.shape
+    assert np.abs(got - want).max() <= 2e-5 * np.abs(want).max()
+    ora3 = oracle.CodecOracle(cw, 3, CODEC_LAYERS, CODEC_CONTEXT)
+    want3 = ora3.decode(codes3)
+    got3 = np.array(mv["pcm"], np.float32)
+    assert got3.shape == want3.shape
+    assert np.abs(got3 - want3).max() <= 2e-5 * np.abs(want3).max()
+    say("  codec: decodeFrames and decodeAudio match the oracle")
