@@ -347,7 +347,10 @@ int mb_codec_reset(mb_ctx* ctx, int n, const int32_t* voices);
 int mb_codec_decode(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm);
 
 /* Device-pointer form of mb_codec_decode (codes and pcm in device memory;
- * a code outside [0, 1024) contributes no codebook row).  Enqueue only. */
+ * a code outside [0, 1024) contributes no codebook row).  The first frame
+ * runs as ordinary launches and the next ones replay it from a HIP graph,
+ * captured once and kept while B, the pointers and the context's buffers
+ * stay the same.  Enqueue only. */
 int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm);
 
 /* Parity read-back of one codec layer's ring for one voice (layers numbered

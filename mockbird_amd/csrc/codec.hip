@@ -73,7 +73,11 @@ struct CodecState {
   int32_t* nrow = nullptr;  // [4][max_voices]: positions per frame of each stage
   float *acc = nullptr, *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr,
         *att = nullptr, *ffn = nullptr, *wide = nullptr;
+  int32_t* frame = nullptr;  // the frame a decode call is at (device counter)
   std::vector<void*> owned;
+  // one captured frame of mb_codec_decode_dev and what it was captured for
+  hipGraphExec_t exec = nullptr;
+  uint64_t key[6] = {};
   // resolved weights
   const float *rvq_w = nullptr, *rvq_b = nullptr, *rvq_book = nullptr, *rvq_out = nullptr,
               *rvq_out_b = nullptr;
@@ -89,7 +93,10 @@ int positions(int s) { return 4 << s; }
 // acc[b][n] = sum_k (W_k[n] . codebook_k[code_k] + b_k[n]) in quantiser
 // order, each dot over the 8 entry values in order (RVQ_ACCUM,
 // kernels-decode.ts:537-558).  A code outside [0, 1024) adds no codebook row.
-__global__ __launch_bounds__(256) void k_rvq_accum(const int32_t* __restrict__ codes, int B,
+// `frame` is the device frame counter: codes of the current frame start at
+// codes + frame * B * 16.
+__global__ __launch_bounds__(256) void k_rvq_accum(const int32_t* __restrict__ codes_all,
+                                                   const int32_t* __restrict__ frame, int B,
                                                    const float* __restrict__ w,
                                                    const float* __restrict__ bias,
                                                    const float* __restrict__ book,
@@ -97,6 +104,7 @@ __global__ __launch_bounds__(256) void k_rvq_accum(const int32_t* __restrict__ c
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)B * kRvq) return;
   const int b = (int)(t / kRvq), n = (int)(t % kRvq);
+  const int32_t* codes = codes_all + (int64_t)*frame * B * NVQ;
   float a = 0.f;
   for (int k = 0; k < NVQ; k++) {
     const int32_t code = codes[(int64_t)b * NVQ + k];
@@ -129,9 +137,11 @@ __global__ __launch_bounds__(256) void k_gather_cols(const float* __restrict__ s
 // last stage's output columns are already (channel, sample) ordered, so the
 // head (CODEC_HEAD, kernels-decode.ts:747-768) is this copy.
 __global__ __launch_bounds__(256) void k_codec_head(const float* __restrict__ latent, int B,
-                                                    int f, int64_t T, float* __restrict__ pcm) {
+                                                    const int32_t* __restrict__ frame, int64_t T,
+                                                    float* __restrict__ pcm) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= (int64_t)B * 2 * kSamples) return;
+  const int f = *frame;
   const int b = (int)(t / (2 * kSamples));
   const int rest = (int)(t % (2 * kSamples));
   const int c = rest / kSamples, i = rest % kSamples, pos = i / 120, j = i % 120;
@@ -305,14 +315,16 @@ int codec_resolve(mb_ctx* ctx) {
   return MB_OK;
 }
 
-// One frame for voices b < B: codes [B][16] (device) -> pcm frame f of
-// [B][2][T].  Every launch is on the context's stream.
-int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T, int f) {
+// One frame for voices b < B: the frame *cs.frame of codes [n][B][16]
+// (device) -> that frame of pcm [B][2][T], then the counter advances.  Every
+// launch is on the context's stream and reads the frame index from the
+// device, so the same launches serve every frame (one captured graph).
+int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T) {
   CodecState& cs = *ctx->codec;
   const int V = cs.cfg.max_voices;
   int rc;
   hipLaunchKernelGGL(k_rvq_accum, dim3((unsigned)(((int64_t)B * kRvq + 255) / 256)), dim3(256), 0,
-                     ctx->stream, codes, B, cs.rvq_w, cs.rvq_b, cs.rvq_book, cs.acc);
+                     ctx->stream, codes, cs.frame, B, cs.rvq_w, cs.rvq_b, cs.rvq_book, cs.acc);
   MB_HIP(ctx, hipGetLastError());
   if ((rc = launch_gemm(ctx, EPI_STORE, cs.acc, kRvq, cs.rvq_out, kRvqOut, kRvq, cs.rvq_out_b,
                         cs.wide, kRvqOut, B)))
@@ -349,7 +361,8 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T,
     in_w = 384;
   }
   hipLaunchKernelGGL(k_codec_head, dim3((unsigned)(((int64_t)B * 2 * kSamples + 255) / 256)),
-                     dim3(256), 0, ctx->stream, cs.wide, B, f, T, pcm);
+                     dim3(256), 0, ctx->stream, cs.wide, B, cs.frame, T, pcm);
+  hipLaunchKernelGGL(k_add_i32, dim3(1), dim3(256), 0, ctx->stream, cs.frame, 1, 1);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
@@ -368,6 +381,7 @@ void codec_free(mb_ctx* ctx) {
   if (!ctx->codec) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->codec->exec) (void)hipGraphExecDestroy(ctx->codec->exec);
   for (void* p : ctx->codec->owned) (void)hipFree(p);
   delete ctx->codec;
   ctx->codec = nullptr;
@@ -415,6 +429,7 @@ extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
   cs->slot_pos = (int32_t*)dev_alloc(ctx, *cs, (size_t)sp * 4);
   cs->pos = (int32_t*)dev_alloc(ctx, *cs, (size_t)kStages * V * 4);
   cs->nrow = (int32_t*)dev_alloc(ctx, *cs, (size_t)kStages * V * 4);
+  cs->frame = (int32_t*)dev_alloc(ctx, *cs, 4);
   cs->acc = (float*)dev_alloc(ctx, *cs, (size_t)V * kRvq * 4);
   cs->x = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
   cs->h = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
@@ -424,6 +439,7 @@ extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
   cs->ffn = (float*)dev_alloc(ctx, *cs, (size_t)rows * kFfn * 4);
   cs->wide = (float*)dev_alloc(ctx, *cs, (size_t)rows * kRvqOut * 4);
   for (void* p : {cs->ring_k, cs->ring_v, (void*)cs->slot_pos, (void*)cs->pos, (void*)cs->nrow,
+                  (void*)cs->frame,
                   (void*)cs->acc, (void*)cs->x, (void*)cs->h, (void*)cs->qkv, (void*)cs->q,
                   (void*)cs->att, (void*)cs->ffn, (void*)cs->wide})
     if (!p) {
@@ -477,10 +493,48 @@ extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32
   if (rc) return rc;
   if (B == 0 || n_frames == 0) return MB_OK;
   if (!codes || !pcm) return fail(ctx, MB_ERR_ARG, "mb_codec_decode_dev: null pointer");
+  CodecState& cs = *ctx->codec;
   const int64_t T = (int64_t)n_frames * kSamples;
-  for (int f = 0; f < n_frames; f++) {
+  if ((rc = cancelled(ctx))) return rc;
+  if ((rc = launch_fill_i32(ctx, cs.frame, 1, 0))) return rc;
+  // Frame 0 runs eagerly (it sizes every scratch buffer a frame touches, so
+  // nothing is allocated during the capture); the next frames replay it
+  // from a HIP graph, captured once per (B, codes, pcm, T) and buffer set.
+  if ((rc = codec_frame(ctx, B, codes, pcm, T))) return rc;
+  if (n_frames == 1) return MB_OK;
+  const uint64_t key[6] = {(uint64_t)B, (uint64_t)(uintptr_t)codes, (uint64_t)(uintptr_t)pcm,
+                           (uint64_t)T, ctx->graph_gen, 1};
+  if (!cs.exec || memcmp(key, cs.key, sizeof key) != 0) {
+    if (cs.exec) {
+      MB_HIP(ctx, hipGraphExecDestroy(cs.exec));
+      cs.exec = nullptr;
+    }
+    if (!ctx->capture_stream)
+      MB_HIP(ctx, hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking));
+    hipStream_t saved = ctx->stream;
+    ctx->stream = ctx->capture_stream;
+    MB_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    rc = codec_frame(ctx, B, codes, pcm, T);
+    hipGraph_t graph = nullptr;
+    const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    ctx->stream = saved;
+    if (rc || e != hipSuccess || ctx->graph_gen != key[4]) {
+      if (graph) (void)hipGraphDestroy(graph);
+      if (rc) return rc;
+      if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamEndCapture");
+      return fail(ctx, MB_ERR_STATE, "a buffer moved while the codec frame was captured");
+    }
+    const hipError_t ei = hipGraphInstantiate(&cs.exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ei != hipSuccess) {
+      cs.exec = nullptr;
+      return hip_fail(ctx, ei, "hipGraphInstantiate");
+    }
+    memcpy(cs.key, key, sizeof key);
+  }
+  for (int f = 1; f < n_frames; f++) {
     if ((rc = cancelled(ctx))) return rc;
-    if ((rc = codec_frame(ctx, B, codes + (int64_t)f * B * NVQ, pcm, T, f))) return rc;
+    MB_HIP(ctx, hipGraphLaunch(cs.exec, ctx->stream));
   }
   return MB_OK;
 }

@@ -461,14 +461,19 @@ __global__ __launch_bounds__(256) void k_flash_f32(
 // positions per frame and attend over windows of 500..3248.  A workgroup is
 // one (sequence, head); its NW waves split the slot range into contiguous
 // runs of 16-slot groups, and each wave computes every query of the chunk
-// against its run, reading K and V straight from HBM into MFMA operands
-// (no LDS staging), with v_mfma_f32_16x16x4f32:
-//  - scores S^T[16 slots][16 queries]: lane l feeds K[slot l%16][16g + kc]
-//    and Q[query l%16][16g + kc] (g = l/16) in step kc, so it loads 16
-//    contiguous dims of one K row;
-//  - P V: output block d row i is dim 4i + d, so in step j lane l feeds
-//    V[slot (l/16)*4 + j][4(l%16) + d] -- 4 contiguous dims -- and its own
-//    score element j as P^T.
+// against its run, reading K and V straight from HBM into MFMA operands (no
+// LDS staging).  Scores are S^T[16 slots][16 queries]; the P V output block
+// d holds dims 4i + d in row i, so in the step for slot 4g + j (g = lane/16)
+// a lane feeds 4 contiguous dims of that V row and its own score element j.
+//  - fp32 rings: v_mfma_f32_16x16x4f32; lane l feeds K[slot l%16][16g + kc]
+//    and Q[query l%16][16g + kc] in step kc (16 contiguous K dims per lane).
+//  - bf16 rings: v_mfma_f32_16x16x32_bf16 for the scores (lane l feeds 8
+//    contiguous K dims 32c + 8g.. of its slot) and v_mfma_f32_16x16x16bf16_1k
+//    for P V (lane l feeds 4 slots 4g..4g+3 of dim 4(l%16) + d, packed from
+//    its four 8-byte V loads).  K and V are exact in bf16; q and P are split
+//    into a bf16 high part and a bf16 remainder, two MFMAs each, so the
+//    products keep about 16 bits (the scores and weights agree with the fp32
+//    path to ~1e-5 relative) at an eighth of the fp32 MFMA time.
 // Partials (max, sum, 64 dims per query) fold across the waves through LDS.
 // Liveness is the window rule: slot position p (empty slots never live) is
 // visible to a query at cur iff 0 <= cur - p < W.
@@ -497,17 +502,33 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
   // outside every window.
   constexpr int32_t kFar = 1 << 30;
   int32_t crel[QB];
+  // fp32: dims 16g .. 16g+15; bf16: dims 32c + 8g .. +7 for c = 0, 1
   float qv[QB][16];
 #pragma unroll
   for (int qb = 0; qb < QB; qb++) {
     const int r = qb * 16 + qc;
     crel[qb] = r < n ? r : -kFar;
-    const float* qp = q + (r < n ? row_at(q_rows, b, r) : 0) + h * HD + g * 16;
+    const float* qp = q + (r < n ? row_at(q_rows, b, r) : 0) + h * HD;
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
-      const float4 t = r < n ? *(const float4*)(qp + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int dim = KV_BF16 ? (i >> 3) * 32 + g * 8 + (i & 7) : g * 16 + i;
+      const float4 t = r < n ? *(const float4*)(qp + dim) : make_float4(0.f, 0.f, 0.f, 0.f);
       qv[qb][i] = t.x; qv[qb][i + 1] = t.y; qv[qb][i + 2] = t.z; qv[qb][i + 3] = t.w;
     }
+  }
+  bf16x8_t qh[QB][2], ql[QB][2];
+  if constexpr (KV_BF16) {
+#pragma unroll
+    for (int qb = 0; qb < QB; qb++)
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float x = qv[qb][c * 8 + e];
+          const __bf16 hi = (__bf16)x;
+          qh[qb][c][e] = hi;
+          ql[qb][c][e] = (__bf16)(x - (float)hi);
+        }
   }
   constexpr int E = KV_BF16 ? 2 : 4;
   const char* kb = (const char*)ring_k + ((int64_t)b * ring_seq_stride + (int64_t)h * C * HD) * E;
@@ -528,14 +549,16 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
 
   for (int gi = g0; gi < g1; gi++) {
     const int s0 = gi * 16;
-    // K: 16 contiguous dims of slot s0 + qc; V: 4 dims of slots s0 + 4g + j
-    float kf[16], vf[4][4];
     const int ks = min(s0 + qc, kv_end - 1);
-    if (KV_BF16) {
-      const uint4 a = *(const uint4*)(kb + ((int64_t)ks * HD + g * 16) * 2);
-      const uint4 c = *(const uint4*)(kb + ((int64_t)ks * HD + g * 16 + 8) * 2);
-      unpack<true>(a, kf);
-      unpack<true>(c, kf + 8);
+    // K: the lane's slot s0 + qc; V: 4 dims of slots s0 + 4g + j
+    float kf[16];
+    bf16x8_t kh[2];
+    float vf[4][4];
+    uint2 vw[4];
+    if constexpr (KV_BF16) {
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+        kh[c] = __builtin_bit_cast(bf16x8_t, *(const uint4*)(kb + ((int64_t)ks * HD + c * 32 + g * 8) * 2));
     } else {
 #pragma unroll
       for (int i = 0; i < 16; i += 4) {
@@ -548,10 +571,8 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
     for (int j = 0; j < 4; j++) {
       const int sl = s0 + 4 * g + j;
       const int vs = min(sl, kv_end - 1);
-      if (KV_BF16) {
-        const uint2 t = *(const uint2*)(vb + ((int64_t)vs * HD + 4 * qc) * 2);
-        vf[j][0] = bf16_lo(t.x); vf[j][1] = bf16_hi(t.x);
-        vf[j][2] = bf16_lo(t.y); vf[j][3] = bf16_hi(t.y);
+      if constexpr (KV_BF16) {
+        vw[j] = *(const uint2*)(vb + ((int64_t)vs * HD + 4 * qc) * 2);
       } else {
         const float4 t = *(const float4*)(vb + ((int64_t)vs * HD + 4 * qc) * 4);
         vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
@@ -560,12 +581,32 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
       const int64_t d = (int64_t)p - p0;
       pj[j] = p < 0 ? kFar : (int32_t)(d < -kFar ? -kFar : d > kFar ? kFar : d);
     }
+    // bf16 P V operands: for block d, slots 4g..4g+3 of dim 4qc + d
+    i16x4_t va[4];
+    if constexpr (KV_BF16) {
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+        const int w = d >> 1;
+        const uint32_t lo = __builtin_amdgcn_perm(w ? vw[1].y : vw[1].x, w ? vw[0].y : vw[0].x, sel);
+        const uint32_t hi = __builtin_amdgcn_perm(w ? vw[3].y : vw[3].x, w ? vw[2].y : vw[2].x, sel);
+        va[d] = __builtin_bit_cast(i16x4_t, make_uint2(lo, hi));
+      }
+    }
 #pragma unroll
     for (int qb = 0; qb < QB; qb++) {
       f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KV_BF16) {
 #pragma unroll
-      for (int kc = 0; kc < 16; kc++)
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kc], qv[qb][kc], sc, 0, 0, 0);
+        for (int c = 0; c < 2; c++) {
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[c], qh[qb][c], sc, 0, 0, 0);
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh[c], ql[qb][c], sc, 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < 16; kc++)
+          sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kc], qv[qb][kc], sc, 0, 0, 0);
+      }
       float t[4];
       float mt = -INFINITY;
 #pragma unroll
@@ -592,11 +633,26 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
         ls += pw[j];
       }
       l[qb] += col_sum(ls);
+      if constexpr (KV_BF16) {
+        i16x4_t ph, pl;
 #pragma unroll
-      for (int j = 0; j < 4; j++)
+        for (int j = 0; j < 4; j++) {
+          const __bf16 hi = (__bf16)pw[j];
+          ph[j] = __builtin_bit_cast(short, hi);
+          pl[j] = __builtin_bit_cast(short, (__bf16)(pw[j] - (float)hi));
+        }
 #pragma unroll
-        for (int d = 0; d < 4; d++)
-          acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j][d], pw[j], acc[qb][d], 0, 0, 0);
+        for (int d = 0; d < 4; d++) {
+          acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[d], ph, acc[qb][d], 0, 0, 0);
+          acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[d], pl, acc[qb][d], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+#pragma unroll
+          for (int d = 0; d < 4; d++)
+            acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j][d], pw[j], acc[qb][d], 0, 0, 0);
+      }
     }
   }
 
