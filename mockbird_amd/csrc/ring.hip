@@ -479,11 +479,26 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
   out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? o / L : 0.f;
 }
 
-// Waves per block for a window of up to `max_valid` slots: about one wave
-// per 180 slots (bf16, 64-slot batches) or 256 slots (fp32, 48-slot
-// batches), at most MAXNW.  Measured on the 64-voice C=2048 step and the
-// 256-voice C=1024 step (windows 200-550), these per-wave lengths were the
-// fastest of the sweep on both shapes.
+// Waves per block for a window of up to `max_valid` slots: one wave per
+// `per_wave` slots (180 bf16 with 64-slot batches, 256 fp32 with 48-slot
+// batches) up to 4 waves, and beyond that one wave per 820 slots, at most
+// MAXNW.  Measured on one MI355X with the fused launch (fractions of 8 TB/s,
+// several runs each):
+//   - 64 sequences, C = 2048, mixed windows: bf16 4 waves 0.69-0.71
+//     (12 waves 0.65-0.67, 2-3 waves 0.68-0.71); fp32 4-5 waves 0.73-0.75
+//     (8 waves 0.71-0.72);
+//   - 32 sequences, C = 4096, full windows: bf16 5 waves 0.68-0.70 (16 waves
+//     0.63-0.64, 4 waves 0.60);
+//   - 256 and 64 voices, C = 1024, windows 214-549: bf16 4 waves best (3 waves
+//     within 0.01; 2 waves 0.66 at 256 voices).
+// At 4-5 waves every block of the 64- and 32-sequence steps (768 and 384
+// blocks) is resident at once: the fused kernel holds 16 waves per CU.
+static int unit_waves(int64_t max_valid, int per_wave, int maxnw) {
+  const int64_t short_rule = std::min<int64_t>(4, (max_valid + per_wave - 1) / per_wave);
+  const int64_t long_rule = (max_valid + 819) / 820;
+  return (int)std::min<int64_t>(maxnw, std::max(short_rule, long_rule));
+}
+
 template <bool APPEND, bool IN_BF16>
 static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const void* q,
                        const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
@@ -500,13 +515,13 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
   const dim3 grid((unsigned)(nq * H));
   if (ring.bf16) {
     constexpr int U = 8, MAXNW = 16;
-    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 179) / 180);
+    const int nw = unit_waves(max_valid, 180, MAXNW);
     hipLaunchKernelGGL((k_attn_unit<true, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                        ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
                        ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
   } else {
     constexpr int U = 12, MAXNW = 8;
-    const int nw = (int)std::min<int64_t>(MAXNW, (max_valid + 255) / 256);
+    const int nw = unit_waves(max_valid, 256, MAXNW);
     hipLaunchKernelGGL((k_attn_unit<false, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                        ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
                        ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
