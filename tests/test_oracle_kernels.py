@@ -12,54 +12,13 @@ reference's (2e-5, 5e-3, 1e-5, 1e-5, exact).
 import numpy as np
 import pytest
 
+from kernel_cases import XorShift, make_cases, rope_f64
 from oracle import oracle
-
-
-class XorShift:
-    """kernels.test.mjs:22-30, with JS's int32/uint32 conversions."""
-
-    def __init__(self, seed=0x2F6E2B1):
-        self.s = seed
-
-    @staticmethod
-    def _i32(x):
-        x &= 0xFFFFFFFF
-        return x - (1 << 32) if x & 0x80000000 else x
-
-    def __call__(self):
-        i32 = self._i32
-        s = i32(i32(self.s) ^ i32(self.s << 13)) & 0xFFFFFFFF
-        s = i32(i32(s) ^ (i32(s) >> 17))
-        s = i32(s ^ i32(s << 5)) & 0xFFFFFFFF
-        self.s = s
-        return (s / 0xFFFFFFFF) * 2 - 1
 
 
 @pytest.fixture(scope="module")
 def cases():
-    r = XorShift()
-    D, H, HD = 768, 12, 64
-    c = {}
-    x = np.zeros(D); b = np.zeros(D)
-    for i in range(D):
-        x[i] = r() * 4
-        b[i] = r() * 0.1
-    c["ln"] = (x.astype(np.float32), np.ones(D, np.float32), b.astype(np.float32))
-    K, N = D, 3 * D
-    xg = np.array([r() for _ in range(K)], np.float32)
-    W = np.array([r() * 0.05 for _ in range(K * N)], np.float32).reshape(K, N)
-    bias = np.array([r() * 0.02 for _ in range(N)], np.float32)
-    c["gemv"] = (xg, W, bias)
-    c["rope"] = np.array([r() for _ in range(HD)], np.float32)
-    n = 512
-    k = np.zeros(n * H * HD, np.float32); v = np.zeros(n * H * HD, np.float32)
-    for i in range(k.size):
-        k[i] = r()
-        v[i] = r()
-    q = np.array([r() for _ in range(H * HD)], np.float32)
-    c["attn"] = (q, k.reshape(n, D), v.reshape(n, D))
-    c["argmax"] = np.array([r() for _ in range(1024)], np.float32)
-    return c
+    return make_cases()
 
 
 def test_xorshift_matches_js_semantics():
@@ -100,15 +59,13 @@ def test_gemv_vs_float64(cases):
 
 def test_rope_pos137_as_complex_rotation(cases):
     v = cases["rope"]
-    z = v[0::2].astype(np.float64) + 1j * v[1::2].astype(np.float64)
-    ang = np.float32(137) * oracle.inv_freq()
-    zr = z * np.exp(1j * ang.astype(np.float64))
-    ref = np.empty(64)
-    ref[0::2], ref[1::2] = zr.real, zr.imag
+    ref = rope_f64(v, 137, oracle.inv_freq())
     got = oracle.rope(v, 137)
     assert np.abs(got - ref).max() < 1e-6  # reference tolerance 1e-5
     # the reference test's inline formula has the opposite sign (kernels.test.mjs:240);
     # it rotates the other way and disagrees with the engine convention the fixture pins
+    z = v[0::2].astype(np.float64) + 1j * v[1::2].astype(np.float64)
+    ang = np.float32(137) * oracle.inv_freq()
     zl = z * np.exp(-1j * ang.astype(np.float64))
     assert np.abs(got[1::2] - zl.imag).max() > 0.1
 
