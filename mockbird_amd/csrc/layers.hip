@@ -137,19 +137,34 @@ int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assis
 
 // ------------------------------------------------------------ greedy choice
 
+// Row b of x = row `tok` of a [*][768] table, one wave: three 16-byte
+// copies per lane.
+__device__ __forceinline__ void copy_row(const float* __restrict__ table, int tok,
+                                         float* __restrict__ x, int b, int lane) {
+  const float4* src = (const float4*)(table + (int64_t)tok * D);
+  float4* dst = (float4*)(x + (int64_t)b * D);
+#pragma unroll
+  for (int i = 0; i < D / 4 / 64; i++) dst[lane + 64 * i] = src[lane + 64 * i];
+}
+
 // Continue/stop: two double-precision dot products of the step-0 hidden
 // state with text-head columns end_id and assistant_id; continue iff
 // assistant >= end (TEXT_HEAD_DECIDE kernels-decode.ts:487-518,
 // decideAssistantStop policy.ts:297-302).  One wave per sequence.  With
-// `alive`, a sequence already stopped (alive[b] == 0) stays stopped.
+// `alive`, a sequence already stopped (alive[b] == 0) stays stopped.  With
+// `x`, the wave also writes step 1's input row, wte[assistant_id]
+// (EMBED_ROW_LOCAL mode 1, kernels-decode.ts:96-124).
 __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h, int B,
                                                      const float* __restrict__ head, int vocab,
                                                      int end_id, int assistant_id,
                                                      const int32_t* __restrict__ alive,
-                                                     int32_t* __restrict__ cont) {
+                                                     int32_t* __restrict__ cont,
+                                                     const float* __restrict__ wte,
+                                                     float* __restrict__ x) {
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
+  if (x) copy_row(wte, assistant_id, x, b, lane);
   double e = 0.0, a = 0.0;
   for (int d = lane; d < D; d += 64) {
     const double x = h[(int64_t)b * D + d];
@@ -165,9 +180,10 @@ __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h
 }
 
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
-                       int assistant_id, const int32_t* alive, int32_t* cont) {
+                       int assistant_id, const int32_t* alive, int32_t* cont, const float* wte,
+                       float* x) {
   hipLaunchKernelGGL(k_text_decide, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream, h, B,
-                     head, vocab, end_id, assistant_id, alive, cont);
+                     head, vocab, end_id, assistant_id, alive, cont, wte, x);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
@@ -183,12 +199,16 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
 // loads and the one seen-mask word that holds their 16 bits, all issued up
 // front; the penalised values are compared in double (policy.ts:273-290 works
 // on JS numbers) with strict > so the lowest id wins a tie, within the lane
-// (ascending ids) and across lanes (the lower id on equal values).
+// (ascending ids) and across lanes (the lower id on equal values).  With
+// `x`, the wave also writes the next step's input row, next_emb[winner]
+// (EMBED_ROW_LOCAL mode 2: the next step embeds this channel's code).
 __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
                                                         int ch, float penalty,
                                                         uint32_t* __restrict__ seen,
                                                         const int32_t* __restrict__ cont,
-                                                        int32_t* __restrict__ tokens) {
+                                                        int32_t* __restrict__ tokens,
+                                                        const float* __restrict__ next_emb,
+                                                        float* __restrict__ x) {
   static_assert(CODES == 64 * 16, "one wave covers the codebook, 16 ids per lane");
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -226,17 +246,20 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
       idx = oi;
     }
   }
+  // the butterfly leaves every lane with the same winner
+  const int tok = idx == 0x7fffffff ? 0 : idx;
   if (lane == 0) {
-    const int tok = idx == 0x7fffffff ? 0 : idx;
     tokens[b * NVQ + ch] = tok;
     if (!cont || cont[b]) sm[tok >> 5] |= 1u << (tok & 31);
   }
+  if (x) copy_row(next_emb, tok, x, b, lane);
 }
 
 int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
-                          uint32_t* seen, const int32_t* cont, int32_t* tokens) {
+                          uint32_t* seen, const int32_t* cont, int32_t* tokens,
+                          const float* next_emb, float* x) {
   hipLaunchKernelGGL(k_argmax_penalty, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream,
-                     logits, B, ch, penalty, seen, cont, tokens);
+                     logits, B, ch, penalty, seen, cont, tokens, next_emb, x);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

@@ -268,10 +268,14 @@ int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, 
                       const AudioTables& audio, float* x);
 int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
                        const AudioTables& audio, const int32_t* tokens, float* x);
+// With x non-null, text_decide also writes wte[assistant_id] to x[b] (step
+// 1's input) and argmax_penalty writes next_emb[winner] (the next step's).
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
-                       int assistant_id, const int32_t* alive, int32_t* cont);
+                       int assistant_id, const int32_t* alive, int32_t* cont,
+                       const float* wte = nullptr, float* x = nullptr);
 int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
-                          uint32_t* seen, const int32_t* cont, int32_t* tokens);
+                          uint32_t* seen, const int32_t* cont, int32_t* tokens,
+                          const float* next_emb = nullptr, float* x = nullptr);
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);
 int launch_frame_emit(mb_ctx* ctx, const int32_t* tokens, const int32_t* cont, int B,
                       int32_t* frame_idx, int32_t* codes, int32_t* cont_out, int32_t* pos,

@@ -264,10 +264,12 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
   const int64_t S = ctx->cfg.max_seqs;
   for (int step = 0; step <= last_step; step++) {
     if ((rc = cancelled(ctx))) return rc;
+    // picking, the previous step's decision kernel already wrote this step's
+    // input row (wte[assistant_id], then the previous channel's code)
     if (step == 0)
       MB_HIP(ctx, hipMemcpyAsync(a.x, hidden, (size_t)B * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
-    else if ((rc = launch_embed_local(ctx, step, B, m.wte, ctx->assistant_id, m.audio_emb,
-                                      ctx->tokens, a.x)))
+    else if (!pick && (rc = launch_embed_local(ctx, step, B, m.wte, ctx->assistant_id,
+                                               m.audio_emb, ctx->tokens, a.x)))
       return rc;
     if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
                         nullptr, false, step + 1, a)))
@@ -279,9 +281,11 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
         (rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
       return rc;
     if (!pick) continue;
+    const bool embed_next = step < last_step;
     if (step == 0) {
       rc = launch_text_decide(ctx, a.norm, B, m.text_head, ctx->cfg.vocab, ctx->end_id,
-                              ctx->assistant_id, ctx->frame_alive, ctx->cont);
+                              ctx->assistant_id, ctx->frame_alive, ctx->cont, m.wte,
+                              embed_next ? a.x : nullptr);
     } else {
       const int ch = step - 1;
       if (folded_head)
@@ -292,7 +296,8 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
                          a.logits, CODES, B);
       if (rc) return rc;
       rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
-                                 ctx->tokens);
+                                 ctx->tokens, embed_next ? m.audio_emb.t[ch] : nullptr,
+                                 embed_next ? a.x : nullptr);
     }
     if (rc) return rc;
   }
