@@ -15,6 +15,8 @@
  *    synchronise before returning, like the reference's submit + mapAsync.
  *  - `_dev` calls take device pointers, enqueue on the context's stream and
  *    return without synchronising (for callers that keep data in HBM).
+ *  - Every call runs on the context's device (mb_config.device) and leaves
+ *    the calling thread's current HIP device as it found it.
  *  - Sequences ("voices") are addressed 0 .. max_seqs-1; a batched call with
  *    B sequences works on sequences 0 .. B-1.
  *  - Fused QKV rows are [2304] = q | k | v, each 768 wide, head-major

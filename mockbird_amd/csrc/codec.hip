@@ -393,6 +393,7 @@ void codec_free(mb_ctx* ctx) {
 using namespace mb;
 
 extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx || !cfg) return MB_ERR_ARG;
   if (cfg->max_voices < 1 || cfg->max_voices > 65535)
     return fail(ctx, MB_ERR_ARG, "codec max_voices %d out of [1, 65535]", cfg->max_voices);
@@ -454,6 +455,7 @@ extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
 }
 
 extern "C" int mb_codec_reset(mb_ctx* ctx, int n, const int32_t* voices) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   if (!ctx->codec) return fail(ctx, MB_ERR_STATE, "codec not initialised (mb_codec_init)");
   CodecState& cs = *ctx->codec;
@@ -487,6 +489,7 @@ extern "C" int mb_codec_reset(mb_ctx* ctx, int n, const int32_t* voices) {
 
 extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32_t* codes,
                                    float* pcm) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   MB_HIP(ctx, hipSetDevice(ctx->device));
   int rc = check_codec(ctx, B, n_frames);
@@ -512,8 +515,9 @@ extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32
     if (!ctx->capture_stream)
       MB_HIP(ctx, hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking));
     hipStream_t saved = ctx->stream;
+    const hipError_t eb = hipStreamBeginCapture(ctx->capture_stream, hipStreamCaptureModeThreadLocal);
+    if (eb != hipSuccess) return hip_fail(ctx, eb, "hipStreamBeginCapture");
     ctx->stream = ctx->capture_stream;
-    MB_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     rc = codec_frame(ctx, B, codes, pcm, T);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
@@ -540,6 +544,7 @@ extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32
 }
 
 extern "C" int mb_codec_decode(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   MB_HIP(ctx, hipSetDevice(ctx->device));
   int rc = check_codec(ctx, B, n_frames);
@@ -564,6 +569,7 @@ extern "C" int mb_codec_decode(mb_ctx* ctx, int B, int n_frames, const int32_t* 
 
 extern "C" int mb_codec_read_ring(mb_ctx* ctx, int layer, int voice, float* k, float* v,
                                   int32_t* slot_pos, int32_t* slots) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   if (!ctx->codec) return fail(ctx, MB_ERR_STATE, "codec not initialised (mb_codec_init)");
   CodecState& cs = *ctx->codec;

@@ -158,6 +158,8 @@ int mb_create(const mb_config* cfg, mb_ctx** out) {
     fprintf(stderr, "mb_create: %s\n", why.c_str());
     return MB_ERR_ARG;
   }
+  // the caller's current device is given back on return
+  mb::DeviceGuard guard(cfg->device);
   mb_ctx* ctx = new mb_ctx();
   ctx->cfg = *cfg;
   ctx->device = cfg->device;
@@ -213,8 +215,8 @@ int mb_create(const mb_config* cfg, mb_ctx** out) {
 }
 
 void mb_destroy(mb_ctx* ctx) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return;
-  (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   mb::codec_free(ctx);
   for (auto& kv : ctx->weights) (void)hipFree(kv.second.ptr);
@@ -243,6 +245,7 @@ int mb_set_stream(mb_ctx* ctx, void* hip_stream) {
 void* mb_get_stream(mb_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
 
 int mb_synchronize(mb_ctx* ctx) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;
@@ -258,6 +261,7 @@ int mb_cancel(mb_ctx* ctx, int on) {
 
 int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int64_t* dims,
                      int ndims) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   if (!name || !data || !dims || ndims < 1 || ndims > 4)
     return fail(ctx, MB_ERR_ARG, "mb_upload_tensor: bad arguments");
@@ -267,6 +271,8 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
   for (int i = 0; i < ndims; i++) {
     if (dims[i] < 1) return fail(ctx, MB_ERR_ARG, "mb_upload_tensor(%s): dim %d is %lld", name, i,
                                  (long long)dims[i]);
+    if (dims[i] > ((int64_t)1 << 40) / numel)
+      return fail(ctx, MB_ERR_ARG, "mb_upload_tensor(%s): more than 2^40 elements", name);
     numel *= dims[i];
   }
   DeviceTensor& t = ctx->weights[name];
@@ -295,6 +301,7 @@ int mb_upload_tensor(mb_ctx* ctx, const char* name, const float* data, const int
 }
 
 int mb_ring_reset(mb_ctx* ctx, int n, const int32_t* seq_ids) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   const int64_t C = ctx->cfg.capacity;
   if (n < 0) {
@@ -317,6 +324,7 @@ int mb_ring_reset(mb_ctx* ctx, int n, const int32_t* seq_ids) {
 }
 
 int mb_ring_poison(mb_ctx* ctx, int layer, int seq, int n_slots, float sentinel) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, 0);
   if (rc) return rc;
   if (seq < 0 || seq >= ctx->cfg.max_seqs || n_slots < 0 || n_slots > ctx->cfg.capacity)
@@ -336,6 +344,7 @@ int mb_ring_poison(mb_ctx* ctx, int layer, int seq, int n_slots, float sentinel)
 
 int mb_read_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, float* k, float* v,
                  int32_t* slot_pos) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, 0);
   if (rc) return rc;
   const int C = ctx->cfg.capacity;
@@ -381,6 +390,7 @@ int mb_read_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, float* k, fl
 int mb_ring_write_rows_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* qkv,
                            int qkv_dtype, const int32_t* pos0, const int32_t* n_rows, void* q_out,
                            int q_dtype) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
@@ -397,6 +407,7 @@ int mb_ring_write_rows_dev(mb_ctx* ctx, int layer, int B, int rows_max, const vo
 
 int mb_ring_append_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
                        int64_t qkv_stride, const int32_t* pos, float* q_out, int64_t q_stride) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (qkv_dtype != MB_DT_F32 && qkv_dtype != MB_DT_BF16)
@@ -412,6 +423,7 @@ int mb_ring_append_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_d
 
 int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64_t q_stride,
                             const int32_t* pos, int32_t max_pos, float* out, int64_t out_stride) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (q_stride < D || out_stride < D) return fail(ctx, MB_ERR_ARG, "row stride too small");
@@ -425,6 +437,7 @@ int mb_decode_attention_dev(mb_ctx* ctx, int layer, int B, const float* q, int64
 int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv_dtype,
                          int64_t qkv_stride, const int32_t* pos, int32_t max_pos, float* q_out,
                          int64_t q_stride, float* out, int64_t out_stride) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (qkv_dtype != MB_DT_F32 && qkv_dtype != MB_DT_BF16)
@@ -446,6 +459,7 @@ int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv
 
 int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const void* q,
                              int q_dtype, const int32_t* pos0, const int32_t* n_rows, float* out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
@@ -460,6 +474,7 @@ int mb_prefill_attention_dev(mb_ctx* ctx, int layer, int B, int rows_max, const 
 
 int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda, const float* W,
                   const float* bias, float* C, int64_t ldc, int epi) {
+  MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
   if (M < 0 || N < 1 || K < 1) return fail(ctx, MB_ERR_ARG, "linear shape M %d N %d K %d", M, N, K);
   if (epi < EPI_STORE || epi > EPI_GELU_ERF) return fail(ctx, MB_ERR_ARG, "unknown epilogue %d", epi);
@@ -475,6 +490,7 @@ int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
 
 int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float* qkv,
                        const int32_t* pos0, const int32_t* n_rows, float* q_out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)
@@ -502,6 +518,7 @@ int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float*
 
 int mb_ring_append(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_t* pos,
                    float* q_out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -524,6 +541,7 @@ int mb_ring_append(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_
 
 int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int32_t* pos,
                         float* out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -549,6 +567,7 @@ int mb_decode_attention(mb_ctx* ctx, int layer, int B, const float* q, const int
 
 int mb_append_attend(mb_ctx* ctx, int layer, int B, const float* qkv, const int32_t* pos,
                      float* q_out, float* out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -576,6 +595,7 @@ int mb_append_attend(mb_ctx* ctx, int layer, int B, const float* qkv, const int3
 
 int mb_prefill_attention(mb_ctx* ctx, int layer, int B, int rows_max, const float* q,
                          const int32_t* pos0, const int32_t* n_rows, float* out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_common(ctx, layer, B);
   if (rc) return rc;
   if (rows_max < 1 || rows_max > ctx->cfg.max_rows)

@@ -163,6 +163,25 @@ int hip_fail(mb_ctx* ctx, hipError_t e, const char* what);
     if (e_ != hipSuccess) return mb::hip_fail((ctx), e_, #call); \
   } while (0)
 
+// Makes the context's device current for one entry point and gives the
+// caller's current device back when it returns, so a context created for
+// device d works from a thread whose current device is another one.
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int device) {
+    int cur = -1;
+    if (device >= 0 && hipGetDevice(&cur) == hipSuccess && cur != device &&
+        hipSetDevice(device) == hipSuccess)
+      prev = cur;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+  DeviceGuard(const DeviceGuard&) = delete;
+  DeviceGuard& operator=(const DeviceGuard&) = delete;
+};
+#define MB_DEVICE_GUARD(ctx) mb::DeviceGuard mb_device_guard_((ctx) ? (ctx)->device : -1)
+
 // Device scratch named `name` of at least `bytes`, kept between calls.
 void* scratch(mb_ctx* ctx, const char* name, size_t bytes);
 

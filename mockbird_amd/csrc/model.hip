@@ -346,6 +346,7 @@ int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, f
 }
 
 int mb_clear_seen(mb_ctx* ctx, int n, const int32_t* seq_ids) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, 0);
   if (rc) return rc;
   if ((rc = local_state(ctx))) return rc;
@@ -458,18 +459,21 @@ extern "C" {
 
 int mb_prefill(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
                float* last_hidden) {
+  MB_DEVICE_GUARD(ctx);
   if (ctx && !last_hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
   return prefill(ctx, B, rows_max, ids, n_rows, ctx ? ctx->cfg.n_layers : 0, last_hidden, nullptr);
 }
 
 int mb_prefill_rows(mb_ctx* ctx, int B, int rows_max, const int32_t* ids, const int32_t* n_rows,
                     int layer_count, float* hidden) {
+  MB_DEVICE_GUARD(ctx);
   if (ctx && !hidden) return fail(ctx, MB_ERR_ARG, "null pointer");
   if (ctx && layer_count <= 0) layer_count = ctx->cfg.n_layers;
   return prefill(ctx, B, rows_max, ids, n_rows, layer_count, nullptr, hidden);
 }
 
 int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, float* hidden) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -499,6 +503,7 @@ int mb_decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos
 }
 
 int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -516,6 +521,7 @@ int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int3
 }
 
 int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float* out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -535,6 +541,7 @@ int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float*
 
 int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos,
                        int32_t max_pos, float* hidden) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
@@ -569,6 +576,7 @@ extern "C" {
 
 int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
                          int32_t max_pos, int32_t* codes, int32_t* cont) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (n_frames < 0) return fail(ctx, MB_ERR_ARG, "n_frames %d is negative", n_frames);
@@ -601,8 +609,9 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
     if (!ctx->capture_stream)
       MB_HIP(ctx, hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking));
     hipStream_t saved = ctx->stream;
+    const hipError_t eb = hipStreamBeginCapture(ctx->capture_stream, hipStreamCaptureModeThreadLocal);
+    if (eb != hipSuccess) return hip_fail(ctx, eb, "hipStreamBeginCapture");
     ctx->stream = ctx->capture_stream;
-    MB_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
     rc = enqueue_frame(ctx, B, hidden, pos, max_pos, rows, fidx, alive, codes, cont);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
@@ -630,6 +639,7 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
 
 int mb_decode_frames(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* pos,
                      int32_t* codes, int32_t* cont) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (n_frames < 0) return fail(ctx, MB_ERR_ARG, "n_frames %d is negative", n_frames);
@@ -666,6 +676,7 @@ int mb_decode_frames(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_t* p
 
 int mb_local_frame_dev(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int32_t* cont,
                        int32_t* rows17_out) {
+  MB_DEVICE_GUARD(ctx);
   int rc = check_b(ctx, B);
   if (rc) return rc;
   if (B == 0) return MB_OK;
