@@ -377,9 +377,9 @@ int check_codec(mb_ctx* ctx, int B, int n_frames) {
 
 }  // namespace
 
+// Called from entry points that already run on the context's device.
 void codec_free(mb_ctx* ctx) {
   if (!ctx->codec) return;
-  (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
   if (ctx->codec->exec) (void)hipGraphExecDestroy(ctx->codec->exec);
   for (void* p : ctx->codec->owned) (void)hipFree(p);
@@ -405,7 +405,6 @@ extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
     if (cfg->context[s] < 1 || cfg->context[s] + positions(s) > (1 << 20))
       return fail(ctx, MB_ERR_ARG, "codec stage %d: context %d out of range", s, cfg->context[s]);
   }
-  MB_HIP(ctx, hipSetDevice(ctx->device));
   codec_free(ctx);
   CodecState* cs = new CodecState();
   ctx->codec = cs;
@@ -491,7 +490,6 @@ extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32
                                    float* pcm) {
   MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
-  MB_HIP(ctx, hipSetDevice(ctx->device));
   int rc = check_codec(ctx, B, n_frames);
   if (rc) return rc;
   if (B == 0 || n_frames == 0) return MB_OK;
@@ -546,7 +544,6 @@ extern "C" int mb_codec_decode_dev(mb_ctx* ctx, int B, int n_frames, const int32
 extern "C" int mb_codec_decode(mb_ctx* ctx, int B, int n_frames, const int32_t* codes, float* pcm) {
   MB_DEVICE_GUARD(ctx);
   if (!ctx) return MB_ERR_ARG;
-  MB_HIP(ctx, hipSetDevice(ctx->device));
   int rc = check_codec(ctx, B, n_frames);
   if (rc) return rc;
   if (B == 0 || n_frames == 0) return MB_OK;
@@ -581,7 +578,6 @@ extern "C" int mb_codec_read_ring(mb_ctx* ctx, int layer, int voice, float* k, f
   while (s + 1 < kStages && layer >= cs.layer0[s + 1]) s++;
   const int C = cs.slots[s];
   if (slots) *slots = C;
-  MB_HIP(ctx, hipSetDevice(ctx->device));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   const RingView ring = codec_ring(ctx, cs, layer, s);
   const bool bf16 = ring.bf16;

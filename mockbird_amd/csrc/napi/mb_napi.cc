@@ -86,7 +86,8 @@ bool get_i64(napi_env env, napi_value v, int64_t* out, const char* what) {
   }
   double d;
   napi_get_value_double(env, v, &d);
-  if (!(d == (double)(int64_t)d) || d < -2147483648.0 || d > 2147483647.0) {
+  // range first: converting a NaN or out-of-range double to an integer is undefined
+  if (!(d >= -2147483648.0 && d <= 2147483647.0) || d != (double)(int64_t)d) {
     throw_range(env, std::string(what) + " must be a 32-bit integer");
     return false;
   }
@@ -164,22 +165,36 @@ bool get_array(napi_env env, napi_value v, napi_typedarray_type want, int64_t ne
   return true;
 }
 
-napi_value new_f32(napi_env env, int64_t n, float** data) {
+// A zeroed typed array of n 4-byte elements, or nullptr with a RangeError
+// thrown when it cannot be allocated.
+napi_value new_typed(napi_env env, int64_t n, napi_typedarray_type type, void** data) {
   napi_value ab, ta;
   void* p = nullptr;
-  napi_create_arraybuffer(env, (size_t)n * 4, &p, &ab);
+  *data = nullptr;
+  if (n < 0 || n > ((int64_t)1 << 32) ||
+      napi_create_arraybuffer(env, (size_t)n * 4, &p, &ab) != napi_ok || (n && !p)) {
+    throw_range(env, "cannot allocate an output array of " + std::to_string(n) + " elements");
+    return nullptr;
+  }
   if (n) std::memset(p, 0, (size_t)n * 4);
-  napi_create_typedarray(env, napi_float32_array, (size_t)n, ab, 0, &ta);
+  if (napi_create_typedarray(env, type, (size_t)n, ab, 0, &ta) != napi_ok) {
+    throw_range(env, "cannot create an output array of " + std::to_string(n) + " elements");
+    return nullptr;
+  }
+  *data = p;
+  return ta;
+}
+
+napi_value new_f32(napi_env env, int64_t n, float** data) {
+  void* p;
+  napi_value ta = new_typed(env, n, napi_float32_array, &p);
   *data = (float*)p;
   return ta;
 }
 
 napi_value new_i32(napi_env env, int64_t n, int32_t** data) {
-  napi_value ab, ta;
-  void* p = nullptr;
-  napi_create_arraybuffer(env, (size_t)n * 4, &p, &ab);
-  if (n) std::memset(p, 0, (size_t)n * 4);
-  napi_create_typedarray(env, napi_int32_array, (size_t)n, ab, 0, &ta);
+  void* p;
+  napi_value ta = new_typed(env, n, napi_int32_array, &p);
   *data = (int32_t*)p;
   return ta;
 }
@@ -379,7 +394,9 @@ napi_value ReadRing(napi_env env, napi_callback_info info) {
   float *k, *v;
   int32_t* sp;
   napi_value K = new_f32(env, (int64_t)n * kD, &k), V = new_f32(env, (int64_t)n * kD, &v);
+  if (!K || !V) return nullptr;
   napi_value S = new_i32(env, n, &sp);
+  if (!S) return nullptr;
   int rc = mb_read_ring(ctx, layer, seq, slot0, n, k, v, sp);
   if (rc) return throw_status(env, ctx, rc);
   napi_value o;
@@ -405,6 +422,7 @@ napi_value RingAppend(napi_env env, napi_callback_info info) {
     return nullptr;
   float* q;
   napi_value Q = new_f32(env, (int64_t)B * kD, &q);
+  if (!Q) return nullptr;
   int rc = mb_ring_append(ctx, layer, B, qkv, pos, q);
   if (rc) return throw_status(env, ctx, rc);
   return Q;
@@ -428,6 +446,7 @@ napi_value RingWriteRows(napi_env env, napi_callback_info info) {
     return nullptr;
   float* q;
   napi_value Q = new_f32(env, (int64_t)B * R * kD, &q);
+  if (!Q) return nullptr;
   int rc = mb_ring_write_rows(ctx, layer, B, R, qkv, p0, nr, q);
   if (rc) return throw_status(env, ctx, rc);
   return Q;
@@ -448,6 +467,7 @@ napi_value DecodeAttention(napi_env env, napi_callback_info info) {
     return nullptr;
   float* out;
   napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  if (!O) return nullptr;
   int rc = mb_decode_attention(ctx, layer, B, q, pos, out);
   if (rc) return throw_status(env, ctx, rc);
   return O;
@@ -471,6 +491,7 @@ napi_value PrefillAttention(napi_env env, napi_callback_info info) {
     return nullptr;
   float* out;
   napi_value O = new_f32(env, (int64_t)B * R * kD, &out);
+  if (!O) return nullptr;
   int rc = mb_prefill_attention(ctx, layer, B, R, q, p0, nr, out);
   if (rc) return throw_status(env, ctx, rc);
   return O;
@@ -501,9 +522,11 @@ napi_value Prefill(napi_env env, napi_callback_info info) {
   napi_value O;
   if (all_rows || layer_count > 0) {
     O = new_f32(env, (int64_t)B * R * kD, &out);
+    if (!O) return nullptr;
     rc = mb_prefill_rows(ctx, B, R, ids, nr, layer_count, out);
   } else {
     O = new_f32(env, (int64_t)B * kD, &out);
+    if (!O) return nullptr;
     rc = mb_prefill(ctx, B, R, ids, nr, out);
   }
   if (rc) return throw_status(env, ctx, rc);
@@ -524,6 +547,7 @@ napi_value DecodeStep(napi_env env, napi_callback_info info) {
     return nullptr;
   float* out;
   napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  if (!O) return nullptr;
   int rc = mb_decode_step(ctx, B, rows, pos, out);
   if (rc) return throw_status(env, ctx, rc);
   return O;
@@ -542,6 +566,7 @@ napi_value LocalFrame(napi_env env, napi_callback_info info) {
     return nullptr;
   int32_t *codes, *cont;
   napi_value Cd = new_i32(env, (int64_t)B * kNvq, &codes), Ct = new_i32(env, B, &cont);
+  if (!Cd || !Ct) return nullptr;
   int rc = mb_local_frame(ctx, B, hidden, codes, cont);
   if (rc) return throw_status(env, ctx, rc);
   napi_value o;
@@ -565,6 +590,7 @@ napi_value LocalSteps(napi_env env, napi_callback_info info) {
     return nullptr;
   float* out;
   napi_value O = new_f32(env, (int64_t)B * kD, &out);
+  if (!O) return nullptr;
   int rc = mb_local_steps(ctx, B, hidden, max_step, out);
   if (rc) return throw_status(env, ctx, rc);
   return O;
@@ -586,7 +612,9 @@ napi_value DecodeFrames(napi_env env, napi_callback_info info) {
     return nullptr;
   int32_t *codes, *cont;
   napi_value Cd = new_i32(env, (int64_t)nf * B * kNvq, &codes);
+  if (!Cd) return nullptr;
   napi_value Ct = new_i32(env, (int64_t)nf * B, &cont);
+  if (!Ct) return nullptr;
   int rc = mb_decode_frames(ctx, B, nf, hidden, pos, codes, cont);
   if (rc) return throw_status(env, ctx, rc);
   napi_value o;
@@ -658,6 +686,7 @@ napi_value CodecDecode(napi_env env, napi_callback_info info) {
     return nullptr;
   float* pcm;
   napi_value P = new_f32(env, (int64_t)B * 2 * nf * 3840, &pcm);
+  if (!P) return nullptr;
   int rc = mb_codec_decode(ctx, B, nf, codes, pcm);
   if (rc) return throw_status(env, ctx, rc);
   return P;
