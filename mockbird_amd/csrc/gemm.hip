@@ -469,6 +469,12 @@ static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) 
   }
   S = 1;
   if (K >= 2048 && !whole_rows) {
+    // From 96 rows up, 32-row tiles split over k read each W column block
+    // half as often as 16-row tiles at the same workgroup count.  Measured on
+    // 768 x 3072 (fc_out, W from HBM) at M = 96 / 128 / 192 / 256: 12.5 /
+    // 13.8 / 15.7 / 19.5 us, where 16-row tiles at their best split took
+    // 16.2 / 16.0 / 22.4 / 23.1 us; at M <= 64 the 16-row tiles stay ahead.
+    if (mt == 16 && M >= 96 && tiles(32) * 2 <= 256) mt = 32;
     for (int s = kStreamMaxSplit; s > 1; s--) {
       if (K % (4 * kStreamChunk * s) == 0 && tiles(mt) * s <= 256) {
         S = s;
@@ -532,7 +538,8 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // M < kStreamMaxM: the streaming kernel.  Its row tile is the smallest of
 // 16 / 32 / 48 / 64 rows that keeps the grid at most one workgroup per CU
 // (256 CUs), so the projection runs as one round; K = 3072 projections with
-// few tiles split K over up to 8 workgroups (fixed-order reduce).  Measured
+// few tiles split K over up to 8 workgroups (fixed-order reduce), on 32-row
+// tiles from 96 rows up (stream_shape).  Measured
 // on the decode projections (M = 1, 64, 256; N x K = 2304 x 768, 768 x 768,
 // 3072 x 768, 768 x 3072, 1024 x 768) these choices were the fastest of a
 // sweep over tile, pipeline depth and split; 16-deep chunks in 4 register
