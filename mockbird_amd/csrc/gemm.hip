@@ -545,7 +545,8 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // sweep over tile, pipeline depth and split; 16-deep chunks in 4 register
 // stages (3 for 48- and 64-row tiles, whose stages are wider).
 // Larger M: the LDS-tiled kernel with the largest tile that still gives the
-// chip (256 CUs) a block per CU, else the smallest tile.
+// chip (256 CUs) a block per CU (128 x 128 only from K = 512 up), else the
+// smallest tile.
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M) {
   if (M <= 0) return MB_OK;
@@ -563,7 +564,11 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
     }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };
-  if (N % 128 == 0 && blocks(128, 128) >= 256)
+  // 128 x 128 tiles need a long k loop to pay off: at K = 256 (the codec's
+  // d = 256 projections) 64 x 64 tiles were faster on every measured shape
+  // (8192 x 768: 41.1 against 53.0 us; 4096 x 1024: 28.9 against 34.4 us),
+  // at K = 768 / 3072 (prefill) the 128 x 128 tiles were.
+  if (N % 128 == 0 && K >= 512 && blocks(128, 128) >= 256)
     gemm_launch<4, 4>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
   else if (N % 64 == 0 && blocks(64, 64) >= 256)
     gemm_launch<2, 2>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M);
