@@ -181,7 +181,8 @@ static void gemm_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const
 }
 
 // ---------------------------------------------------------------------------
-// Streaming GEMM for decode-sized M (M < kStreamMaxM): W is read straight
+// Streaming GEMM for decode-sized M (and mid-sized M with few tiles, see
+// launch_gemm): W is read straight
 // from HBM in the MFMA B-operand layout, one 16-byte load per lane, with no
 // LDS staging.  In 16x16x4 step t of a 16-deep k group, lane (l16 = lane & 15,
 // r = lane >> 4) feeds A[m0 + l16][k + 4r + t] and W[k + 4r + t][n + 4*l16 + j]
@@ -535,7 +536,8 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
   }
 }
 
-// M < kStreamMaxM: the streaming kernel.  Its row tile is the smallest of
+// M < kStreamMaxM, or few enough 64-row tiles: the streaming kernel.  Its
+// row tile is the smallest of
 // 16 / 32 / 48 / 64 rows that keeps the grid at most one workgroup per CU
 // (256 CUs), so the projection runs as one round; K = 3072 projections with
 // few tiles split K over up to 8 workgroups (fixed-order reduce), on 32-row
@@ -553,7 +555,13 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
   if (N % 64 || K % 64 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
-  if (M < kStreamMaxM) {
+  // The streaming kernel also takes larger M while its 64-row tiling needs at
+  // most two rounds of the chip (<= 512 workgroups): measured on the codec's
+  // shapes it beat the LDS-tiled kernel everywhere there (8192 x 256 x 1024:
+  // 43.6 against 61.0 us; 4096 x 256 x 1024: 22.3 against 40.1 us; 1024 x 768
+  // x 768: 16.2 against 31.2 us; 2048 x 768 x 256: 15.8 against 16.9 us).
+  const int64_t stream_tiles = (int64_t)((M + 63) / 64) * (N / 64);
+  if (M < kStreamMaxM || stream_tiles <= 512) {
     int mt, S;
     stream_shape(M, N, K, false, mt, S);
     switch (mt) {
