@@ -50,6 +50,8 @@ constexpr int kDecoderIndex[kStages] = {1, 3, 5, 7};
 
 struct CodecLayerW {
   const float *ln1_w, *ln1_b, *qkv, *o, *ln2_w, *ln2_b, *f1, *f2, *s1, *s2;
+  // norm1 folded into qkv and norm2 into f1 (launch_fold_ln): W', c, d
+  const float *qkv_g, *qkv_c, *qkv_d, *f1_g, *f1_c, *f1_d;
 };
 
 struct CodecStageW {
@@ -263,6 +265,28 @@ int codec_resolve(mb_ctx* ctx) {
   }
   if (!missing.empty()) return fail(ctx, MB_ERR_STATE, "codec %s", missing.c_str());
 
+  // norm1 / norm2 folded into the projections after them, for the frames
+  // whose rows the streaming kernel takes
+  auto fold = [&](const std::string& name, const float* W, int N, const float* gamma,
+                  const float* beta, const float*& wg, const float*& c, const float*& d) {
+    float* pw = internal_tensor(ctx, name + ".w", (int64_t)kD * N);
+    float* pc = internal_tensor(ctx, name + ".c", N);
+    float* pd = internal_tensor(ctx, name + ".d", N);
+    if (!pw || !pc || !pd) return fail(ctx, MB_ERR_NOMEM, "codec folded weights (%s)", name.c_str());
+    wg = pw;
+    c = pc;
+    d = pd;
+    return launch_fold_ln(ctx, W, kD, N, gamma, beta, pw, pc, pd);
+  };
+  for (int s = 0; s < kStages; s++)
+    for (int i = 0; i < cs.cfg.layers[s]; i++) {
+      CodecLayerW& w = cs.stages[s].layers[i];
+      const std::string key = "#codec/s" + std::to_string(s) + "l" + std::to_string(i);
+      int frc = fold(key + ".qkv", w.qkv, 3 * kD, w.ln1_w, w.ln1_b, w.qkv_g, w.qkv_c, w.qkv_d);
+      if (!frc) frc = fold(key + ".f1", w.f1, kFfn, w.ln2_w, w.ln2_b, w.f1_g, w.f1_c, w.f1_d);
+      if (frc) return frc;
+    }
+
   // the per-quantiser tensors side by side: W [16][512][8], b [16][512], codebooks [16][1024][8]
   float* rw = internal_tensor(ctx, "#codec/rvq_w", (int64_t)NVQ * kRvq * kEntry);
   float* rb = internal_tensor(ctx, "#codec/rvq_b", (int64_t)NVQ * kRvq);
@@ -340,15 +364,24 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
     for (int i = 0; i < cs.cfg.layers[s]; i++) {
       const CodecLayerW& w = st.layers[i];
       const RingView ring = codec_ring(ctx, cs, cs.layer0[s] + i, s);
-      if ((rc = launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln1_w, w.ln1_b, cs.h, kD, kD)) ||
-          (rc = launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M)) ||
+      // norm1 / norm2 are folded into the projection where the streaming
+      // kernel takes the rows, else run apart
+      const bool fold_qkv = gemm_streams(M, 3 * kD), fold_f1 = gemm_streams(M, kFfn);
+      if ((rc = fold_qkv ? launch_gemm_ln(ctx, EPI_STORE, cs.x, kD, w.qkv_g, 3 * kD, kD, w.qkv_c,
+                                          w.qkv_d, nullptr, cs.qkv, 3 * kD, M)
+                         : launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln1_w, w.ln1_b, cs.h, kD, kD)) ||
+          (!fold_qkv &&
+           (rc = launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M))) ||
           (rc = launch_ring_write(ctx, ring, B, n, cs.qkv, MB_DT_F32, dense_rows(3 * kD, n), pos,
                                   nrow, cs.q, MB_DT_F32, dense_rows(kD, n))) ||
           (rc = launch_window_attention(ctx, ring, B, n, cs.q, dense_rows(kD, n), pos, nrow,
                                         cs.att, dense_rows(kD, n))) ||
           (rc = launch_gemm(ctx, EPI_SCALE_ADD, cs.att, kD, w.o, kD, kD, w.s1, cs.x, kD, M)) ||
-          (rc = launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln2_w, w.ln2_b, cs.h, kD, kD)) ||
-          (rc = launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M)) ||
+          (rc = fold_f1 ? launch_gemm_ln(ctx, EPI_GELU_ERF, cs.x, kD, w.f1_g, kFfn, kD, w.f1_c,
+                                         w.f1_d, nullptr, cs.ffn, kFfn, M)
+                        : launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln2_w, w.ln2_b, cs.h, kD, kD)) ||
+          (!fold_f1 &&
+           (rc = launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M))) ||
           (rc = launch_gemm(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2, kD, kFfn, w.s2, cs.x, kD, M)))
         return rc;
     }

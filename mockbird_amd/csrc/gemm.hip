@@ -436,11 +436,11 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
   }
   dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
   const int kw = K / (4 * S);
-  if (LNF && epi != EPI_STORE && epi != EPI_GELU)
+  if (LNF && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
     return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
   with_epi(epi, [&](auto e) {
     constexpr int E = decltype(e)::value;
-    if constexpr (!LNF || E == EPI_STORE || E == EPI_GELU)
+    if constexpr (!LNF || E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
       hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, LNF>), grid, dim3(256), 0, ctx->stream, A, lda,
                          W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
   });
@@ -515,15 +515,26 @@ int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma
   return MB_OK;
 }
 
-// out = epi(LN(x) W + bias) for decode-sized M with the LayerNorm folded in
-// (Wg, c, d from launch_fold_ln); K must be the row width 768.  Larger M
-// returns MB_ERR_STATE so the caller runs the LayerNorm and the GEMM apart.
+// The streaming kernel takes M < kStreamMaxM, and larger M while its 64-row
+// tiling needs at most two rounds of the chip (<= 512 workgroups): measured on
+// the codec's shapes it beat the LDS-tiled kernel everywhere there (8192 x 256
+// x 1024: 43.6 against 61.0 us; 4096 x 256 x 1024: 22.3 against 40.1 us;
+// 1024 x 768 x 768: 16.2 against 31.2 us; 2048 x 768 x 256: 15.8 against
+// 16.9 us), and lost beyond (8192 x 768 x 256: 47.9 against 40.5 us).
+bool gemm_streams(int M, int N) {
+  return M < kStreamMaxM || (int64_t)((M + 63) / 64) * (N / 64) <= 512;
+}
+
+// out = epi(LN(x) W + bias) with the LayerNorm folded in (Wg, c, d from
+// launch_fold_ln); K is the row width (the workgroup sees whole rows).  Where
+// the streaming kernel does not take the shape (gemm_streams) it returns
+// MB_ERR_STATE, so the caller runs the LayerNorm and the GEMM apart.
 int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const float* Wg, int N,
                    int K, const float* c, const float* d, const float* bias, float* Cm,
                    int64_t ldc, int M) {
   if (M <= 0) return MB_OK;
-  if (M >= kStreamMaxM) return MB_ERR_STATE;
-  if (K != D || N % 64 || ldx % 4 || ldc % 4 || ((uintptr_t)x & 15) || ((uintptr_t)Wg & 15) ||
+  if (!gemm_streams(M, N)) return MB_ERR_STATE;
+  if (K % 64 || N % 64 || ldx % 4 || ldc % 4 || ((uintptr_t)x & 15) || ((uintptr_t)Wg & 15) ||
       ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) || ((uintptr_t)c & 15) || ((uintptr_t)d & 15))
     return fail(ctx, MB_ERR_ARG, "folded gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
   int mt, S;
@@ -555,13 +566,7 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
   if (N % 64 || K % 64 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
-  // The streaming kernel also takes larger M while its 64-row tiling needs at
-  // most two rounds of the chip (<= 512 workgroups): measured on the codec's
-  // shapes it beat the LDS-tiled kernel everywhere there (8192 x 256 x 1024:
-  // 43.6 against 61.0 us; 4096 x 256 x 1024: 22.3 against 40.1 us; 1024 x 768
-  // x 768: 16.2 against 31.2 us; 2048 x 768 x 256: 15.8 against 16.9 us).
-  const int64_t stream_tiles = (int64_t)((M + 63) / 64) * (N / 64);
-  if (M < kStreamMaxM || stream_tiles <= 512) {
+  if (gemm_streams(M, N)) {
     int mt, S;
     stream_shape(M, N, K, false, mt, S);
     switch (mt) {

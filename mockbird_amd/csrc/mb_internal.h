@@ -272,8 +272,11 @@ enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2, EPI_SCALE_ADD = 3, EPI_GELU_ERF
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M);
 
-// LayerNorm folded into the projection after it (decode-sized M): Wg, c, d
-// from launch_fold_ln; launch_gemm_ln returns MB_ERR_STATE for M >= 1024.
+// LayerNorm folded into the projection after it: Wg, c, d from
+// launch_fold_ln; launch_gemm_ln returns MB_ERR_STATE where the streaming
+// kernel does not take M x N (gemm_streams false), and the caller then runs
+// the LayerNorm and launch_gemm apart.
+bool gemm_streams(int M, int N);
 int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma,
                    const float* beta, float* Wg, float* c, float* d);
 int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const float* Wg, int N,
