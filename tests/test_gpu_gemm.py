@@ -98,6 +98,8 @@ def test_linear_rejects_bad_shapes(ctx):
 CODEC_SHAPES = [  # (M, N, K): the codec's projections at 1-256 voices
     (4, 256, 192), (16, 768, 256), (64, 256, 256), (128, 1024, 256), (256, 256, 1024),
     (512, 768, 384), (1024, 256, 1024), (2048, 1024, 256), (8192, 256, 256),
+    # streaming kernel at 384 tiles (two rounds); LDS-tiled 64 x 64 tiles at K = 256
+    (2048, 768, 256), (4096, 768, 256),
 ]
 
 
