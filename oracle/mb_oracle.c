@@ -1,9 +1,10 @@
 /*
  * CPU ORACLE for the MOSS-TTS-Nano decoder hot path -- TEST INFRASTRUCTURE ONLY.
  *
- * This file is the checker. Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load it; the product path (the HIP library
- * under mockbird_amd/) never links or calls it.
+ * It checks the HIP library's results; it is never the thing measured or
+ * shipped.  Only tests/, __graft_entry__.smoke() and the cpu_baseline leg of
+ * bench.py may load it; the product path (the HIP library under mockbird_amd/)
+ * never links or calls it.
  *
  * It is a plain-C restatement of the reference's algorithm, written from the
  * reference's CPU restatement and WGSL kernels:

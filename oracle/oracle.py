@@ -1,7 +1,7 @@
 """ctypes wrapper over the C oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and the cpu_baseline leg of bench.py may
-import this module; it is the checker, never the thing measured or shipped.
+import this module; it checks results and is never the thing measured or shipped.
 Every function here is a thin call into oracle/mb_oracle.c, whose header lists
 the reference file:line each piece restates.
 
