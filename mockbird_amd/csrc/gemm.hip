@@ -235,7 +235,7 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
 // It accumulates them from the A values it streams anyway -- sums of
 // x - x0 and (x - x0)^2 with x0 = x[row][0], so the variance does not cancel
 // -- which requires the workgroup to see the whole row (S == 1, K == 768).
-template <int MT, int ST, int EPI, bool LNF>
+template <int MT, int ST, int EPI, bool LNF, bool TILED>
 __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int N, int kw,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
@@ -270,11 +270,15 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
         sxx[i] = 0.f;
       }
     }
-    const float* Wp = W + (int64_t)4 * r * N + n;
+    // TILED: W column-block-major, [N / 64][K][64] (launch_tile_w), so a
+    // workgroup streams one contiguous strip instead of 256 bytes of every row
+    const int64_t wstride = TILED ? 64 : N;
+    const float* Wp = TILED ? W + (int64_t)blockIdx.x * 64 * (4 * S * kw) + 4 * r * 64 + 4 * l16
+                            : W + (int64_t)4 * r * N + n;
     float4 a[ST][MI], w[ST][4];
     auto load = [&](int st, int k) {
 #pragma unroll
-      for (int t = 0; t < 4; t++) w[st][t] = *(const float4*)(Wp + (int64_t)(k + t) * N);
+      for (int t = 0; t < 4; t++) w[st][t] = *(const float4*)(Wp + (int64_t)(k + t) * wstride);
 #pragma unroll
       for (int i = 0; i < MI; i++) a[st][i] = *(const float4*)(Ap[i] + k);
     };
@@ -427,7 +431,7 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
 template <int MT, int ST, bool LNF>
 static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
                          int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
-                         const float* lnc, const float* lnd) {
+                         const float* lnc, const float* lnd, bool tiled) {
   const int tx = N / 64, ty = (M + MT - 1) / MT;
   float* part = nullptr;
   if (S > 1) {
@@ -440,9 +444,18 @@ static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, cons
     return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
   with_epi(epi, [&](auto e) {
     constexpr int E = decltype(e)::value;
-    if constexpr (!LNF || E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
-      hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, LNF>), grid, dim3(256), 0, ctx->stream, A, lda,
-                         W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    // folded weights (LNF) always come tiled from launch_fold_ln
+    if constexpr (LNF) {
+      if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
+        hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, true, true>), grid, dim3(256), 0, ctx->stream,
+                           A, lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    } else if (tiled) {
+      hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, false, true>), grid, dim3(256), 0, ctx->stream,
+                         A, lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    } else {
+      hipLaunchKernelGGL((k_gemm_stream<MT, ST, E, false, false>), grid, dim3(256), 0, ctx->stream,
+                         A, lda, W, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    }
   });
   if (S > 1) {
     const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
@@ -487,7 +500,29 @@ static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) 
 
 // W' = diag(gamma) W, c = column sums of W', d = beta W: the folded form of
 // "LayerNorm, then x W" used by the LNF streaming kernel.  One thread per
-// column; c and d are summed in double in k order and rounded once.
+// column; c and d are summed in double in k order and rounded once.  W' is
+// written column-block-major ([N / 64][K][64]), the layout the streaming
+// kernel reads contiguously.
+__global__ __launch_bounds__(256) void k_tile_w(const float* __restrict__ W, int K, int N,
+                                                float* __restrict__ Wt) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one output element
+  if (i >= (int64_t)K * N) return;
+  const int c = (int)(i & 63);
+  const int64_t rest = i >> 6;
+  const int k = (int)(rest % K), cb = (int)(rest / K);
+  Wt[i] = W[(int64_t)k * N + cb * 64 + c];
+}
+
+// Wt = W ([K][N] row-major) in column-block-major order [N / 64][K][64].
+int launch_tile_w(mb_ctx* ctx, const float* W, int K, int N, float* Wt) {
+  if (N % 64) return fail(ctx, MB_ERR_ARG, "tiled projection width %d is not a multiple of 64", N);
+  const int64_t n = (int64_t)K * N;
+  hipLaunchKernelGGL(k_tile_w, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, W, K,
+                     N, Wt);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
 __global__ __launch_bounds__(256) void k_fold_ln(const float* __restrict__ W, int K, int N,
                                                  const float* __restrict__ gamma,
                                                  const float* __restrict__ beta,
@@ -495,11 +530,12 @@ __global__ __launch_bounds__(256) void k_fold_ln(const float* __restrict__ W, in
                                                  float* __restrict__ d) {
   const int n = blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
+  float* wg = Wg + (int64_t)(n >> 6) * K * 64 + (n & 63);  // column-block-major, as launch_tile_w
   double sc = 0.0, sd = 0.0;
   for (int k = 0; k < K; k++) {
     const float w = W[(int64_t)k * N + n];
     const float g = __fmul_rn(gamma[k], w);
-    Wg[(int64_t)k * N + n] = g;
+    wg[(int64_t)k * 64] = g;
     sc += (double)g;
     sd += (double)beta[k] * (double)w;
   }
@@ -509,6 +545,7 @@ __global__ __launch_bounds__(256) void k_fold_ln(const float* __restrict__ W, in
 
 int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma,
                    const float* beta, float* Wg, float* c, float* d) {
+  if (N % 64) return fail(ctx, MB_ERR_ARG, "folded projection width %d is not a multiple of 64", N);
   hipLaunchKernelGGL(k_fold_ln, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, ctx->stream, W, K,
                      N, gamma, beta, Wg, c, d);
   MB_HIP(ctx, hipGetLastError());
@@ -540,10 +577,10 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
   int mt, S;
   stream_shape(M, N, K, true, mt, S);
   switch (mt) {
-    case 16: return stream_launch<16, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
-    case 32: return stream_launch<32, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
-    case 48: return stream_launch<48, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
-    default: return stream_launch<64, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d);
+    case 16: return stream_launch<16, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    case 32: return stream_launch<32, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    case 48: return stream_launch<48, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    default: return stream_launch<64, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
   }
 }
 
@@ -561,8 +598,10 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // chip (256 CUs) a block per CU (128 x 128 only from K = 512 up), else the
 // smallest tile.
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
-                const float* bias, float* Cm, int64_t ldc, int M) {
+                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled) {
   if (M <= 0) return MB_OK;
+  if (w_tiled && !gemm_streams(M, N))
+    return fail(ctx, MB_ERR_STATE, "tiled weights need the streaming kernel (M %d N %d)", M, N);
   if (N % 64 || K % 64 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
@@ -570,10 +609,10 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
     int mt, S;
     stream_shape(M, N, K, false, mt, S);
     switch (mt) {
-      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
+      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
+      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
+      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
     }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };

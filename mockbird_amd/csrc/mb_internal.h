@@ -69,11 +69,14 @@ struct AudioTables {
 
 // Device pointers of one d=768 transformer layer ([K, N] row-major matrices),
 // plus the LayerNorm-folded forms of the two projections that follow a
-// LayerNorm (W' = diag(gamma) W, c = column sums of W', d = beta W).
+// LayerNorm (W' = diag(gamma) W, c = column sums of W', d = beta W; W'
+// column-block-major) and column-block-major copies of the other two, which
+// the streaming kernel reads at decode sizes.
 struct LayerW {
   const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
   const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
   const float *attn_wg, *attn_c, *attn_d, *fc_in_wg, *fc_in_c, *fc_in_d;
+  const float *proj_wt, *fc_out_wt;
 };
 
 // Every weight a model call needs, resolved from the uploaded tensors.
@@ -269,11 +272,16 @@ int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value);
 // argument as a per-column scale s and stores C + s * (A W); EPI_GELU_ERF
 // applies the exact (erf) GELU after the bias.
 enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2, EPI_SCALE_ADD = 3, EPI_GELU_ERF = 4 };
+// W is [K][N] row-major, or with w_tiled the column-block-major copy from
+// launch_tile_w ([N / 64][K][64]; only where gemm_streams(M, N), else
+// MB_ERR_STATE).
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
-                const float* bias, float* Cm, int64_t ldc, int M);
+                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled = false);
+int launch_tile_w(mb_ctx* ctx, const float* W, int K, int N, float* Wt);
 
 // LayerNorm folded into the projection after it: Wg, c, d from
-// launch_fold_ln; launch_gemm_ln returns MB_ERR_STATE where the streaming
+// launch_fold_ln (Wg column-block-major, as launch_tile_w writes it);
+// launch_gemm_ln returns MB_ERR_STATE where the streaming
 // kernel does not take M x N (gemm_streams false), and the caller then runs
 // the LayerNorm and launch_gemm apart.
 bool gemm_streams(int M, int N);

@@ -45,10 +45,20 @@ int fold(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, con
   return launch_fold_ln(ctx, W, K, N, gamma, beta, pw, pc, pd);
 }
 
+// A column-block-major copy of the [K][N] projection W (launch_tile_w).
+int tile(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, const float*& wt) {
+  float* p = internal_tensor(ctx, name, (int64_t)K * N);
+  if (!p) return fail(ctx, MB_ERR_NOMEM, "tiled weight allocation failed (%s)", name.c_str());
+  wt = p;
+  return launch_tile_w(ctx, W, K, N, p);
+}
+
 int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
   int rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
                 w.attn_d);
   if (rc) return rc;
+  if ((rc = tile(ctx, key + ".proj.t", w.proj_w, D, D, w.proj_wt))) return rc;
+  if ((rc = tile(ctx, key + ".fc_out.t", w.fc_out_w, FFN, D, w.fc_out_wt))) return rc;
   return fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
               w.fc_in_d);
 }
@@ -167,7 +177,11 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
                             Rows{}, a.att, q_rows);
   }
   if (rc) return rc;
-  if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, w.proj_w, D, D, w.proj_b, a.x, D, (int)M))) return rc;
+  // decode sizes read the column-block-major copies of O and fc_out
+  const bool tiled = gemm_streams((int)M, D);
+  if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b, a.x,
+                        D, (int)M, tiled)))
+    return rc;
   if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_GELU, a.x, D, w.fc_in_wg, FFN, D, w.fc_in_c, w.fc_in_d,
                              w.fc_in_b, a.ffn, FFN, (int)M)))
@@ -177,7 +191,8 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
     if ((rc = launch_gemm(ctx, EPI_GELU, a.norm, D, w.fc_in_w, FFN, D, w.fc_in_b, a.ffn, FFN, (int)M)))
       return rc;
   }
-  return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_w, D, FFN, w.fc_out_b, a.x, D, (int)M);
+  return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, tiled ? w.fc_out_wt : w.fc_out_w, D, FFN, w.fc_out_b,
+                     a.x, D, (int)M, tiled);
 }
 
 // Local-head state, allocated on first use: every local slot empty, seen
