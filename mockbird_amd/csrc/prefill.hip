@@ -177,8 +177,11 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
   const bool v_role = tid < 128;
   const int sg = tid & 15, vdc = (tid >> 4) & 7;           // V: slots 4sg.., dims 8vdc..
   const int kt = tid - 128, ks = (kt >> 3) & 15, kdc = kt & 7;  // K: slots ks + 16i, dims 8kdc..
+  // The prefetch only issues loads; every use of what it loaded (the stash,
+  // and the slot positions' conversion to relative positions) comes after the
+  // next barrier, so the loads stay in flight under a whole tile's MFMAs.
   uint4 pre[4];
-  int32_t ppre = kRelEmpty;
+  int32_t praw = -1;
   auto fetch = [&](int t0) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -186,11 +189,7 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
       const uint16_t* src = v_role ? vb + (int64_t)slot * HD + vdc * 8 : kb + (int64_t)slot * HD + kdc * 8;
       pre[i] = slot < kv_end ? *(const uint4*)src : make_uint4(0, 0, 0, 0);
     }
-    if (wave == 0) {
-      const int32_t p = t0 + lane < kv_end ? sp[t0 + lane] : -1;
-      const int64_t d = (int64_t)p - base;
-      ppre = p < 0 ? kRelEmpty : (int32_t)(d < -kRelEmpty ? -kRelEmpty : d >= kRelEmpty ? kRelEmpty - 1 : d);
-    }
+    if (wave == 0) praw = t0 + lane < kv_end ? sp[t0 + lane] : -1;
   };
 
   f32x4_t acc[2][4];
@@ -205,6 +204,12 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
   for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.f;
 
   fetch(0);
+  // Wait here for every load issued so far (q and the first tile): the
+  // compiler cannot tell at the loop head that q's loads are complete, and
+  // would otherwise wait for all loads (the next tile's prefetch included)
+  // before each tile's first MFMA.  s_waitcnt vmcnt(0), expcnt and lgkmcnt
+  // left at their maxima (gfx9 encoding).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
   int buf = 0;
   for (int t0 = 0; t0 < kv_end; t0 += KT, buf ^= 1) {
     // the buffer written here was last read two tiles ago, before the
@@ -226,6 +231,9 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
       for (int i = 0; i < 4; i++) *(uint4*)&Ks[buf][(ks + 16 * i) * KPAD + kdc * 8] = pre[i];
     }
     if (wave == 0) {
+      const int64_t d = (int64_t)praw - base;
+      const int32_t ppre =
+          praw < 0 ? kRelEmpty : (int32_t)(d < -kRelEmpty ? -kRelEmpty : d >= kRelEmpty ? kRelEmpty - 1 : d);
       Ps[buf][lane] = ppre;
       const int lo = wave_extreme<false>(ppre);
       const int hi = wave_extreme<true>(ppre);
@@ -547,37 +555,74 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
     l[qb] = 0.f;
   }
 
-  for (int gi = g0; gi < g1; gi++) {
+  // One 16-slot group's loads, as raw registers: K of the lane's slot
+  // s0 + qc, V (4 dims) and the stored positions of slots s0 + 4g + j.  Every
+  // index is clamped into the window so the loads carry no branch, and the
+  // loop issues group gi + 1's loads before computing group gi: the loads of
+  // one group stay in flight under the MFMAs of the one before.
+  struct Raw {
+    uint4 k[KV_BF16 ? 2 : 4];
+    uint4 v[KV_BF16 ? 2 : 4];  // bf16: slots j = 0..3 as 2 x uint2 per uint4
+    int32_t p[4];
+  };
+  auto load_group = [&](int gi, Raw& r) {
     const int s0 = gi * 16;
     const int ks = min(s0 + qc, kv_end - 1);
-    // K: the lane's slot s0 + qc; V: 4 dims of slots s0 + 4g + j
+    if constexpr (KV_BF16) {
+#pragma unroll
+      for (int c = 0; c < 2; c++) r.k[c] = *(const uint4*)(kb + ((int64_t)ks * HD + c * 32 + g * 8) * 2);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) r.k[i] = *(const uint4*)(kb + ((int64_t)ks * HD + g * 16 + 4 * i) * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int sl = s0 + 4 * g + j;
+      const int vs = min(sl, kv_end - 1);
+      if constexpr (KV_BF16) {
+        const uint2 w = *(const uint2*)(vb + ((int64_t)vs * HD + 4 * qc) * 2);
+        if (j & 1) { r.v[j >> 1].z = w.x; r.v[j >> 1].w = w.y; }
+        else { r.v[j >> 1].x = w.x; r.v[j >> 1].y = w.y; }
+      } else {
+        r.v[j] = *(const uint4*)(vb + ((int64_t)vs * HD + 4 * qc) * 4);
+      }
+      r.p[j] = sp[vs];
+    }
+  };
+
+  Raw cur, nxt;
+  if (g0 < g1) load_group(g0, cur);
+  for (int gi = g0; gi < g1; gi++) {
+    load_group(min(gi + 1, g1 - 1), nxt);  // past the last group: a reload, unused
+    const int s0 = gi * 16;
     float kf[16];
     bf16x8_t kh[2];
     float vf[4][4];
     uint2 vw[4];
     if constexpr (KV_BF16) {
 #pragma unroll
-      for (int c = 0; c < 2; c++)
-        kh[c] = __builtin_bit_cast(bf16x8_t, *(const uint4*)(kb + ((int64_t)ks * HD + c * 32 + g * 8) * 2));
+      for (int c = 0; c < 2; c++) kh[c] = __builtin_bit_cast(bf16x8_t, cur.k[c]);
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        vw[j] = (j & 1) ? make_uint2(cur.v[j >> 1].z, cur.v[j >> 1].w)
+                        : make_uint2(cur.v[j >> 1].x, cur.v[j >> 1].y);
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; i += 4) {
-        const float4 t = *(const float4*)(kb + ((int64_t)ks * HD + g * 16 + i) * 4);
-        kf[i] = t.x; kf[i + 1] = t.y; kf[i + 2] = t.z; kf[i + 3] = t.w;
+      for (int i = 0; i < 4; i++) {
+        kf[4 * i] = __uint_as_float(cur.k[i].x); kf[4 * i + 1] = __uint_as_float(cur.k[i].y);
+        kf[4 * i + 2] = __uint_as_float(cur.k[i].z); kf[4 * i + 3] = __uint_as_float(cur.k[i].w);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        vf[j][0] = __uint_as_float(cur.v[j].x); vf[j][1] = __uint_as_float(cur.v[j].y);
+        vf[j][2] = __uint_as_float(cur.v[j].z); vf[j][3] = __uint_as_float(cur.v[j].w);
       }
     }
     int32_t pj[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int sl = s0 + 4 * g + j;
-      const int vs = min(sl, kv_end - 1);
-      if constexpr (KV_BF16) {
-        vw[j] = *(const uint2*)(vb + ((int64_t)vs * HD + 4 * qc) * 2);
-      } else {
-        const float4 t = *(const float4*)(vb + ((int64_t)vs * HD + 4 * qc) * 4);
-        vf[j][0] = t.x; vf[j][1] = t.y; vf[j][2] = t.z; vf[j][3] = t.w;
-      }
-      const int32_t p = sl < kv_end ? sp[sl] : -1;
+      const int32_t p = sl < kv_end ? cur.p[j] : -1;
       const int64_t d = (int64_t)p - p0;
       pj[j] = p < 0 ? kFar : (int32_t)(d < -kFar ? -kFar : d > kFar ? kFar : d);
     }
@@ -654,6 +699,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
             acc[qb][d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[j][d], pw[j], acc[qb][d], 0, 0, 0);
       }
     }
+    cur = nxt;
   }
 
   // fold the waves: lane (qc, g) holds dims 4((g*4) + r) + d of query qb*16 + qc
