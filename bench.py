@@ -437,14 +437,24 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
             "all_continued": ok}
 
 
-def cpu_baseline_c1(seconds=12.0):
-    """The oracle (double-precision C, OpenMP over sequences) on a sample of the
-    c1 workload: one sequence per host thread (at most the 64), fp32 rings,
-    append + attention steps, repeated until `seconds` have passed."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_sample(B, seconds):
+    """Append + attention steps of the oracle over the first B of the c1
+    sequences (fp32 rings, C = 2048) until `seconds` have passed; the oracle
+    parallelises over sequences, so B = 1 runs on one thread."""
     from oracle import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    B, C = max(1, min(64, threads)), 2048
+    C = 2048
     pos = c1_positions(64)[:B]
     g = np.random.default_rng(5)
     ring = oracle.Ring(B, C)
@@ -464,10 +474,24 @@ def cpu_baseline_c1(seconds=12.0):
         nbytes += fused_bytes(p, C, 4)
         p = p + 1
         steps += 1
-    dt = time.perf_counter() - t0
+    return nbytes, steps, time.perf_counter() - t0
+
+
+def cpu_baseline_c1(seconds=12.0):
+    """The oracle (double-precision C, OpenMP over sequences) on a sample of the
+    c1 workload: one sequence per host thread (at most the 64), fp32 rings,
+    append + attention steps, repeated until `seconds` have passed; then the
+    same on one sequence (one thread) for a third of the time."""
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    B = max(1, min(64, threads))
+    nbytes, steps, dt = _cpu_sample(B, seconds)
+    nb1, steps1, dt1 = _cpu_sample(1, seconds / 3)
     return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": B, "kind": "port",
             "sample": f"{steps} append+attention steps of {B} of the 64 sequences (fp32 rings, "
-                      f"C=2048, OpenMP over sequences), {dt:.1f} s"}
+                      f"C=2048, OpenMP over sequences), {dt:.1f} s",
+            "single_thread": {"value": nb1 / dt1 / 1e9, "unit": "GB/s",
+                              "sample": f"{steps1} steps of sequence 0, {dt1:.1f} s"},
+            "cpu_model": _cpu_model(), "nproc": os.cpu_count()}
 
 
 def main():
