@@ -314,6 +314,9 @@ napi_value UploadTensor(napi_env env, napi_callback_info info) {
     napi_get_element(env, a.at(3), i, &e);
     if (!get_i64(env, e, &dims[i], "dims[i]")) return nullptr;
     if (dims[i] <= 0) return throw_range(env, "dims must be positive");
+    // the library's own limit, checked before the product can overflow
+    if (dims[i] > ((int64_t)1 << 40) / numel)
+      return throw_range(env, "dims describe more than 2^40 elements");
     numel *= dims[i];
   }
   float* data;
