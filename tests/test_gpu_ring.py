@@ -67,6 +67,55 @@ def test_append_and_attention_small(name, kv):
         assert (ctx.read_ring(0, 2)[2] == -1).all()
 
 
+@pytest.mark.parametrize("name,kv", KV)
+@pytest.mark.parametrize("C", [1, 2, 3])
+def test_tiny_rings(name, kv, C):
+    """Rings of 1-3 slots, where every append past the first C evicts: the
+    fused launch and the two-launch form against the oracle, ring contents
+    bit-exact.  With one slot the window is the new row alone, so the output
+    is that row's stored V exactly (the softmax of one score is 1)."""
+    say(f"tiny ring C={C} kv={name}")
+    B = 4
+    rng = np.random.default_rng(40 + C)
+    pos = np.array([0, 1, 7, 70_001], np.int32)
+    with mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=C, kv_dtype=kv) as fused, \
+            mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=C, kv_dtype=kv) as twin:
+        ring = _oracle_ring(B, C, kv)
+        for step in range(2 * C + 3):
+            qkv = rng.standard_normal((B, 2304), dtype=np.float32)
+            q_f, out_f = fused.append_attend(0, qkv, pos)
+            q_t = twin.ring_append(0, qkv, pos)
+            out_t = twin.decode_attention(0, q_t, pos)
+            q_or = ring.append(qkv, pos)
+            assert np.array_equal(q_f, q_or) and np.array_equal(q_t, q_or), step
+            assert np.array_equal(out_f, out_t), step
+            assert np.abs(out_f - ring.attend(q_or, pos)).max() < 1e-4, step
+            if C == 1:
+                for b in range(B):
+                    assert np.array_equal(out_f[b], ring.V[b][0]), (step, b)
+            pos = pos + 1
+        _check_ring(fused, ring, 0, range(B))
+        _check_ring(twin, ring, 0, range(B))
+
+
+def test_empty_batches_are_no_ops():
+    """B = 0 through every host-pointer ring and attention entry point: no
+    error, empty outputs, and the rings stay empty."""
+    say("empty batches")
+    with mb.Context(n_layers=1, capacity=8, max_seqs=2, max_rows=8) as ctx:
+        none = np.zeros(0, np.int32)
+        assert ctx.ring_append(0, np.zeros((0, 2304), np.float32), none).shape == (0, 768)
+        q, out = ctx.append_attend(0, np.zeros((0, 2304), np.float32), none)
+        assert q.shape == (0, 768) and out.shape == (0, 768)
+        assert ctx.decode_attention(0, np.zeros((0, 768), np.float32), none).shape == (0, 768)
+        rows = ctx.ring_write_rows(0, np.zeros((0, 4, 2304), np.float32), none, none)
+        assert rows.shape == (0, 4, 768)
+        out = ctx.prefill_attention(0, np.zeros((0, 4, 768), np.float32), none, none)
+        assert out.shape == (0, 4, 768)
+        for b in range(2):
+            assert (ctx.read_ring(0, b)[2] == -1).all()
+
+
 def test_rope_positions_beyond_the_table():
     """Positions below 65536 take cos/sin from the context's table, later ones
     are evaluated in-kernel; both must reproduce the oracle bit for bit."""
