@@ -289,8 +289,12 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 // a non-wrapping ring) ropes k, stores K and V there -- the head-0 block also
 // records the slot's position -- and feeds the new row to its own batch from
 // registers, so the attention sees it without reading it back.  Rows 1 only.
+// The fused fp32 form keeps 3 waves per SIMD (at most 168 VGPRs): with
+// fewer, the local head's launches at 256 voices (3072 one-wave blocks) no
+// longer fit the chip in one round.  The bf16 forms get 4 from their
+// 1024-thread blocks already.
 template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16>
-__global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
+__global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn_unit(
     const void* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, int rows, void* __restrict__ ring_k,
     void* __restrict__ ring_v, int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C,
@@ -319,6 +323,22 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
   const char* kbase = (const char*)ring_k + kv_off * (KV_BF16 ? 2 : 4);
   const char* vbase = (const char*)ring_v + kv_off * (KV_BF16 ? 2 : 4);
   const int32_t* sp = slot_pos + (int64_t)b * C;
+  // Fused fp32 form (one voice's global layers, the local head): slot_pos of
+  // the wave's first 256-slot tile (4 slots per lane) is loaded before the
+  // q | k | v row, so the two round trips overlap; frames 0.8 / 0.45 / 0.45 %
+  // faster at 1 / 64 / 256 voices.  Every other tile, and the bf16 forms,
+  // load slot_pos at the tile's start: in the bf16 forms the early load made
+  // the 64-sequence C = 2048 step 2.3 % slower on one GPU (0.2 % faster on
+  // another).
+  constexpr bool kEarlySlots = APPEND && !KV_BF16;
+  int32_t spn[4];
+  if constexpr (kEarlySlots) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      const int idx = s0 + 4 * lane + c;
+      spn[c] = idx < min(s0 + TILE, s1) ? sp[idx] : -1;
+    }
+  }
 
   float qv[VD];
   // The appended row: its slot and whether this wave's range holds it.  The
@@ -373,7 +393,8 @@ __global__ __launch_bounds__(64 * MAXNW) void k_attn_unit(
 #pragma unroll
     for (int c = 0; c < 4; c++) {
       const int idx = t0 + 4 * lane + c;
-      const int64_t p = idx < t1 ? (int64_t)sp[idx] : -1;
+      const int64_t p = kEarlySlots && t0 == s0 ? (int64_t)spn[c]
+                                                : idx < t1 ? (int64_t)sp[idx] : -1;
       const int64_t dlt = cur - p;
       live[c] = __ballot(p >= 0 && dlt >= 0 && dlt < C);
     }
