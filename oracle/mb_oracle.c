@@ -22,7 +22,7 @@
  *   - greedy rules ............. src/lib/tts/engine/policy.ts:273-302
  *
  * Arithmetic follows ref-decode.mjs: every reduction (dot products, LN
- * moments, softmax) is carried in double and each op's output is stored as
+ * moments, softmax) is carried in double (acc_t) and each op's output is stored as
  * fp32, as the JS reference does with Float32Array buffers.  Two places
  * deliberately follow the ONNX graph (the reference's ORT CPU path) instead of
  * the JS restatement, because the reference's own ORT fixture
@@ -37,13 +37,21 @@
  * [slot][head*64 + dim] (prefill.ts:55-56), K and V in separate arrays, plus
  * slot_pos[slot] = absolute position stored in that slot (-1 = empty).
  *
- * Build: oracle/Makefile (gcc -O2 -fopenmp -ffp-contract=off).  The
- * contraction flag matters: the fp32 RoPE below must not be fused into FMAs.
+ * Build: oracle/Makefile.  liboracle.so (the checker) is built with
+ * -ffp-contract=off: the fp32 RoPE below must not be fused into FMAs.
+ *
+ * The same source also builds liboracle_fp32.so with -DOR_ACC=float and
+ * FMA contraction on: every reduction is then carried in fp32, as ORT's MLAS
+ * kernels do.  That build is only the CPU throughput baseline (the stand-in
+ * for the reference's ORT-wasm path); it is never used as a checker.
  */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 #define OR_D 768
 #define OR_H 12
@@ -55,6 +63,12 @@
 #define OR_PAD 1024
 #define OR_CODES 1024
 #define OR_EPS 1e-5
+
+/* Accumulator type of every dot product, moment and softmax sum. */
+#ifndef OR_ACC
+#define OR_ACC double
+#endif
+typedef OR_ACC acc_t;
 
 /* fp32 inverse frequencies 1 / 10000^(2i/64) exactly as the exported graph
  * carries them (the fp32 values torch produces for
@@ -175,37 +189,37 @@ int or_ring_write(int B, int C, int wrap, int kv_bf16, int rows_max, const float
 }
 
 /* One query row against the live slots of a ring, per head (ref-decode.mjs:
- * 138-161 with the live mask of kernels-decode.ts:608-611).  Double throughout;
- * scale 0.125.  No live slot gives a zero row. */
+ * 138-161 with the live mask of kernels-decode.ts:608-611).  Scale 0.125,
+ * reductions in acc_t.  No live slot gives a zero row. */
 static void attend_one(const float* q, int64_t cur, int C, const float* K, const float* V,
-                       const int32_t* sp, float* out, double* scores) {
+                       const int32_t* sp, float* out, acc_t* scores) {
   for (int h = 0; h < OR_H; h++) {
-    double mx = -INFINITY;
+    acc_t mx = -INFINITY;
     for (int j = 0; j < C; j++) {
       if (!or_slot_live(sp[j], cur, C)) {
         scores[j] = -INFINITY;
         continue;
       }
-      double s = 0.0;
+      acc_t s = 0;
       const float* kr = K + (int64_t)j * OR_D + h * OR_HD;
-      for (int d = 0; d < OR_HD; d++) s += (double)q[h * OR_HD + d] * (double)kr[d];
-      scores[j] = s * 0.125;
+      for (int d = 0; d < OR_HD; d++) s += (acc_t)q[h * OR_HD + d] * (acc_t)kr[d];
+      scores[j] = s * (acc_t)0.125;
       if (scores[j] > mx) mx = scores[j];
     }
-    double sum = 0.0;
+    acc_t sum = 0;
     for (int j = 0; j < C; j++) {
-      scores[j] = scores[j] == -INFINITY ? 0.0 : exp(scores[j] - mx);
+      scores[j] = scores[j] == -INFINITY ? 0 : (acc_t)exp((double)(scores[j] - mx));
       sum += scores[j];
     }
-    double acc[OR_HD];
-    for (int d = 0; d < OR_HD; d++) acc[d] = 0.0;
+    acc_t acc[OR_HD];
+    for (int d = 0; d < OR_HD; d++) acc[d] = 0;
     for (int j = 0; j < C; j++) {
-      if (scores[j] == 0.0) continue;
-      const double p = scores[j] / sum;
+      if (scores[j] == 0) continue;
+      const acc_t p = scores[j] / sum;
       const float* vr = V + (int64_t)j * OR_D + h * OR_HD;
-      for (int d = 0; d < OR_HD; d++) acc[d] += p * (double)vr[d];
+      for (int d = 0; d < OR_HD; d++) acc[d] += p * (acc_t)vr[d];
     }
-    for (int d = 0; d < OR_HD; d++) out[h * OR_HD + d] = sum > 0.0 ? (float)acc[d] : 0.0f;
+    for (int d = 0; d < OR_HD; d++) out[h * OR_HD + d] = sum > 0 ? (float)acc[d] : 0.0f;
   }
 }
 
@@ -215,7 +229,7 @@ void or_decode_attention(int B, int C, const float* q, const int32_t* pos, const
                          const float* ringV, const int32_t* slot_pos, float* out) {
 #pragma omp parallel
   {
-    double* scores = (double*)malloc(sizeof(double) * (size_t)C);
+    acc_t* scores = (acc_t*)malloc(sizeof(acc_t) * (size_t)C);
 #pragma omp for schedule(dynamic, 1)
     for (int b = 0; b < B; b++)
       attend_one(q + (int64_t)b * OR_D, pos[b], C, ringK + (int64_t)b * C * OR_D,
@@ -236,7 +250,7 @@ void or_prefill_attention(int B, int C, int rows_max, const float* q, const int3
   const int64_t total = (int64_t)B * rows_max;
 #pragma omp parallel
   {
-    double* scores = (double*)malloc(sizeof(double) * (size_t)C);
+    acc_t* scores = (acc_t*)malloc(sizeof(acc_t) * (size_t)C);
     int32_t* sp = (int32_t*)malloc(sizeof(int32_t) * (size_t)C);
 #pragma omp for schedule(dynamic, 4)
     for (int64_t t = 0; t < total; t++) {
@@ -260,36 +274,64 @@ void or_prefill_attention(int B, int C, int rows_max, const float* q, const int3
 
 /* LayerNorm eps 1e-5 over n features (ref-decode.mjs:85-99). */
 void or_layernorm(const float* x, const float* w, const float* b, int n, float* out) {
-  double m = 0.0;
+  acc_t m = 0;
   for (int i = 0; i < n; i++) m += x[i];
   m /= n;
-  double v = 0.0;
+  acc_t v = 0;
   for (int i = 0; i < n; i++) {
-    const double d = x[i] - m;
+    const acc_t d = x[i] - m;
     v += d * d;
   }
   v /= n;
-  const double inv = 1.0 / sqrt(v + OR_EPS);
+  const acc_t inv = (acc_t)(1.0 / sqrt((double)v + OR_EPS));
   for (int i = 0; i < n; i++)
-    out[i] = (float)((x[i] - m) * inv * (w ? w[i] : 1.0) + (b ? b[i] : 0.0));
+    out[i] = (float)((x[i] - m) * inv * (w ? (acc_t)w[i] : (acc_t)1) + (b ? (acc_t)b[i] : (acc_t)0));
+}
+
+/* Rows [m0, m1) x columns [n0, n1) of y = x W + bias; acc holds n1 - n0. */
+static void gemm_block(int K, int N, const float* x, const float* W, const float* bias, float* y,
+                       int m0, int m1, int n0, int n1, acc_t* acc) {
+  for (int m = m0; m < m1; m++) {
+    for (int n = n0; n < n1; n++) acc[n - n0] = bias ? bias[n] : 0;
+    const float* xr = x + (int64_t)m * K;
+    for (int k = 0; k < K; k++) {
+      const acc_t xv = xr[k];
+      const float* wr = W + (int64_t)k * N;
+      for (int n = n0; n < n1; n++) acc[n - n0] += xv * (acc_t)wr[n];
+    }
+    for (int n = n0; n < n1; n++) y[(int64_t)m * N + n] = (float)acc[n - n0];
+  }
 }
 
 /* y[m][n] = bias[n] + sum_k x[m][k] * W[k][n], W [K, N] row-major
- * (ref-decode.mjs:100-108; kernels-batch.ts:156-184).  Double accumulation. */
+ * (ref-decode.mjs:100-108; kernels-batch.ts:156-184), summed over k in order.
+ * Threads split the rows, or the columns when there are fewer rows than
+ * threads; every output is the same sum either way. */
 void or_gemm(int M, int K, int N, const float* x, const float* W, const float* bias, float* y) {
+#ifdef _OPENMP
+  const int nt = omp_in_parallel() ? 1 : omp_get_max_threads();
+#else
+  const int nt = 1;
+#endif
+  if (M >= nt || nt == 1) {
+#pragma omp parallel if (nt > 1)
+    {
+      acc_t* acc = (acc_t*)malloc(sizeof(acc_t) * (size_t)N);
+#pragma omp for schedule(static)
+      for (int m = 0; m < M; m++) gemm_block(K, N, x, W, bias, y, m, m + 1, 0, N, acc);
+      free(acc);
+    }
+    return;
+  }
+  const int blk = 256;
+  const int nb = (N + blk - 1) / blk;
 #pragma omp parallel
   {
-    double* acc = (double*)malloc(sizeof(double) * (size_t)N);
-#pragma omp for schedule(static)
-    for (int m = 0; m < M; m++) {
-      for (int n = 0; n < N; n++) acc[n] = bias ? bias[n] : 0.0;
-      const float* xr = x + (int64_t)m * K;
-      for (int k = 0; k < K; k++) {
-        const double xv = xr[k];
-        const float* wr = W + (int64_t)k * N;
-        for (int n = 0; n < N; n++) acc[n] += xv * (double)wr[n];
-      }
-      for (int n = 0; n < N; n++) y[(int64_t)m * N + n] = (float)acc[n];
+    acc_t* acc = (acc_t*)malloc(sizeof(acc_t) * blk);
+#pragma omp for schedule(dynamic, 1)
+    for (int j = 0; j < nb; j++) {
+      const int n0 = j * blk, n1 = n0 + blk < N ? n0 + blk : N;
+      gemm_block(K, N, x, W, bias, y, 0, M, n0, n1, acc);
     }
     free(acc);
   }
@@ -319,7 +361,7 @@ typedef struct {
   const float* text_head;             /* [768][vocab] */
   const float* audio_heads[OR_NVQ];   /* [768][1024] each */
   int audio_end_id, assistant_id;     /* 7, 9 */
-  float penalty;                      /* 1.2 */
+  double penalty;                     /* 1.2, a JS number in the reference */
 } or_model;
 
 /* Embed one 17-wide row: wte[row[0]] + sum_k audio_k[row[1+k]], pads skipped,
@@ -406,19 +448,20 @@ int or_model_decode_step(const or_model* M, int C, int wrap, int kv_bf16, const 
 /* Greedy argmax with the HuggingFace repetition penalty over a 1024-bit seen
  * mask (policy.ts:273-290, ref-decode.mjs:273-286): scores of seen ids are
  * multiplied by the penalty when negative, divided when not; strict '>' so a
- * tie keeps the lowest id.  The penalised score is formed in double, as the
- * JS reference does.  Returns the winning id; *best_out / *second_out get the
+ * tie keeps the lowest id.  The penalty and the penalised score are doubles,
+ * as in the JS reference (GEN.audio_repetition_penalty is the JS number 1.2,
+ * mossTtsRuntime.js:506-521).  Returns the winning id; *best_out / *second_out get the
  * winning and runner-up penalised scores (for margin reports). */
-int or_argmax_penalty(const float* logits, int n, const uint32_t* seen, float penalty,
+int or_argmax_penalty(const float* logits, int n, const uint32_t* seen, double penalty,
                       double* best_out, double* second_out) {
   int any = 0;
   for (int w = 0; w < (n + 31) / 32; w++) any |= seen[w] != 0;
-  const int apply = any && penalty != 1.0f;
+  const int apply = any && penalty != 1.0;
   int best = 0;
   double bv = -INFINITY, sv = -INFINITY;
   for (int i = 0; i < n; i++) {
     double s = logits[i];
-    if (apply && ((seen[i >> 5] >> (i & 31)) & 1u)) s = s < 0 ? s * (double)penalty : s / (double)penalty;
+    if (apply && ((seen[i >> 5] >> (i & 31)) & 1u)) s = s < 0 ? s * penalty : s / penalty;
     if (s > bv) {
       sv = bv;
       bv = s;
@@ -521,6 +564,33 @@ void or_local_steps(const or_model* M, const float* hidden, int max_step, const 
   free(V);
 }
 
+/* The local frame head teacher-forced with given codes: the 17 steps of
+ * or_local_frame (ref-decode.mjs:383-412) with codes[ch] fed to step ch + 2
+ * in place of the greedy choice.  text2[0] / text2[1] receive step 0's
+ * audio_end and assistant dot products (or_text_decide), logits[ch][1024]
+ * the audio head of channel ch on step ch + 1 before any penalty
+ * (ref-decode.mjs:401-402). */
+void or_local_logits(const or_model* M, const float* hidden, const int32_t* codes, double* text2,
+                     float* logits) {
+  float* K = (float*)calloc((size_t)OR_ROW * OR_D, sizeof(float));
+  float* V = (float*)calloc((size_t)OR_ROW * OR_D, sizeof(float));
+  int32_t sp[OR_ROW];
+  for (int i = 0; i < OR_ROW; i++) sp[i] = -1;
+  float h[OR_D], x[OR_D];
+  local_step(M, hidden, 0, K, V, sp, h);
+  or_text_decide(M, h, &text2[0], &text2[1]);
+  for (int ch = 0; ch < OR_NVQ; ch++) {
+    if (ch == 0)
+      memcpy(x, M->wte + (int64_t)M->assistant_id * OR_D, sizeof x);
+    else
+      memcpy(x, M->audio_emb[ch - 1] + (int64_t)codes[ch - 1] * OR_D, sizeof x);
+    local_step(M, x, ch + 1, K, V, sp, h);
+    or_gemm(1, OR_D, OR_CODES, h, M->audio_heads[ch], NULL, logits + (int64_t)ch * OR_CODES);
+  }
+  free(K);
+  free(V);
+}
+
 /* Prompt rows of buildVoiceCloneRows with empty templates (policy.ts:49-80):
  * [audio_start] + one audio row per code frame + [audio_end] + text rows +
  * [audio_start].  Returns the row count (n_frames + n_text + 3). */
@@ -550,7 +620,8 @@ int or_build_rows(int n_frames, const int32_t* codes, int n_text, const int32_t*
 /* ------------------------------------------------------ batched helpers */
 /* The batched forms run independent voices on OpenMP threads; each voice's
  * own arithmetic is exactly the single-voice function above (nested parallel
- * regions inside are inactive, so every GEMM runs single-threaded per voice).
+ * regions inside are inactive, so every GEMM runs single-threaded per voice;
+ * a single voice runs outside the voice loop and its GEMMs use the threads).
  * Ring arrays are per voice: K/V[b][layer][C][768], sp[b][layer][C]. */
 
 int or_model_prefill_batch(const or_model* M, int B, int C, int wrap, int kv_bf16, int rows_max,
@@ -558,7 +629,7 @@ int or_model_prefill_batch(const or_model* M, int B, int C, int wrap, int kv_bf1
                            int32_t* sp, float* last_hidden) {
   int rc = 0;
   const int64_t ring = (int64_t)M->n_layers * C;
-#pragma omp parallel for schedule(dynamic, 1) reduction(| : rc)
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : rc) if (B > 1)
   for (int b = 0; b < B; b++) {
     float* hid = (float*)malloc(sizeof(float) * (size_t)(n_rows[b] > 0 ? n_rows[b] : 1) * OR_D);
     int r = or_model_prefill(M, C, wrap, kv_bf16, n_rows[b], ids + (int64_t)b * rows_max * OR_ROW,
@@ -577,7 +648,7 @@ int or_model_decode_step_batch(const or_model* M, int B, int C, int wrap, int kv
                                int32_t* sp, float* hidden) {
   int rc = 0;
   const int64_t ring = (int64_t)M->n_layers * C;
-#pragma omp parallel for schedule(dynamic, 1) reduction(| : rc)
+#pragma omp parallel for schedule(dynamic, 1) reduction(| : rc) if (B > 1)
   for (int b = 0; b < B; b++)
     rc |= or_model_decode_step(M, C, wrap, kv_bf16, rows17 + (int64_t)b * OR_ROW, pos[b],
                                K + b * ring * OR_D, V + b * ring * OR_D, sp + b * ring,
@@ -587,7 +658,7 @@ int or_model_decode_step_batch(const or_model* M, int B, int C, int wrap, int kv
 
 void or_local_frame_batch(const or_model* M, int B, const float* hidden, uint32_t* seen,
                           int32_t* codes, int32_t* cont, double* margins) {
-#pragma omp parallel for schedule(dynamic, 1)
+#pragma omp parallel for schedule(dynamic, 1) if (B > 1)
   for (int b = 0; b < B; b++)
     cont[b] = or_local_frame(M, hidden + (int64_t)b * OR_D, seen + (int64_t)b * OR_NVQ * 32,
                              codes + (int64_t)b * OR_NVQ, margins ? margins + (int64_t)b * 17 : NULL);

@@ -19,7 +19,11 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = os.path.join(_HERE, "liboracle.so")
+#: the fp32-accumulating build of mb_oracle.c: the CPU throughput baseline
+#: only (bench.py's cpu_baseline leg), never a checker
+_LIB_FP32 = os.path.join(_HERE, "liboracle_fp32.so")
 _lib = None
+_libs = {}
 
 D, H, HD, QKV, FFN, NVQ, ROW, PAD, CODES = 768, 12, 64, 2304, 3072, 16, 17, 1024, 1024
 
@@ -38,41 +42,55 @@ def build() -> str:
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_LIB):
-            build()
-        L = C.CDLL(_LIB)
-        L.or_inv_freq.argtypes = [_f32p]
-        L.or_bf16_round.argtypes = [C.c_float]
-        L.or_bf16_round.restype = C.c_float
-        L.or_bf16_round_array.argtypes = [_f32p, C.c_int64, _f32p]
-        L.or_rope.argtypes = [_f32p, C.c_int, C.c_int64, _f32p]
-        L.or_slot_of.argtypes = [C.c_int64, C.c_int, C.c_int]
-        L.or_slot_live.argtypes = [C.c_int64, C.c_int64, C.c_int]
-        L.or_ring_write.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int64,
-                                    _i32p, _i32p, C.c_void_p, _f32p, _f32p, _i32p]
-        L.or_decode_attention.argtypes = [C.c_int, C.c_int, _f32p, _i32p, _f32p, _f32p, _i32p, _f32p]
-        L.or_prefill_attention.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _i32p, _i32p, _f32p,
-                                           _f32p, _i32p, _f32p]
-        L.or_layernorm.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, _f32p]
-        L.or_gemm.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_void_p, _f32p]
-        L.or_gelu_tanh.argtypes = [C.c_float]
-        L.or_gelu_tanh.restype = C.c_float
-        L.or_argmax_penalty.argtypes = [_f32p, C.c_int, _u32p, C.c_float, C.c_void_p, C.c_void_p]
-        L.or_build_rows.argtypes = [C.c_int, _i32p, C.c_int, _i32p, _i32p]
-        L.or_embed_row.argtypes = [C.c_void_p, _i32p, _f32p]
-        L.or_text_decide.argtypes = [C.c_void_p, _f32p, C.c_void_p, C.c_void_p]
-        L.or_model_prefill.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _f32p,
+        _lib = _load(_LIB)
+    return _lib
+
+
+def lib_fp32():
+    """The fp32 baseline build (same functions, fp32 accumulators)."""
+    return _load(_LIB_FP32, codec=False)
+
+
+def _load(path, codec=True):
+    if path in _libs:
+        return _libs[path]
+    if not os.path.exists(path):
+        build()
+    L = C.CDLL(path)
+    L.or_inv_freq.argtypes = [_f32p]
+    L.or_bf16_round.argtypes = [C.c_float]
+    L.or_bf16_round.restype = C.c_float
+    L.or_bf16_round_array.argtypes = [_f32p, C.c_int64, _f32p]
+    L.or_rope.argtypes = [_f32p, C.c_int, C.c_int64, _f32p]
+    L.or_slot_of.argtypes = [C.c_int64, C.c_int, C.c_int]
+    L.or_slot_live.argtypes = [C.c_int64, C.c_int64, C.c_int]
+    L.or_ring_write.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _f32p, C.c_int64,
+                                _i32p, _i32p, C.c_void_p, _f32p, _f32p, _i32p]
+    L.or_decode_attention.argtypes = [C.c_int, C.c_int, _f32p, _i32p, _f32p, _f32p, _i32p, _f32p]
+    L.or_prefill_attention.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _i32p, _i32p, _f32p,
                                        _f32p, _i32p, _f32p]
-        L.or_model_decode_step.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i32p, C.c_int,
-                                           _f32p, _f32p, _i32p, _f32p]
-        L.or_local_frame.argtypes = [C.c_void_p, _f32p, _u32p, _i32p, C.c_void_p]
-        L.or_local_steps.argtypes = [C.c_void_p, _f32p, C.c_int, _i32p, _f32p]
-        L.or_model_prefill_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+    L.or_layernorm.argtypes = [_f32p, C.c_void_p, C.c_void_p, C.c_int, _f32p]
+    L.or_gemm.argtypes = [C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_void_p, _f32p]
+    L.or_gelu_tanh.argtypes = [C.c_float]
+    L.or_gelu_tanh.restype = C.c_float
+    L.or_argmax_penalty.argtypes = [_f32p, C.c_int, _u32p, C.c_double, C.c_void_p, C.c_void_p]
+    L.or_build_rows.argtypes = [C.c_int, _i32p, C.c_int, _i32p, _i32p]
+    L.or_embed_row.argtypes = [C.c_void_p, _i32p, _f32p]
+    L.or_text_decide.argtypes = [C.c_void_p, _f32p, C.c_void_p, C.c_void_p]
+    L.or_model_prefill.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, _i32p, _f32p,
+                                   _f32p, _i32p, _f32p]
+    L.or_model_decode_step.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, _i32p, C.c_int,
+                                       _f32p, _f32p, _i32p, _f32p]
+    L.or_local_frame.argtypes = [C.c_void_p, _f32p, _u32p, _i32p, C.c_void_p]
+    L.or_local_steps.argtypes = [C.c_void_p, _f32p, C.c_int, _i32p, _f32p]
+    L.or_local_logits.argtypes = [C.c_void_p, _f32p, _i32p, _f64p, _f32p]
+    L.or_model_prefill_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         _i32p, _i32p, _f32p, _f32p, _i32p, _f32p]
+    L.or_model_decode_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
                                              _i32p, _i32p, _f32p, _f32p, _i32p, _f32p]
-        L.or_model_decode_step_batch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_int, C.c_int,
-                                                 _i32p, _i32p, _f32p, _f32p, _i32p, _f32p]
-        L.or_local_frame_batch.argtypes = [C.c_void_p, C.c_int, _f32p, _u32p, _i32p, _i32p,
-                                           C.c_void_p]
+    L.or_local_frame_batch.argtypes = [C.c_void_p, C.c_int, _f32p, _u32p, _i32p, _i32p,
+                                       C.c_void_p]
+    if codec:
         L.or_erf_as.argtypes = [C.c_double]
         L.or_erf_as.restype = C.c_double
         L.or_gelu_erf.argtypes = [C.c_float]
@@ -83,8 +101,8 @@ def lib():
         L.or_codec_decode_batch.argtypes = [C.c_void_p, C.c_int, _f32p, _f32p, _i32p, _i32p,
                                             C.c_int, _i32p, _f32p]
         L.or_codec_decode_batch.restype = C.c_int
-        _lib = L
-    return _lib
+    _libs[path] = L
+    return L
 
 
 def _c(a, dt):
@@ -198,7 +216,7 @@ def argmax_penalty(logits, seen_ids=(), penalty: float = 1.2):
     for i in seen_ids:
         seen[i >> 5] |= np.uint32(1 << (i & 31))
     bv, sv = C.c_double(), C.c_double()
-    tok = lib().or_argmax_penalty(logits, logits.size, seen, C.c_float(penalty), C.byref(bv),
+    tok = lib().or_argmax_penalty(logits, logits.size, seen, C.c_double(penalty), C.byref(bv),
                                   C.byref(sv))
     return tok, bv.value, sv.value
 
@@ -232,7 +250,7 @@ class _Model(C.Structure):
         ("text_head", C.c_void_p),
         ("audio_heads", C.c_void_p * NVQ),
         ("audio_end_id", C.c_int), ("assistant_id", C.c_int),
-        ("penalty", C.c_float),
+        ("penalty", C.c_double),
     ]
 
 
@@ -246,7 +264,9 @@ class Model:
     reference's ONNX tensor names, ref-decode.mjs:40-80)."""
 
     def __init__(self, weights: dict, n_layers: int, vocab: int, penalty: float = 1.2,
-                 audio_end_id: int = 7, assistant_id: int = 9):
+                 audio_end_id: int = 7, assistant_id: int = 9, fp32: bool = False):
+        # fp32 selects the fp32-accumulating baseline build (timing only)
+        self._lib = lib_fp32() if fp32 else lib()
         self._keep = {k: _c(v, np.float32) for k, v in weights.items()}
         w = self._keep
         self._layers = (_Layer * n_layers)()
@@ -277,19 +297,29 @@ class Model:
 
     def embed_row(self, row17) -> np.ndarray:
         x = np.zeros(D, np.float32)
-        lib().or_embed_row(self.ptr, _c(row17, np.int32), x)
+        self._lib.or_embed_row(self.ptr, _c(row17, np.int32), x)
         return x
 
     def local_steps(self, hidden, max_step: int, codes) -> np.ndarray:
         """ln_f output of local-head step `max_step` with the codes fed in."""
         out = np.zeros(D, np.float32)
-        lib().or_local_steps(self.ptr, _c(hidden, np.float32), int(max_step), _c(codes, np.int32),
+        self._lib.or_local_steps(self.ptr, _c(hidden, np.float32), int(max_step), _c(codes, np.int32),
                              out)
         return out
 
+    def local_logits(self, hidden, codes):
+        """The frame head teacher-forced with `codes` [16]: returns
+        (text2 = (audio_end, assistant) dot products of step 0 [2] float64,
+        audio-head logits of every channel [16][1024] before the penalty)."""
+        text2 = np.zeros(2, np.float64)
+        logits = np.zeros((NVQ, CODES), np.float32)
+        self._lib.or_local_logits(self.ptr, _c(hidden, np.float32), _c(codes, np.int32), text2,
+                                  logits)
+        return text2, logits
+
     def text_decide(self, h):
         e, a = C.c_double(), C.c_double()
-        c = lib().or_text_decide(self.ptr, _c(h, np.float32), C.byref(e), C.byref(a))
+        c = self._lib.or_text_decide(self.ptr, _c(h, np.float32), C.byref(e), C.byref(a))
         return bool(c), e.value, a.value
 
 
@@ -309,7 +339,7 @@ class ModelState:
         """ids [B][rows_max][17] -> last-row hidden [B][768]."""
         ids = _c(ids, np.int32)
         out = np.zeros((self.B, D), np.float32)
-        rc = lib().or_model_prefill_batch(self.m.ptr, self.B, self.C, int(self.wrap),
+        rc = self.m._lib.or_model_prefill_batch(self.m.ptr, self.B, self.C, int(self.wrap),
                                           int(self.kv_bf16), ids.shape[1], _c(n_rows, np.int32),
                                           ids, self.K, self.V, self.slot_pos, out)
         if rc != 0:
@@ -322,7 +352,7 @@ class ModelState:
         S = ids.shape[0]
         out = np.zeros((S, D), np.float32)
         K, V, sp = self.K[b], self.V[b], self.slot_pos[b]
-        rc = lib().or_model_prefill(self.m.ptr, self.C, int(self.wrap), int(self.kv_bf16), S, ids, K,
+        rc = self.m._lib.or_model_prefill(self.m.ptr, self.C, int(self.wrap), int(self.kv_bf16), S, ids, K,
                                     V, sp, out)
         if rc != 0:
             raise ValueError("prompt does not fit the ring")
@@ -330,7 +360,7 @@ class ModelState:
 
     def decode_step(self, rows17: np.ndarray, pos) -> np.ndarray:
         out = np.zeros((self.B, D), np.float32)
-        rc = lib().or_model_decode_step_batch(self.m.ptr, self.B, self.C, int(self.wrap),
+        rc = self.m._lib.or_model_decode_step_batch(self.m.ptr, self.B, self.C, int(self.wrap),
                                               int(self.kv_bf16), _c(rows17, np.int32),
                                               _c(pos, np.int32), self.K, self.V, self.slot_pos, out)
         if rc != 0:
@@ -342,7 +372,7 @@ class ModelState:
         codes = np.zeros((self.B, NVQ), np.int32)
         cont = np.zeros(self.B, np.int32)
         margins = np.zeros((self.B, 17), np.float64)
-        lib().or_local_frame_batch(self.m.ptr, self.B, _c(hidden, np.float32), self.seen, codes,
+        self.m._lib.or_local_frame_batch(self.m.ptr, self.B, _c(hidden, np.float32), self.seen, codes,
                                    cont, margins.ctypes.data)
         return codes, cont.astype(bool), margins
 

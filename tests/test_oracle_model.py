@@ -72,9 +72,20 @@ def test_repetition_penalty_cases():
     # nothing seen: plain argmax; penalty 1: plain argmax
     assert ap(np.array([1.0, 1.1], np.float32), [])[0] == 1
     assert ap(np.array([1.0, 1.1], np.float32), [1], penalty=1.0)[0] == 1
-    # exact tie keeps the lowest id, also when created by the penalty
+    # exact tie keeps the lowest id
     assert ap(np.array([0.5, 0.5, 0.2], np.float32), [])[0] == 0
-    assert ap(np.array([1.0, 1.2, 0.0], np.float32), [1])[0] == 0
+    # the penalty is the JS double 1.2 (mossTtsRuntime.js:506-521): the fp32
+    # logit 1.2f divided by it is 1.00000004 > 1.0, not a tie
+    assert ap(np.array([1.0, 1.2, 0.0], np.float32), [1])[0] == 1
+    assert ap(np.array([1.0, 1.2, 0.0], np.float32), [1], penalty=float(np.float32(1.2)))[0] == 0
+    # a winner that s / 1.2 and s / 1.2f decide differently:
+    # 1 / 1.2 = 0.83333333 > fp32(0.8333333) = 0.83333331 > 1 / 1.2f = 0.83333330
+    crafted = np.array([1.0, 0.8333333], np.float32)
+    assert ap(crafted, [0])[0] == 0
+    assert ap(crafted, [0], penalty=float(np.float32(1.2)))[0] == 1
+    # negative seen logits are multiplied: -1.0 * 1.2 = -1.2 > fp32(-1.2) = -1.20000005
+    assert ap(np.array([-1.0, -1.2], np.float32), [0])[0] == 0
+    assert ap(np.array([-1.0, -1.2], np.float32), [0], penalty=float(np.float32(1.2)))[0] == 0
     # zero counts as non-negative (divided), NaN never wins
     assert ap(np.array([0.0, -0.1], np.float32), [0])[0] == 0
     assert ap(np.array([np.nan, -5.0], np.float32), [])[0] == 1
