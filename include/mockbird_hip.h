@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define MB_ABI_VERSION 1
+#define MB_ABI_VERSION 2
 
 enum {
   MB_OK = 0,
@@ -210,8 +210,12 @@ int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
 
 /* Local-head settings (LocalHeadSettings, gpu.ts:59-63): the text-head
  * columns of audio_end and assistant_slot (7, 9) and the repetition penalty
- * (1.2).  Those are also the defaults. */
-int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, float penalty);
+ * (1.2).  Those are also the defaults.  The penalty is a double: the
+ * reference applies the JS number generation_defaults.audio_repetition_penalty
+ * (mossTtsRuntime.js:506-521, policy.ts:273-290), and a penalised score can
+ * fall between s / 1.2 and s / 1.2f.  A change invalidates the captured
+ * frame graph of mb_decode_frames_dev. */
+int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, double penalty);
 
 /* Global prefill of sequences b < B: ids [B][rows_max][17], n_rows[b] rows at
  * positions 0 .. n_rows[b]-1 (n_rows[b] <= capacity).  Each sequence's rings
@@ -251,6 +255,20 @@ int mb_local_frame(mb_ctx* ctx, int B, const float* hidden, int32_t* codes, int3
  * of the previous frame.  The conformance probe
  * DecodeRunner.nextFrameSteps (decode.ts:970-1030). */
 int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float* out);
+
+/* The 17-step local frame head teacher-forced with codes[b][16] (each in
+ * [0, 1024)): step 0 runs on hidden[b][768], step 1 on wte[assistant_id], step
+ * s >= 2 on the embedding of codes[b][s - 2] on channel s - 2, exactly as the
+ * greedy frame would have run had it chosen those codes.  text2[b][2]
+ * receives step 0's text-head dot products (audio_end, assistant) as the
+ * continue decision compares them, and logits[b][16][1024] each channel's
+ * audio-head logits before the repetition penalty, as the greedy choice reads
+ * them.  The repetition history, the last frame's codes and the captured
+ * frame graph are left untouched.  The logits buffer the reference's
+ * ARGMAX_PENALTY reads (decode.ts:879-927, kernels-decode.ts:428-478), made
+ * visible for parity checks. */
+int mb_local_logits(mb_ctx* ctx, int B, const float* hidden, const int32_t* codes, double* text2,
+                    float* logits);
 
 /* Forget the repetition history of `n` sequences (n < 0: all) -- the
  * clearSeen part of engine.reset (decode.ts:276-280, gpu.ts:237-242). */

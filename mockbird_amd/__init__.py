@@ -32,7 +32,7 @@ EXPORTS = (
     "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
-    "mb_local_steps", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
+    "mb_local_steps", "mb_local_logits", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
     "mb_linear_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
     "mb_append_attend_dev", "mb_codec_init", "mb_codec_reset", "mb_codec_decode",
     "mb_codec_decode_dev", "mb_codec_read_ring",
@@ -106,10 +106,11 @@ def load():
                                     C.c_int),
         "mb_prefill_attention_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int, _vp, _vp, _vp],
                                      C.c_int),
-        "mb_set_local_head": ([_vp, _i32, _i32, _f32], C.c_int),
+        "mb_set_local_head": ([_vp, _i32, _i32, C.c_double], C.c_int),
         "mb_prefill": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_prefill_rows": ([_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp], C.c_int),
         "mb_local_steps": ([_vp, C.c_int, _vp, C.c_int, _vp], C.c_int),
+        "mb_local_logits": ([_vp, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
         "mb_decode_step": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_local_frame": ([_vp, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_clear_seen": ([_vp, C.c_int, _vp], C.c_int),
@@ -384,6 +385,18 @@ class Context:
         self.check(self.lib.mb_local_steps(self.h, hidden.shape[0], hidden.ctypes.data, max_step,
                                            out.ctypes.data))
         return out
+
+    def local_logits(self, hidden: np.ndarray, codes: np.ndarray):
+        """The frame head teacher-forced with codes [B][16]: returns (text2
+        [B][2] float64 = (audio_end, assistant) dot products of step 0,
+        logits [B][16][1024] before the repetition penalty)."""
+        hidden, codes = _f32c(hidden), _i32c(codes)
+        B = hidden.shape[0]
+        text2 = np.zeros((B, 2), np.float64)
+        logits = np.zeros((B, NVQ, CODES), np.float32)
+        self.check(self.lib.mb_local_logits(self.h, B, hidden.ctypes.data, codes.ctypes.data,
+                                            text2.ctypes.data, logits.ctypes.data))
+        return text2, logits
 
     def decode_step(self, rows17: np.ndarray, pos) -> np.ndarray:
         rows17, pos = _i32c(rows17), _i32c(pos)

@@ -153,14 +153,16 @@ __device__ __forceinline__ void copy_row(const float* __restrict__ table, int to
 // decideAssistantStop policy.ts:297-302).  One wave per sequence.  With
 // `alive`, a sequence already stopped (alive[b] == 0) stays stopped.  With
 // `x`, the wave also writes step 1's input row, wte[assistant_id]
-// (EMBED_ROW_LOCAL mode 1, kernels-decode.ts:96-124).
+// (EMBED_ROW_LOCAL mode 1, kernels-decode.ts:96-124).  With `te`, the two
+// dot products go to te[b] = (end, assistant).
 __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h, int B,
                                                      const float* __restrict__ head, int vocab,
                                                      int end_id, int assistant_id,
                                                      const int32_t* __restrict__ alive,
                                                      int32_t* __restrict__ cont,
                                                      const float* __restrict__ wte,
-                                                     float* __restrict__ x) {
+                                                     float* __restrict__ x,
+                                                     double* __restrict__ te) {
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
@@ -176,22 +178,29 @@ __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h
     e += __shfl_xor(e, off);
     a += __shfl_xor(a, off);
   }
-  if (lane == 0) cont[b] = a >= e && (!alive || alive[b]) ? 1 : 0;
+  if (lane == 0) {
+    cont[b] = a >= e && (!alive || alive[b]) ? 1 : 0;
+    if (te) {
+      te[2 * b] = e;
+      te[2 * b + 1] = a;
+    }
+  }
 }
 
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
                        int assistant_id, const int32_t* alive, int32_t* cont, const float* wte,
-                       float* x) {
+                       float* x, double* te) {
   hipLaunchKernelGGL(k_text_decide, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream, h, B,
-                     head, vocab, end_id, assistant_id, alive, cont, wte, x);
+                     head, vocab, end_id, assistant_id, alive, cont, wte, x, te);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
 
 // Greedy argmax over 1024 logits with the HuggingFace repetition penalty on
 // this channel's seen set: a seen id's score is multiplied by the penalty
-// when negative and divided when not, formed in double as the JS reference
-// does (argmaxWithRepetitionPenalty, policy.ts:273-290; ARGMAX_PENALTY,
+// when negative and divided when not; penalty and score are doubles, as the
+// JS numbers of the reference are (audio_repetition_penalty is the double
+// 1.2, mossTtsRuntime.js:506-521) (argmaxWithRepetitionPenalty, policy.ts:273-290; ARGMAX_PENALTY,
 // kernels-decode.ts:428-478).  Strict '>' keeps the lowest id on ties and a
 // NaN never wins.  The winner goes to tokens[b][ch]; the seen bit is set only
 // for sequences that continue (the reference stops before drawing codes).
@@ -203,7 +212,7 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
 // `x`, the wave also writes the next step's input row, next_emb[winner]
 // (EMBED_ROW_LOCAL mode 2: the next step embeds this channel's code).
 __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
-                                                        int ch, float penalty,
+                                                        int ch, double penalty,
                                                         uint32_t* __restrict__ seen,
                                                         const int32_t* __restrict__ cont,
                                                         int32_t* __restrict__ tokens,
@@ -225,13 +234,13 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
   const uint32_t bits = (word >> (16 * (lane & 1))) & 0xffffu;
   // the penalty applies once the channel has emitted anything (policy.ts:282)
   const bool any = __ballot(word != 0u) != 0ull;
-  const bool apply = any && penalty != 1.f;
+  const bool apply = any && penalty != 1.0;
   double best = -INFINITY;
   int idx = 0x7fffffff;
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     double s = v[j];
-    if (apply && ((bits >> j) & 1u)) s = s < 0 ? s * (double)penalty : s / (double)penalty;
+    if (apply && ((bits >> j) & 1u)) s = s < 0 ? s * penalty : s / penalty;
     if (s > best) {
       best = s;
       idx = 16 * lane + j;
@@ -255,7 +264,7 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
   if (x) copy_row(next_emb, tok, x, b, lane);
 }
 
-int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
                           uint32_t* seen, const int32_t* cont, int32_t* tokens,
                           const float* next_emb, float* x) {
   hipLaunchKernelGGL(k_argmax_penalty, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream,

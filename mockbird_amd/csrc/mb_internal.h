@@ -122,7 +122,7 @@ struct mb_ctx {
   bool model_ok = false;       // `model` resolved since the last upload
   int32_t end_id = 7;          // audio_end_token_id
   int32_t assistant_id = 9;    // audio_assistant_slot_token_id
-  float penalty = 1.2f;        // audio_repetition_penalty
+  double penalty = 1.2;        // audio_repetition_penalty (a JS number in the reference)
 
   // Local head state: a 17-slot fp32 cache per sequence, the per-channel
   // repetition history, the last frame's codes and continue flags.
@@ -299,11 +299,13 @@ int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, 
 int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
                        const AudioTables& audio, const int32_t* tokens, float* x);
 // With x non-null, text_decide also writes wte[assistant_id] to x[b] (step
-// 1's input) and argmax_penalty writes next_emb[winner] (the next step's).
+// 1's input) and argmax_penalty writes next_emb[winner] (the next step's);
+// with te non-null text_decide writes its two dot products (end, assistant)
+// to te[b][2].
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
                        int assistant_id, const int32_t* alive, int32_t* cont,
-                       const float* wte = nullptr, float* x = nullptr);
-int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, float penalty,
+                       const float* wte = nullptr, float* x = nullptr, double* te = nullptr);
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
                           uint32_t* seen, const int32_t* cont, int32_t* tokens,
                           const float* next_emb = nullptr, float* x = nullptr);
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);

@@ -4,6 +4,7 @@
 // LN -> fc_in GEMM (+GELU) -> fc_out GEMM (+x) per layer; ref-decode.mjs:
 // 175-272 and decode.ts:474-620 give the order, including that each layer's
 // MLP follows its own attention).
+#include <cmath>
 #include <cstring>
 
 #include "mb_internal.h"
@@ -265,18 +266,33 @@ int decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, i
   return launch_layernorm(ctx, a.x, D, nullptr, B, m.lnf_w, m.lnf_b, hidden, D);
 }
 
+// What a teacher-forced run of the local head (mb_local_logits) reads and
+// writes: the codes fed to steps 2..16 ([B][16]), and where the text
+// decision's two dot products ([B][2]) and every channel's audio-head logits
+// ([B][16][1024]) go.
+struct LogitsProbe {
+  const int32_t* forced = nullptr;
+  double* text2 = nullptr;
+  float* logits = nullptr;
+  int32_t* cont = nullptr;  // the decision's flag (not the context's)
+};
+
 // Local-head steps 0 .. last_step on device buffers.  With `pick` each step
 // ends in its greedy choice (the text decision at step 0, a code per channel
 // after it); without it the steps only run the layer and ln_f, embedding the
 // codes already held in ctx->tokens, and the last step's ln_f output is left in
-// a.norm (DecodeRunner.nextFrameSteps, decode.ts:970-1030).
-int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pick, Act& a) {
+// a.norm (DecodeRunner.nextFrameSteps, decode.ts:970-1030).  With `probe`
+// (no pick) the steps embed probe->forced instead and end in the same heads
+// the picking frame evaluates, written to the probe's outputs.
+int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pick, Act& a,
+                const LogitsProbe* probe = nullptr) {
   int rc;
   if ((rc = local_state(ctx))) return rc;
   if ((rc = activations(ctx, B, a))) return rc;
   const ModelW& m = ctx->model;
   const RingView ring = local_ring(ctx);
   const int64_t S = ctx->cfg.max_seqs;
+  const bool heads = pick || probe;
   for (int step = 0; step <= last_step; step++) {
     if ((rc = cancelled(ctx))) return rc;
     // picking, the previous step's decision kernel already wrote this step's
@@ -284,35 +300,40 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
     if (step == 0)
       MB_HIP(ctx, hipMemcpyAsync(a.x, hidden, (size_t)B * D * 4, hipMemcpyDeviceToDevice, ctx->stream));
     else if (!pick && (rc = launch_embed_local(ctx, step, B, m.wte, ctx->assistant_id,
-                                               m.audio_emb, ctx->tokens, a.x)))
+                                               m.audio_emb, probe ? probe->forced : ctx->tokens,
+                                               a.x)))
       return rc;
     if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
                         nullptr, false, step + 1, a)))
       return rc;
     // the audio heads take ln_f folded in (decode-sized B); the text decision
     // and the step probe read ln_f itself
-    const bool folded_head = pick && step > 0 && B < kFoldMaxM;
+    const bool folded_head = heads && step > 0 && B < kFoldMaxM;
     if (!folded_head &&
         (rc = launch_layernorm(ctx, a.x, D, nullptr, B, m.local_lnf_w, m.local_lnf_b, a.norm, D)))
       return rc;
-    if (!pick) continue;
-    const bool embed_next = step < last_step;
+    if (!heads) continue;
+    const bool embed_next = pick && step < last_step;
     if (step == 0) {
       rc = launch_text_decide(ctx, a.norm, B, m.text_head, ctx->cfg.vocab, ctx->end_id,
-                              ctx->assistant_id, ctx->frame_alive, ctx->cont, m.wte,
-                              embed_next ? a.x : nullptr);
+                              ctx->assistant_id, pick ? ctx->frame_alive : nullptr,
+                              pick ? ctx->cont : probe->cont, m.wte, embed_next ? a.x : nullptr,
+                              probe ? probe->text2 : nullptr);
     } else {
       const int ch = step - 1;
+      float* lg = pick ? a.logits : probe->logits + (int64_t)ch * CODES;
+      const int64_t ldl = pick ? CODES : (int64_t)NVQ * CODES;
       if (folded_head)
         rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, m.head_wg.t[ch], CODES, D, m.head_c.t[ch],
-                            m.head_d.t[ch], nullptr, a.logits, CODES, B);
+                            m.head_d.t[ch], nullptr, lg, ldl, B);
       else
-        rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr,
-                         a.logits, CODES, B);
+        rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr, lg, ldl,
+                         B);
       if (rc) return rc;
-      rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
-                                 ctx->tokens, embed_next ? m.audio_emb.t[ch] : nullptr,
-                                 embed_next ? a.x : nullptr);
+      if (pick)
+        rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
+                                   ctx->tokens, embed_next ? m.audio_emb.t[ch] : nullptr,
+                                   embed_next ? a.x : nullptr);
     }
     if (rc) return rc;
   }
@@ -349,11 +370,14 @@ using namespace mb;
 
 extern "C" {
 
-int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, float penalty) {
+int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, double penalty) {
   if (!ctx) return MB_ERR_ARG;
   if (audio_end_id < 0 || assistant_id < 0 || audio_end_id >= ctx->cfg.vocab ||
-      assistant_id >= ctx->cfg.vocab || !(penalty > 0.f))
+      assistant_id >= ctx->cfg.vocab || !(penalty > 0.0) || !(penalty < INFINITY))
     return fail(ctx, MB_ERR_ARG, "local head settings out of range");
+  // the captured frame graph holds these values as kernel arguments
+  if (audio_end_id != ctx->end_id || assistant_id != ctx->assistant_id || penalty != ctx->penalty)
+    ctx->graph_gen++;
   ctx->end_id = audio_end_id;
   ctx->assistant_id = assistant_id;
   ctx->penalty = penalty;
@@ -550,6 +574,39 @@ int mb_local_steps(mb_ctx* ctx, int B, const float* hidden, int max_step, float*
   Act a;
   if ((rc = local_steps(ctx, B, d_hidden, max_step, false, a))) return rc;
   MB_HIP(ctx, hipMemcpyAsync(out, a.norm, (size_t)B * D * 4, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return MB_OK;
+}
+
+int mb_local_logits(mb_ctx* ctx, int B, const float* hidden, const int32_t* codes, double* text2,
+                    float* logits) {
+  MB_DEVICE_GUARD(ctx);
+  int rc = check_b(ctx, B);
+  if (rc) return rc;
+  if (B == 0) return MB_OK;
+  if (!hidden || !codes || !text2 || !logits) return fail(ctx, MB_ERR_ARG, "null pointer");
+  for (int64_t i = 0; i < (int64_t)B * NVQ; i++)
+    if (codes[i] < 0 || codes[i] >= CODES)
+      return fail(ctx, MB_ERR_ARG, "code %d outside [0, %d)", codes[i], CODES);
+  if ((rc = need_model(ctx))) return rc;
+  float* d_hidden = (float*)scratch(ctx, "hidden", (size_t)B * D * 4);
+  int32_t* d_codes = (int32_t*)scratch(ctx, "probe_codes", (size_t)B * (NVQ + 1) * 4);
+  double* d_text = (double*)scratch(ctx, "probe_text", (size_t)B * 2 * 8);
+  float* d_logits = (float*)scratch(ctx, "probe_logits", (size_t)B * NVQ * CODES * 4);
+  if (!d_hidden || !d_codes || !d_text || !d_logits)
+    return fail(ctx, MB_ERR_NOMEM, "staging allocation failed");
+  MB_HIP(ctx, hipMemcpyAsync(d_hidden, hidden, (size_t)B * D * 4, hipMemcpyHostToDevice, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(d_codes, codes, (size_t)B * NVQ * 4, hipMemcpyHostToDevice, ctx->stream));
+  LogitsProbe probe;
+  probe.forced = d_codes;
+  probe.cont = d_codes + (int64_t)B * NVQ;
+  probe.text2 = d_text;
+  probe.logits = d_logits;
+  Act a;
+  if ((rc = local_steps(ctx, B, d_hidden, ROW - 1, false, a, &probe))) return rc;
+  MB_HIP(ctx, hipMemcpyAsync(text2, d_text, (size_t)B * 2 * 8, hipMemcpyDeviceToHost, ctx->stream));
+  MB_HIP(ctx, hipMemcpyAsync(logits, d_logits, (size_t)B * NVQ * CODES * 4, hipMemcpyDeviceToHost,
+                             ctx->stream));
   MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return MB_OK;
 }

@@ -10,13 +10,19 @@
 // non-zero status into a thrown Error carrying mb_last_error() and the status
 // name as `code` (MB_ERR_RANGE, ...).
 //
-// Every function is synchronous, as every reference engine call is awaited
-// before the next one starts (runtime.ts:523-561 never overlaps two calls).
+// The model calls (prefill, decodeStep, localFrame, decodeFrames,
+// codecDecode) also come as *Async forms that run the C call on a libuv
+// worker thread and return a Promise, so the reference's awaited engine calls
+// (gpu.ts:173-272) leave the Node event loop free.  A context runs one call
+// at a time, as the reference's runtime never overlaps two engine calls
+// (runtime.ts:523-561): while an asynchronous call is in flight every other
+// call on that context throws MB_ERR_BUSY.
 #include <node_api.h>
 
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -49,7 +55,7 @@ napi_value throw_range(napi_env env, const std::string& msg) {
 }
 
 // An Error with .code = status name and .status = the numeric code.
-napi_value throw_status(napi_env env, mb_ctx* ctx, int rc) {
+napi_value status_error(napi_env env, mb_ctx* ctx, int rc) {
   const char* msg = ctx ? mb_last_error(ctx) : "mb_create failed";
   napi_value code, text, err, st;
   napi_create_string_utf8(env, status_name(rc), NAPI_AUTO_LENGTH, &code);
@@ -57,7 +63,11 @@ napi_value throw_status(napi_env env, mb_ctx* ctx, int rc) {
   napi_create_error(env, code, text, &err);
   napi_create_int32(env, rc, &st);
   napi_set_named_property(env, err, "status", st);
-  napi_throw(env, err);
+  return err;
+}
+
+napi_value throw_status(napi_env env, mb_ctx* ctx, int rc) {
+  napi_throw(env, status_error(env, ctx, rc));
   return nullptr;
 }
 
@@ -102,20 +112,32 @@ bool get_int(napi_env env, napi_value v, int* out, const char* what) {
   return true;
 }
 
-bool get_f32(napi_env env, napi_value v, float* out, const char* what) {
+bool get_f64(napi_env env, napi_value v, double* out, const char* what) {
   napi_valuetype t;
   napi_typeof(env, v, &t);
   if (t != napi_number) {
     throw_type(env, std::string(what) + " must be a number");
     return false;
   }
+  napi_get_value_double(env, v, out);
+  return true;
+}
+
+bool get_f32(napi_env env, napi_value v, float* out, const char* what) {
   double d;
-  napi_get_value_double(env, v, &d);
+  if (!get_f64(env, v, &d, what)) return false;
   *out = (float)d;
   return true;
 }
 
-mb_ctx* get_ctx(napi_env env, napi_value v) {
+// What a JS context handle (an external) points at: the context and whether
+// an asynchronous call on it is in flight.  Only the JS thread touches it.
+struct Handle {
+  mb_ctx* ctx = nullptr;
+  bool busy = false;
+};
+
+Handle* get_handle(napi_env env, napi_value v) {
   void* p = nullptr;
   napi_valuetype t;
   napi_typeof(env, v, &t);
@@ -123,12 +145,22 @@ mb_ctx* get_ctx(napi_env env, napi_value v) {
     throw_type(env, "the first argument must be a live context handle");
     return nullptr;
   }
-  mb_ctx** slot = (mb_ctx**)p;
-  if (!*slot) {
+  Handle* h = (Handle*)p;
+  if (!h->ctx) {
     throw_type(env, "the context was destroyed");
     return nullptr;
   }
-  return *slot;
+  if (h->busy) {
+    napi_throw_error(env, "MB_ERR_BUSY",
+                     "the context is running an asynchronous call: await it before the next call");
+    return nullptr;
+  }
+  return h;
+}
+
+mb_ctx* get_ctx(napi_env env, napi_value v) {
+  Handle* h = get_handle(env, v);
+  return h ? h->ctx : nullptr;
 }
 
 // A typed array of the expected element type with at least `need` elements
@@ -233,9 +265,93 @@ bool read_config_field(napi_env env, napi_value obj, const char* key, int32_t* o
 }
 
 void finalize_ctx(napi_env, void* data, void*) {
-  mb_ctx** slot = (mb_ctx**)data;
-  if (*slot) mb_destroy(*slot);
-  delete slot;
+  Handle* h = (Handle*)data;
+  if (h->ctx) mb_destroy(h->ctx);
+  delete h;
+}
+
+// ------------------------------------------------------ asynchronous calls
+
+// One C call run on a libuv worker.  The job holds references to the handle,
+// the result and every typed array the call reads or writes, so none of them
+// can be collected (or their backing stores freed) before it completes.
+struct Job {
+  napi_async_work work = nullptr;
+  napi_deferred deferred = nullptr;
+  Handle* h = nullptr;
+  std::vector<napi_ref> refs;
+  napi_ref result = nullptr;
+  std::function<int(mb_ctx*)> call;
+  int rc = 0;
+};
+
+void job_execute(napi_env, void* data) {
+  Job* j = (Job*)data;
+  j->rc = j->call(j->h->ctx);
+}
+
+void job_complete(napi_env env, napi_status status, void* data) {
+  Job* j = (Job*)data;
+  j->h->busy = false;
+  if (status != napi_ok) {
+    napi_value code, text, err;
+    napi_create_string_utf8(env, "MB_ERR_UNKNOWN", NAPI_AUTO_LENGTH, &code);
+    napi_create_string_utf8(env, "the asynchronous call did not run", NAPI_AUTO_LENGTH, &text);
+    napi_create_error(env, code, text, &err);
+    napi_reject_deferred(env, j->deferred, err);
+  } else if (j->rc) {
+    napi_reject_deferred(env, j->deferred, status_error(env, j->h->ctx, j->rc));
+  } else {
+    napi_value v;
+    napi_get_reference_value(env, j->result, &v);
+    napi_resolve_deferred(env, j->deferred, v);
+  }
+  for (napi_ref r : j->refs) napi_delete_reference(env, r);
+  napi_delete_reference(env, j->result);
+  napi_delete_async_work(env, j->work);
+  delete j;
+}
+
+// Run `call` now and return `result` (sync), or queue it on a worker and
+// return a Promise of `result` (async).  `keep` lists the typed arrays the
+// call touches.
+napi_value finish(napi_env env, napi_value handle_value, bool async, napi_value result,
+                  std::initializer_list<napi_value> keep, std::function<int(mb_ctx*)> call) {
+  Handle* h = get_handle(env, handle_value);
+  if (!h) return nullptr;
+  if (!async) {
+    const int rc = call(h->ctx);
+    if (rc) return throw_status(env, h->ctx, rc);
+    return result;
+  }
+  Job* j = new Job;
+  j->h = h;
+  j->call = std::move(call);
+  napi_value promise, name;
+  napi_create_promise(env, &j->deferred, &promise);
+  napi_create_reference(env, result, 1, &j->result);
+  napi_ref r;
+  napi_create_reference(env, handle_value, 1, &r);
+  j->refs.push_back(r);
+  for (napi_value v : keep) {
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    if (t != napi_object) continue;  // a null optional array
+    napi_create_reference(env, v, 1, &r);
+    j->refs.push_back(r);
+  }
+  napi_create_string_utf8(env, "mockbird_hip", NAPI_AUTO_LENGTH, &name);
+  if (napi_create_async_work(env, nullptr, name, job_execute, job_complete, j, &j->work) != napi_ok ||
+      napi_queue_async_work(env, j->work) != napi_ok) {
+    for (napi_ref x : j->refs) napi_delete_reference(env, x);
+    napi_delete_reference(env, j->result);
+    if (j->work) napi_delete_async_work(env, j->work);
+    delete j;
+    napi_throw_error(env, "MB_ERR_UNKNOWN", "cannot queue the asynchronous call");
+    return nullptr;
+  }
+  h->busy = true;
+  return promise;
 }
 
 // ---------------------------------------------------------------- bindings
@@ -265,9 +381,10 @@ napi_value Create(napi_env env, napi_callback_info info) {
     napi_throw_error(env, status_name(rc), "mb_create failed (bad configuration or no device)");
     return nullptr;
   }
-  mb_ctx** slot = new mb_ctx*(ctx);
+  Handle* handle = new Handle;
+  handle->ctx = ctx;
   napi_value h;
-  napi_create_external(env, slot, finalize_ctx, nullptr, &h);
+  napi_create_external(env, handle, finalize_ctx, nullptr, &h);
   return h;
 }
 
@@ -278,9 +395,13 @@ napi_value Destroy(napi_env env, napi_callback_info info) {
   napi_typeof(env, a.at(0), &t);
   if (t != napi_external || napi_get_value_external(env, a.at(0), &p) != napi_ok || !p)
     return throw_type(env, "destroy() takes a context handle");
-  mb_ctx** slot = (mb_ctx**)p;
-  if (*slot) mb_destroy(*slot);
-  *slot = nullptr;
+  Handle* h = (Handle*)p;
+  if (h->busy) {
+    napi_throw_error(env, "MB_ERR_BUSY", "destroy() while an asynchronous call is in flight");
+    return nullptr;
+  }
+  if (h->ctx) mb_destroy(h->ctx);
+  h->ctx = nullptr;
   return undef(env);
 }
 
@@ -346,10 +467,10 @@ napi_value SetLocalHead(napi_env env, napi_callback_info info) {
   mb_ctx* ctx = get_ctx(env, a.at(0));
   if (!ctx) return nullptr;
   int end_id, assistant;
-  float penalty;
+  double penalty;
   if (!get_int(env, a.at(1), &end_id, "audioEndTokenId") ||
       !get_int(env, a.at(2), &assistant, "audioAssistantSlotTokenId") ||
-      !get_f32(env, a.at(3), &penalty, "repetitionPenalty"))
+      !get_f64(env, a.at(3), &penalty, "repetitionPenalty"))
     return nullptr;
   int rc = mb_set_local_head(ctx, end_id, assistant, penalty);
   if (rc) return throw_status(env, ctx, rc);
@@ -502,10 +623,11 @@ napi_value PrefillAttention(napi_env env, napi_callback_info info) {
 
 // prefill(h, B, rowsMax, ids Int32Array[B*rowsMax*17], nRows Int32Array[B], layerCount?, allRows?)
 //   -> Float32Array: [B*768] last-row hidden, or [B*rowsMax*768] with allRows
+//   (prefillAsync: a Promise of the same)
+template <bool ASYNC>
 napi_value Prefill(napi_env env, napi_callback_info info) {
   Args a(env, info);
-  mb_ctx* ctx = get_ctx(env, a.at(0));
-  if (!ctx) return nullptr;
+  if (!get_ctx(env, a.at(0))) return nullptr;
   int B, R, layer_count = 0;
   if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &R, "rowsMax")) return nullptr;
   if (B < 0 || R < 0) return throw_range(env, "B and rowsMax must be >= 0");
@@ -520,27 +642,21 @@ napi_value Prefill(napi_env env, napi_callback_info info) {
   bool all_rows = false;
   napi_typeof(env, a.at(6), &t);
   if (t == napi_boolean) napi_get_value_bool(env, a.at(6), &all_rows);
+  all_rows = all_rows || layer_count > 0;
   float* out;
-  int rc;
-  napi_value O;
-  if (all_rows || layer_count > 0) {
-    O = new_f32(env, (int64_t)B * R * kD, &out);
-    if (!O) return nullptr;
-    rc = mb_prefill_rows(ctx, B, R, ids, nr, layer_count, out);
-  } else {
-    O = new_f32(env, (int64_t)B * kD, &out);
-    if (!O) return nullptr;
-    rc = mb_prefill(ctx, B, R, ids, nr, out);
-  }
-  if (rc) return throw_status(env, ctx, rc);
-  return O;
+  napi_value O = new_f32(env, (int64_t)B * (all_rows ? R : 1) * kD, &out);
+  if (!O) return nullptr;
+  return finish(env, a.at(0), ASYNC, O, {a.at(3), a.at(4)}, [=](mb_ctx* ctx) {
+    return all_rows ? mb_prefill_rows(ctx, B, R, ids, nr, layer_count, out)
+                    : mb_prefill(ctx, B, R, ids, nr, out);
+  });
 }
 
 // decodeStep(h, B, rows17 Int32Array[B*17], pos Int32Array[B]) -> hidden Float32Array[B*768]
+template <bool ASYNC>
 napi_value DecodeStep(napi_env env, napi_callback_info info) {
   Args a(env, info);
-  mb_ctx* ctx = get_ctx(env, a.at(0));
-  if (!ctx) return nullptr;
+  if (!get_ctx(env, a.at(0))) return nullptr;
   int B;
   if (!get_int(env, a.at(1), &B, "B")) return nullptr;
   if (B < 0) return throw_range(env, "B must be >= 0");
@@ -551,16 +667,15 @@ napi_value DecodeStep(napi_env env, napi_callback_info info) {
   float* out;
   napi_value O = new_f32(env, (int64_t)B * kD, &out);
   if (!O) return nullptr;
-  int rc = mb_decode_step(ctx, B, rows, pos, out);
-  if (rc) return throw_status(env, ctx, rc);
-  return O;
+  return finish(env, a.at(0), ASYNC, O, {a.at(2), a.at(3)},
+                [=](mb_ctx* ctx) { return mb_decode_step(ctx, B, rows, pos, out); });
 }
 
 // localFrame(h, B, hidden Float32Array[B*768]) -> {codes Int32Array[B*16], cont Int32Array[B]}
+template <bool ASYNC>
 napi_value LocalFrame(napi_env env, napi_callback_info info) {
   Args a(env, info);
-  mb_ctx* ctx = get_ctx(env, a.at(0));
-  if (!ctx) return nullptr;
+  if (!get_ctx(env, a.at(0))) return nullptr;
   int B;
   if (!get_int(env, a.at(1), &B, "B")) return nullptr;
   if (B < 0) return throw_range(env, "B must be >= 0");
@@ -570,13 +685,12 @@ napi_value LocalFrame(napi_env env, napi_callback_info info) {
   int32_t *codes, *cont;
   napi_value Cd = new_i32(env, (int64_t)B * kNvq, &codes), Ct = new_i32(env, B, &cont);
   if (!Cd || !Ct) return nullptr;
-  int rc = mb_local_frame(ctx, B, hidden, codes, cont);
-  if (rc) return throw_status(env, ctx, rc);
   napi_value o;
   napi_create_object(env, &o);
   napi_set_named_property(env, o, "codes", Cd);
   napi_set_named_property(env, o, "cont", Ct);
-  return o;
+  return finish(env, a.at(0), ASYNC, o, {a.at(2)},
+                [=](mb_ctx* ctx) { return mb_local_frame(ctx, B, hidden, codes, cont); });
 }
 
 // localSteps(h, B, hidden[B*768], maxStep) -> Float32Array[B*768]
@@ -601,10 +715,10 @@ napi_value LocalSteps(napi_env env, napi_callback_info info) {
 
 // decodeFrames(h, B, nFrames, hidden Float32Array[B*768] (in/out), pos Int32Array[B] (in/out))
 //   -> {codes Int32Array[nFrames*B*16], cont Int32Array[nFrames*B]}
+template <bool ASYNC>
 napi_value DecodeFrames(napi_env env, napi_callback_info info) {
   Args a(env, info);
-  mb_ctx* ctx = get_ctx(env, a.at(0));
-  if (!ctx) return nullptr;
+  if (!get_ctx(env, a.at(0))) return nullptr;
   int B, nf;
   if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &nf, "nFrames")) return nullptr;
   if (B < 0 || nf < 0) return throw_range(env, "B and nFrames must be >= 0");
@@ -618,13 +732,12 @@ napi_value DecodeFrames(napi_env env, napi_callback_info info) {
   if (!Cd) return nullptr;
   napi_value Ct = new_i32(env, (int64_t)nf * B, &cont);
   if (!Ct) return nullptr;
-  int rc = mb_decode_frames(ctx, B, nf, hidden, pos, codes, cont);
-  if (rc) return throw_status(env, ctx, rc);
   napi_value o;
   napi_create_object(env, &o);
   napi_set_named_property(env, o, "codes", Cd);
   napi_set_named_property(env, o, "cont", Ct);
-  return o;
+  return finish(env, a.at(0), ASYNC, o, {a.at(3), a.at(4)},
+                [=](mb_ctx* ctx) { return mb_decode_frames(ctx, B, nf, hidden, pos, codes, cont); });
 }
 
 // A 4-element array field of a config object (each entry an integer).
@@ -677,10 +790,10 @@ napi_value CodecInit(napi_env env, napi_callback_info info) {
 
 // codecDecode(h, B, nFrames, codes Int32Array[nFrames*B*16])
 //   -> pcm Float32Array[B*2*nFrames*3840] (per voice: left, then right)
+template <bool ASYNC>
 napi_value CodecDecode(napi_env env, napi_callback_info info) {
   Args a(env, info);
-  mb_ctx* ctx = get_ctx(env, a.at(0));
-  if (!ctx) return nullptr;
+  if (!get_ctx(env, a.at(0))) return nullptr;
   int B, nf;
   if (!get_int(env, a.at(1), &B, "B") || !get_int(env, a.at(2), &nf, "nFrames")) return nullptr;
   if (B < 0 || nf < 0) return throw_range(env, "B and nFrames must be >= 0");
@@ -690,9 +803,8 @@ napi_value CodecDecode(napi_env env, napi_callback_info info) {
   float* pcm;
   napi_value P = new_f32(env, (int64_t)B * 2 * nf * 3840, &pcm);
   if (!P) return nullptr;
-  int rc = mb_codec_decode(ctx, B, nf, codes, pcm);
-  if (rc) return throw_status(env, ctx, rc);
-  return P;
+  return finish(env, a.at(0), ASYNC, P, {a.at(3)},
+                [=](mb_ctx* ctx) { return mb_codec_decode(ctx, B, nf, codes, pcm); });
 }
 
 napi_value LastError(napi_env env, napi_callback_info info) {
@@ -724,14 +836,19 @@ napi_value Init(napi_env env, napi_value exports) {
       {"ringWriteRows", RingWriteRows},
       {"decodeAttention", DecodeAttention},
       {"prefillAttention", PrefillAttention},
-      {"prefill", Prefill},
-      {"decodeStep", DecodeStep},
-      {"localFrame", LocalFrame},
+      {"prefill", Prefill<false>},
+      {"prefillAsync", Prefill<true>},
+      {"decodeStep", DecodeStep<false>},
+      {"decodeStepAsync", DecodeStep<true>},
+      {"localFrame", LocalFrame<false>},
+      {"localFrameAsync", LocalFrame<true>},
       {"localSteps", LocalSteps},
-      {"decodeFrames", DecodeFrames},
+      {"decodeFrames", DecodeFrames<false>},
+      {"decodeFramesAsync", DecodeFrames<true>},
       {"codecInit", CodecInit},
       {"codecReset", SeqListCall<mb_codec_reset>},
-      {"codecDecode", CodecDecode},
+      {"codecDecode", CodecDecode<false>},
+      {"codecDecodeAsync", CodecDecode<true>},
       {"lastError", LastError},
   };
   for (const Fn& f : fns) {

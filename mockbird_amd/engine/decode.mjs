@@ -38,7 +38,7 @@ export class DecodeRunner {
   async globalStep(row, position, _layers, _lnF, _embed) {
     const staged = new Int32Array(ROW_WIDTH);
     for (let i = 0; i < ROW_WIDTH; i += 1) staged[i] = orDefault(row[i], AUDIO_PAD_ID);
-    return this.native.decodeStep(this.handle, 1, staged, Int32Array.of(position));
+    return this.native.decodeStepAsync(this.handle, 1, staged, Int32Array.of(position));
   }
 
   /**
@@ -46,7 +46,7 @@ export class DecodeRunner {
    * null when the text head chooses audio_end (decode.ts:788-939).
    */
   async nextFrame(hidden, _embed) {
-    const r = this.native.localFrame(this.handle, 1, hidden);
+    const r = await this.native.localFrameAsync(this.handle, 1, hidden);
     if (!r.cont[0]) return null;
     return Array.from(r.codes);
   }

@@ -7,9 +7,9 @@
 // weight table; the clone encoder (encodeWaveform) is not part of this
 // library.  A missing stage throws EngineNotImplemented, which is how the
 // reference itself reports one (gpu.ts:28-36, :279-281).
-import { HIDDEN, kvDtypeCode, loadNative, N_VQ, orDefault, ROW_WIDTH } from "./native.mjs";
+import { kvDtypeCode, loadNative, N_VQ, orDefault, ROW_WIDTH } from "./native.mjs";
 import { DecodeRunner } from "./decode.mjs";
-import { PrefillRunner, stageRows } from "./prefill.mjs";
+import { PrefillRunner, packPromptRows } from "./prefill.mjs";
 import { CODEC_SHAPE, resolveCodecTensors, resolveEngineTensors } from "./weights.mjs";
 
 export class EngineNotImplemented extends Error {
@@ -22,30 +22,40 @@ export class EngineNotImplemented extends Error {
 const SAMPLES_PER_FRAME = 3840;
 const SAMPLE_RATE = 48000;
 const CHANNELS = 2;
+const AUDIO_START = 6;
+/** -1.5 * 2^13: exact in fp32 and in bf16, so it reads back unchanged from either ring. */
+const KV_SENTINEL = -12288;
 
 /** buildFrameRow / frameRowFrom (policy.ts:83-88, promptRows.ts:39-44). */
 export function frameRowFrom(assistantSlot, frame) {
   const row = new Int32Array(ROW_WIDTH).fill(1024);
   row[0] = assistantSlot;
-  for (let k = 0; k < Math.min(frame.length, ROW_WIDTH - 1); k += 1) row[k + 1] = frame[k];
+  row.set(frame.slice(0, ROW_WIDTH - 1), 1);
   return row;
 }
 
+/** max |a - b| over two equally long arrays */
+function maxAbsDiff(a, b) {
+  let m = 0;
+  for (let i = 0; i < a.length; i += 1) m = Math.max(m, Math.abs(a[i] - b[i]));
+  return m;
+}
+
+/**
+ * One engine = one context holding one voice.  All per-utterance state is
+ * the `utterance` record: how many rows its ring holds (the position the next
+ * decode step appends at) and the hidden state of its latest global step.
+ * `null` between reset() and the next prefill.
+ */
 class HipTtsEngineImpl {
   constructor(native, handle, info, settings, maxSlots, maxRows, layers) {
+    Object.assign(this, { native, handle, info, settings, layerCount: layers, maxSlots });
     this.sampleRate = SAMPLE_RATE;
     this.channels = CHANNELS;
     this.samplesPerFrame = SAMPLES_PER_FRAME;
-    this.native = native;
-    this.handle = handle;
-    this.info = info;
-    this.settings = settings;
-    this.layerCount = layers;
     this.prefillRunner = new PrefillRunner(native, handle, maxSlots, maxRows);
     this.decoder = new DecodeRunner(native, handle, maxSlots, settings);
-    /** rows currently in the global KV cache (== the next sequence position) */
-    this.pastValidLength = 0;
-    this.lastHidden = null;
+    this.utterance = null;
     this.hasCodec = false;
     this.disposed = false;
   }
@@ -54,78 +64,89 @@ class HipTtsEngineImpl {
     return this.info;
   }
 
-  /** rows in the global KV cache -- the decode step appends at this position */
+  /** rows in the global KV ring: the position the next decode step appends at */
   get position() {
-    return this.pastValidLength;
+    return this.utterance ? this.utterance.rows : 0;
   }
 
   async prefill(input) {
-    const rows = input.inputIds.length;
-    if (rows === 0) throw new Error("prefill called with no rows");
-    this.prefillRunner.stageIds(stageRows(input.inputIds));
-    const hidden = await this.prefillRunner.run(rows, null, null, this.decoder.maxSlotCount);
-    this.pastValidLength = rows;
-    this.lastHidden = hidden.slice((rows - 1) * HIDDEN, rows * HIDDEN);
-    return this.lastHidden;
+    const ids = packPromptRows(input.inputIds);
+    const rows = ids.length / ROW_WIDTH;
+    const hidden = await this.native.prefillAsync(this.handle, 1, rows, ids, Int32Array.of(rows));
+    this.utterance = { rows, hidden };
+    return hidden;
+  }
+
+  async decodeStep(input) {
+    const u = this.utterance;
+    if (u === null) throw new Error("decodeStep before prefill");
+    const at = orDefault(input.position, u.rows);
+    const hidden = await this.decoder.globalStep(input.row, at);
+    u.rows = at + 1;
+    u.hidden = hidden;
+    return hidden;
+  }
+
+  nextFrame(hidden) {
+    return this.decoder.nextFrame(hidden);
   }
 
   /**
-   * Warm-up (gpu.ts:196-235): prove the read-back path with a poisoned cache,
-   * run one two-row prefill, check the hidden state is finite and non-zero and
-   * that layer 0's cache was written, then reset.
+   * Bring-up self-test of this library's path, then a clean state.
+   *  1. Layer 0's first four slots are poisoned and a two-row prompt is
+   *     prefilled: slots 0-1 must now hold K/V and slots 2-3 must still read
+   *     the sentinel (the read-back path works, and the prefill wrote exactly
+   *     its rows).
+   *  2. The prefill's hidden state must be finite and non-zero.
+   *  3. The same two rows as a one-row prefill plus one decode step at
+   *     position 1 must give the same hidden state: the decode path (fused
+   *     ring append + decode attention) agrees with the prefill path (ring
+   *     write + causal prefill attention).
+   * The failure messages are the reference's where its warm-up checks the
+   * same condition (gpu.ts:201-234).
    */
   async warmup() {
-    const row = new Array(ROW_WIDTH).fill(1024);
-    row[0] = 6; // audio_start_token_id
-    const rows = [row, row];
-    await this.prefillRunner.poisonKv(rows.length);
-    const poison = await this.prefillRunner.readLayerCache(0, rows.length);
-    if (!poison.key.every((value) => value === -12345.5)) {
-      throw new Error("warmup read-back is broken: the KV sentinel was not visible");
+    const row = new Int32Array(ROW_WIDTH).fill(1024);
+    row[0] = AUDIO_START;
+    const prompt = [Array.from(row), Array.from(row)];
+    const probeSlots = Math.min(4, this.maxSlots);
+    this.native.ringPoison(this.handle, 0, 0, probeSlots, KV_SENTINEL);
+    const t0 = Date.now();
+    const both = await this.prefill({ inputIds: prompt, attentionMask: [[1, 1]] });
+    const prefillMs = Date.now() - t0;
+    if (both.some((x) => !Number.isFinite(x))) {
+      throw new Error("warmup produced a non-finite hidden state — a kernel wrote garbage");
     }
-    const started = Date.now();
-    const hidden = await this.prefill({ inputIds: rows, attentionMask: [[1, 1]] });
-    const elapsed = Date.now() - started;
-    for (const value of hidden) {
-      if (!Number.isFinite(value)) {
-        throw new Error("warmup produced a non-finite hidden state — a kernel wrote garbage");
-      }
-    }
-    if (!hidden.some((value) => value !== 0)) {
+    if (both.every((x) => x === 0)) {
       throw new Error("warmup produced an all-zero hidden state — nothing was computed");
     }
-    const cache = await this.prefillRunner.readLayerCache(0, rows.length);
-    if (!cache.key.some((value) => value !== 0) || !cache.value.some((value) => value !== 0)) {
+    const ring = this.native.readRing(this.handle, 0, 0, 0, probeSlots);
+    const untouched = ring.key.subarray(prompt.length * 768);
+    if (untouched.length && !untouched.every((x) => x === KV_SENTINEL)) {
+      throw new Error("warmup read-back is broken: the KV sentinel was not visible");
+    }
+    const written = (a) => a.subarray(0, prompt.length * 768).some((x) => x !== 0 && x !== KV_SENTINEL);
+    if (!written(ring.key) || !written(ring.value)) {
       throw new Error(
         "warmup left the layer-0 KV cache empty (read-back verified: the sentinel was visible)",
       );
     }
+    await this.prefill({ inputIds: prompt.slice(0, 1), attentionMask: [[1]] });
+    const stepped = await this.decodeStep({ row, position: 1 });
+    const gap = maxAbsDiff(stepped, both);
+    if (!(gap < 1e-3)) {
+      throw new Error(`warmup: the decode step disagrees with the prefill of the same rows (max |diff| ${gap})`);
+    }
     this.reset();
-    return { prefillMs: elapsed, layers: this.layerCount, rows: rows.length };
+    return { prefillMs, layers: this.layerCount, rows: prompt.length };
   }
 
-  /** A fresh utterance: drop the KV ring and the repetition history (gpu.ts:237-242). */
+  /** A fresh utterance: empty ring, repetition history and codec rings (gpu.ts:237-242). */
   reset() {
-    this.pastValidLength = 0;
-    this.lastHidden = null;
-    this.decoder.clearSeen();
+    this.utterance = null;
     this.native.ringReset(this.handle, null);
+    this.decoder.clearSeen();
     if (this.hasCodec) this.native.codecReset(this.handle, null);
-  }
-
-  async decodeStep(input) {
-    if (!this.lastHidden) throw new Error("decodeStep before prefill");
-    const position = orDefault(input.position, this.pastValidLength);
-    const hidden = await this.decoder.globalStep(input.row, position);
-    this.pastValidLength = position + 1;
-    this.lastHidden = hidden;
-    return hidden;
-  }
-
-  async nextFrame(hidden) {
-    const frame = await this.decoder.nextFrame(hidden);
-    if (frame) this.lastHidden = hidden;
-    return frame;
   }
 
   /**
@@ -134,16 +155,15 @@ class HipTtsEngineImpl {
    * channel, 3840 samples per frame.  A missing code reads as 0, as there.
    */
   async decodeFrames(frames) {
-    if (!frames.length) return [];
+    if (frames.length === 0) return [];
     if (!this.hasCodec) throw new EngineNotImplemented("codec decoder (no codec weights given)");
-    const n = frames.length;
-    const codes = new Int32Array(n * N_VQ);
-    for (let f = 0; f < n; f += 1) {
-      for (let k = 0; k < N_VQ; k += 1) codes[f * N_VQ + k] = orDefault(frames[f][k], 0);
-    }
-    const pcm = this.native.codecDecode(this.handle, 1, n, codes);
-    const T = n * SAMPLES_PER_FRAME;
-    return [pcm.slice(0, T), pcm.slice(T, 2 * T)];
+    const codes = new Int32Array(frames.length * N_VQ);
+    frames.forEach((frame, f) => {
+      for (let k = 0; k < N_VQ; k += 1) codes[f * N_VQ + k] = orDefault(frame[k], 0);
+    });
+    const pcm = await this.native.codecDecodeAsync(this.handle, 1, frames.length, codes);
+    const half = pcm.length / 2;
+    return [pcm.subarray(0, half), pcm.subarray(half)];
   }
 
   encodeWaveform(_waveform, _length) {
@@ -153,7 +173,7 @@ class HipTtsEngineImpl {
   dispose() {
     if (this.disposed) return;
     this.disposed = true;
-    this.decoder.dispose();
+    this.utterance = null;
     this.prefillRunner.dispose();
     this.native.destroy(this.handle);
   }
@@ -209,7 +229,8 @@ export async function createGpuEngineFor(tables, log, options) {
       log(`codec: ${codecTensors.length} tensors, stages ${codecShape.layersPerStage.join("/")}`);
     }
     const info = { adapterName: "MI355X (gfx950, HIP)", deviceBytes: native.deviceBytes(handle) };
-    const engine = new HipTtsEngineImpl(native, handle, info, options.localHead, maxSlots, maxRows, layers);
+    const engine = new HipTtsEngineImpl(native, handle, info, options.localHead, maxSlots, maxRows,
+      layers);
     engine.hasCodec = codecShape !== null;
     log(`engine ready: ${layers} layers, KV ring ${maxSlots} slots, vocab ${vocab}`);
     const warm = await engine.warmup();

@@ -3,7 +3,7 @@
 // the batch only shares launches.  Rings wrap by default (slot = pos mod C,
 // FIFO eviction), the codec ring's rule (kernels-decode.ts:590-714).
 import { HIDDEN, kvDtypeCode, loadNative, N_VQ, orDefault, ROW_WIDTH } from "./native.mjs";
-import { stageRows } from "./prefill.mjs";
+import { packPromptRows } from "./prefill.mjs";
 import { CODEC_SHAPE, resolveCodecTensors, resolveEngineTensors } from "./weights.mjs";
 
 const SAMPLES_PER_FRAME = 3840;
@@ -34,9 +34,9 @@ export class MultiVoiceEngine {
     const rowsMax = Math.max(...n);
     if (Math.min(...n) < 1) throw new Error("prefill called with no rows");
     const ids = new Int32Array(B * rowsMax * ROW_WIDTH).fill(1024);
-    prompts.forEach((p, b) => ids.set(stageRows(p), b * rowsMax * ROW_WIDTH));
+    prompts.forEach((p, b) => ids.set(packPromptRows(p), b * rowsMax * ROW_WIDTH));
     this.native.clearSeen(this.handle, null);
-    const flat = this.native.prefill(this.handle, B, rowsMax, ids, n);
+    const flat = await this.native.prefillAsync(this.handle, B, rowsMax, ids, n);
     this.voices = B;
     this.hidden = flat;
     this.positions = n.slice();
@@ -52,7 +52,8 @@ export class MultiVoiceEngine {
   async generate(nFrames) {
     const B = this.voices;
     if (!B) throw new Error("generate before prefill");
-    const { codes, cont } = this.native.decodeFrames(this.handle, B, nFrames, this.hidden, this.positions);
+    const { codes, cont } = await this.native.decodeFramesAsync(this.handle, B, nFrames, this.hidden,
+      this.positions);
     const frames = Array.from({ length: B }, () => []);
     for (let f = 0; f < nFrames; f += 1) {
       for (let b = 0; b < B; b += 1) {
@@ -73,7 +74,7 @@ export class MultiVoiceEngine {
     const B = hidden.length;
     const flat = new Float32Array(B * HIDDEN);
     hidden.forEach((h, b) => flat.set(h, b * HIDDEN));
-    const r = this.native.localFrame(this.handle, B, flat);
+    const r = await this.native.localFrameAsync(this.handle, B, flat);
     return Array.from({ length: B }, (_, b) =>
       r.cont[b] ? Array.from(r.codes.subarray(b * N_VQ, (b + 1) * N_VQ)) : null,
     );
@@ -84,7 +85,7 @@ export class MultiVoiceEngine {
     const B = rows.length;
     const flat = new Int32Array(B * ROW_WIDTH).fill(1024);
     rows.forEach((r, b) => flat.set(r.subarray ? r.subarray(0, ROW_WIDTH) : r.slice(0, ROW_WIDTH), b * ROW_WIDTH));
-    const out = this.native.decodeStep(this.handle, B, flat, Int32Array.from(positions));
+    const out = await this.native.decodeStepAsync(this.handle, B, flat, Int32Array.from(positions));
     return Array.from({ length: B }, (_, b) => out.slice(b * HIDDEN, (b + 1) * HIDDEN));
   }
 
@@ -104,7 +105,7 @@ export class MultiVoiceEngine {
       if (codes[f].length !== B) throw new Error(`frame ${f} has ${codes[f].length} voices, expected ${B}`);
       for (let b = 0; b < B; b += 1) flat.set(codes[f][b].slice(0, N_VQ), (f * B + b) * N_VQ);
     }
-    const pcm = this.native.codecDecode(this.handle, B, n, flat);
+    const pcm = await this.native.codecDecodeAsync(this.handle, B, n, flat);
     const T = n * SAMPLES_PER_FRAME;
     return Array.from({ length: B }, (_, b) => [
       pcm.slice((2 * b) * T, (2 * b + 1) * T),

@@ -83,6 +83,30 @@ export interface Native {
   codecReset(h: NativeHandle, voices: Int32Array | null): void;
   /** codes [nFrames][B][16] -> pcm [B][2][nFrames * 3840] */
   codecDecode(h: NativeHandle, B: number, nFrames: number, codes: Int32Array): Float32Array;
+  /**
+   * The same calls run on a libuv worker thread: each returns a Promise of
+   * what its synchronous form returns.  While one is in flight every other
+   * call on the handle throws an Error with code "MB_ERR_BUSY".
+   */
+  prefillAsync(
+    h: NativeHandle,
+    B: number,
+    rowsMax: number,
+    ids: Int32Array,
+    nRows: Int32Array,
+    layerCount?: number,
+    allRows?: boolean,
+  ): Promise<Float32Array>;
+  decodeStepAsync(h: NativeHandle, B: number, rows17: Int32Array, pos: Int32Array): Promise<Float32Array>;
+  localFrameAsync(h: NativeHandle, B: number, hidden: Float32Array): Promise<{ codes: Int32Array; cont: Int32Array }>;
+  decodeFramesAsync(
+    h: NativeHandle,
+    B: number,
+    nFrames: number,
+    hidden: Float32Array,
+    pos: Int32Array,
+  ): Promise<{ codes: Int32Array; cont: Int32Array }>;
+  codecDecodeAsync(h: NativeHandle, B: number, nFrames: number, codes: Int32Array): Promise<Float32Array>;
   lastError(h: NativeHandle): string;
 }
 

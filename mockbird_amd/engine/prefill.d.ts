@@ -12,4 +12,5 @@ export class PrefillRunner {
   dispose(): void;
 }
 
-export function stageRows(inputIds: number[][]): Uint32Array;
+/** A prompt as 17-wide Int32 rows, missing columns padded with 1024; throws on no rows. */
+export function packPromptRows(inputIds: number[][]): Int32Array;

@@ -49,7 +49,7 @@ export class PrefillRunner {
     }
     const ids = this.staged.subarray(0, rows * ROW_WIDTH);
     const count = layerCount === undefined ? 0 : layerCount;
-    return this.native.prefill(this.handle, 1, rows, ids, Int32Array.of(rows), count, true);
+    return this.native.prefillAsync(this.handle, 1, rows, ids, Int32Array.of(rows), count, true);
   }
 
   /**
@@ -72,14 +72,19 @@ export class PrefillRunner {
   }
 }
 
-/** Pad a prompt of number rows to 17-wide u32 ids with the audio pad (gpu.ts:173-181). */
-export function stageRows(inputIds) {
-  const rows = inputIds.length;
-  const ids = new Uint32Array(rows * ROW_WIDTH);
-  inputIds.forEach((row, i) => {
-    for (let j = 0; j < ROW_WIDTH; j += 1) {
-      ids[i * ROW_WIDTH + j] = j < row.length ? row[j] >>> 0 : AUDIO_PAD_ID;
-    }
-  });
-  return ids;
+/**
+ * A prompt of rows (number arrays: text id, then up to 16 codes) as one
+ * Int32Array of 17-wide rows; columns a row leaves out are the audio pad
+ * (the reference pads the same way, gpu.ts:176-181).  Throws on an empty
+ * prompt with the reference's message.
+ */
+export function packPromptRows(inputIds) {
+  if (inputIds.length === 0) throw new Error("prefill called with no rows");
+  const out = new Int32Array(inputIds.length * ROW_WIDTH).fill(AUDIO_PAD_ID);
+  let at = 0;
+  for (const row of inputIds) {
+    out.set(row.length > ROW_WIDTH ? row.slice(0, ROW_WIDTH) : row, at);
+    at += ROW_WIDTH;
+  }
+  return out;
 }

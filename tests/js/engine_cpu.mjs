@@ -6,7 +6,7 @@
 import { loadNative } from "../../mockbird_amd/engine/native.mjs";
 import { createGpuEngine, EngineNotImplemented, frameRowFrom } from "../../mockbird_amd/engine/gpu.mjs";
 import { resolveCodecTensors, resolveEngineTensors, tableOf } from "../../mockbird_amd/engine/weights.mjs";
-import { stageRows } from "../../mockbird_amd/engine/prefill.mjs";
+import { packPromptRows } from "../../mockbird_amd/engine/prefill.mjs";
 
 const out = {};
 const native = loadNative();
@@ -92,7 +92,12 @@ out.codec = resolveCodecTensors(tableOf(c), { layersPerStage: codecLayers, conte
   .map((x) => [x.name, x.dims, x.data[0]]);
 
 // staging and frame rows
-out.staged = Array.from(stageRows([[6], [8, 1, 2, 3]]));
+out.staged = Array.from(packPromptRows([[6], [8, 1, 2, 3]]));
+try {
+  packPromptRows([]);
+} catch (e) {
+  out.emptyPrompt = e.message;
+}
 out.frameRow = Array.from(frameRowFrom(9, [5, 6, 7]));
 
 // errors before any device call
@@ -106,6 +111,11 @@ try {
   native.prefill({}, 1, 1, new Int32Array(17), Int32Array.of(1));
 } catch (e) {
   errs.badHandle = [e.name, e.message];
+}
+try {
+  native.prefillAsync({}, 1, 1, new Int32Array(17), Int32Array.of(1));
+} catch (e) {
+  errs.badHandleAsync = [e.name, e.message];
 }
 try {
   createGpuEngine();

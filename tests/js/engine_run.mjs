@@ -50,6 +50,26 @@ async function single() {
     res.hiddens.push(Array.from(hidden));
   }
   res.position = engine.position;
+  // the engine's calls run off the JS thread: the event loop keeps turning
+  // while a prefill runs, and another call on the busy context is refused
+  let ticks = 0;
+  let running = true;
+  const spin = () => {
+    if (!running) return;
+    ticks += 1;
+    setImmediate(spin);
+  };
+  setImmediate(spin);
+  const pending = engine.prefill({ inputIds: prompt, attentionMask: [prompt.map(() => 1)] });
+  let busy = null;
+  try {
+    engine.native.readRing(engine.handle, 0, 0, 0, 1);
+  } catch (e) {
+    busy = e.code;
+  }
+  await pending;
+  running = false;
+  res.async = { ticks, busy };
   // the codec: the voice's code frames over two calls (the rings carry over)
   const codes = spec.codec.single;
   const a = await engine.decodeFrames(codes.slice(0, 2));

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_argument_errors():
     lib = mb.load()
-    assert lib.mb_abi_version() == 1
+    assert lib.mb_abi_version() == 2
     # a bad config is rejected before any device call
     cfg = mb.Config(0, 0, 0, 0, 0, 0, 0, 0)
     h = ctypes.c_void_p()

@@ -16,6 +16,7 @@ BINDINGS = {
     "decodeStep", "destroy", "deviceBytes", "lastError", "localFrame", "localSteps", "prefill",
     "prefillAttention", "readRing", "ringAppend", "ringPoison", "ringReset", "ringWriteRows",
     "setLocalHead", "uploadTensor", "codecInit", "codecReset", "codecDecode",
+    "prefillAsync", "decodeStepAsync", "localFrameAsync", "decodeFramesAsync", "codecDecodeAsync",
 }
 
 
@@ -38,7 +39,7 @@ def report():
 
 def test_addon_exports_every_binding(report):
     assert set(report["exports"]) == BINDINGS
-    assert report["abi"] == 1
+    assert report["abi"] == 2
 
 
 def test_tables_resolve_by_name_then_shape(report):
@@ -65,12 +66,14 @@ def test_rows_are_padded_with_the_audio_pad(report):
     assert s[:17] == [6] + [1024] * 16
     assert s[17:34] == [8, 1, 2, 3] + [1024] * 13
     assert report["frameRow"] == [9, 5, 6, 7] + [1024] * 13
+    assert report["emptyPrompt"] == "prefill called with no rows"
 
 
 def test_errors_throw_before_device_calls(report):
     e = report["errors"]
     assert e["badConfig"][0] == "MB_ERR_ARG"
     assert e["badHandle"][0] == "TypeError"
+    assert e["badHandleAsync"][0] == "TypeError"  # thrown before a Promise is made
     assert e["notImplemented"] == [True, "EngineNotImplemented"]
 
 
