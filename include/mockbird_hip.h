@@ -203,6 +203,18 @@ int mb_append_attend_dev(mb_ctx* ctx, int layer, int B, const void* qkv, int qkv
 int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda, const float* W,
                   const float* bias, float* C, int64_t ldc, int epi);
 
+/* mb_linear_dev that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as mb_linear_dev; the split-K partials that
+ * mb_linear_dev keeps in the context's growable scratch live in a static
+ * 4 MiB device array per GPU instead (resolved by mb_create, held until the
+ * process ends).  That size covers every split the kernel chooses; a shape
+ * needing more returns MB_ERR_ARG.  Every call on one GPU shares that GPU's
+ * array, so calls that overlap on one GPU race.  Enqueue only. */
+int mb_linear_noalloc_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
+                          const float* W, const float* bias, float* C, int64_t ldc, int epi);
+
 /* ------------------------------------------------------------------ model
  * The decoder around the rings, fp32 weights uploaded with mb_upload_tensor.
  * Row ids are int32 [17]: text id in column 0 (< vocab), audio codes in

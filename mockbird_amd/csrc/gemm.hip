@@ -428,14 +428,25 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
   *(float4*)cp = epilogue4<EPI>(sum, bias, col, cp);
 }
 
+// part_ext (optional, part_cap floats) holds the split-K partials instead of
+// the context's growable scratch.
 template <int MT, int ST, bool LNF>
 static int stream_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
                          int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
-                         const float* lnc, const float* lnd, bool tiled) {
+                         const float* lnc, const float* lnd, bool tiled, float* part_ext = nullptr,
+                         size_t part_cap = 0) {
   const int tx = N / 64, ty = (M + MT - 1) / MT;
   float* part = nullptr;
   if (S > 1) {
-    part = (float*)scratch(ctx, "gemm_part", (size_t)S * M * N * 4);
+    const size_t need = (size_t)S * M * N;
+    if (part_ext) {
+      if (need > part_cap)
+        return fail(ctx, MB_ERR_ARG, "gemm split-K partials need %zu floats, the buffer holds %zu",
+                    need, part_cap);
+      part = part_ext;
+    } else {
+      part = (float*)scratch(ctx, "gemm_part", need * 4);
+    }
     if (!part) return fail(ctx, MB_ERR_NOMEM, "gemm split-K partials (%d x %d x %d)", S, M, N);
   }
   dim3 grid((unsigned)tx, (unsigned)ty, (unsigned)S);
@@ -597,8 +608,16 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // Larger M: the LDS-tiled kernel with the largest tile that still gives the
 // chip (256 CUs) a block per CU (128 x 128 only from K = 512 up), else the
 // smallest tile.
+size_t gemm_partial_floats(int M, int N, int K) {
+  if (M <= 0 || !gemm_streams(M, N)) return 0;
+  int mt, S;
+  stream_shape(M, N, K, false, mt, S);
+  return S > 1 ? (size_t)S * M * N : 0;
+}
+
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
-                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled) {
+                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled, float* part,
+                size_t part_cap) {
   if (M <= 0) return MB_OK;
   if (w_tiled && !gemm_streams(M, N))
     return fail(ctx, MB_ERR_STATE, "tiled weights need the streaming kernel (M %d N %d)", M, N);
@@ -609,10 +628,10 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
     int mt, S;
     stream_shape(M, N, K, false, mt, S);
     switch (mt) {
-      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
-      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
-      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
-      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled);
+      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
     }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };

@@ -167,6 +167,7 @@ int mb_create(const mb_config* cfg, mb_ctx** out) {
   do {
     hipError_t e = hipSetDevice(cfg->device);
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipSetDevice"); break; }
+    if ((rc = noalloc_init(ctx))) break;
     e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipStreamCreate"); break; }
     ctx->stream = ctx->own_stream;

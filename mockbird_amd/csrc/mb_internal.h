@@ -275,8 +275,18 @@ enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2, EPI_SCALE_ADD = 3, EPI_GELU_ERF
 // W is [K][N] row-major, or with w_tiled the column-block-major copy from
 // launch_tile_w ([N / 64][K][64]; only where gemm_streams(M, N), else
 // MB_ERR_STATE).
+// `part` (optional, part_cap floats) takes the streaming kernel's split-K
+// partials in place of the context's growable scratch; a split that needs
+// more is MB_ERR_ARG.
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
-                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled = false);
+                const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled = false,
+                float* part = nullptr, size_t part_cap = 0);
+// Floats of split-K partials launch_gemm writes for an M x N x K projection
+// (0: no split).
+size_t gemm_partial_floats(int M, int N, int K);
+// noalloc.hip: resolve the static split-K scratch array's address on the
+// context's (current) device, once per device.
+int noalloc_init(mb_ctx* ctx);
 int launch_tile_w(mb_ctx* ctx, const float* W, int K, int N, float* Wt);
 
 // LayerNorm folded into the projection after it: Wg, c, d from
