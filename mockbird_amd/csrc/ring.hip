@@ -261,12 +261,21 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 }
 
 // One block per (query, head): the live window [0, min(cur + 1, C)) of the
-// query at position cur = pos0[b] + r is cut into `nw` equal ranges (whole
-// load batches), one per wave; the waves fold their online-softmax partials
+// query at position cur = pos0[b] + r is cut into batches of GU = G * U
+// slots, and the block's `nw` waves take them in turn (wave w: batches w,
+// w + nw, ...), so the block reads its (sequence, head) run front to back as
+// one sequential stream.  The waves fold their online-softmax partials
 // through LDS and wave 0 writes the normalised row.  A query attends the
 // slots whose stored position p satisfies 0 <= cur - p < C
 // (kernels-decode.ts:608-611); they all lie inside physical slots
 // [0, min(cur + 1, C)).
+//
+// Why the batches alternate: a read-only kernel over the same windows (64
+// sequences, C = 2048, bf16) reached 0.70 of 8 TB/s when each wave streamed
+// its own quarter of the window, and 0.77 when the waves alternated 4-load
+// batches; at C = 4096 (full windows) 0.64 against 0.78.  A plain sequential
+// read of 4 GiB reached 0.87 on the same GPU.  Fewer, longer streams keep
+// the HBM row buffers open.
 //
 // Lane layout: LR = 64 / VD lanes hold one 64-dim row (VD dims each, one
 // 16-byte load), so a wave covers G = VD consecutive slots -- 1 KB of one
@@ -275,9 +284,9 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 // lane group keeps its own online-softmax state (max, sum, VD accumulators)
 // and the G groups merge with cross-row shuffles at the end of the range.
 //
-// Liveness: for each tile of 256 slots every lane loads the stored positions
-// of 4 slots and the wave turns them into four 64-bit ballot masks, so the
-// per-slot test in the hot loop is a bit lookup, not a memory access.
+// Liveness: each batch's stored positions are loaded with its K and V rows
+// (one dword per lane) and turned into one 64-bit ballot mask, so no load
+// waits on another and the per-slot test is a bit lookup.
 //
 // No barrier is skipped: a block whose query row is beyond n_rows returns as
 // a whole before the only __syncthreads.
@@ -285,10 +294,11 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 // With APPEND the kernel also does the ring append of ROPE_SPLIT_RING
 // (kernels-decode.ts:216-241) for its (sequence, head): `q` is then the fused
 // q | k | v row (IN_BF16: bf16 elements), q is roped in registers (and stored
-// to q_out when given), and the wave whose range holds slot cur mod C (cur in
-// a non-wrapping ring) ropes k, stores K and V there -- the head-0 block also
-// records the slot's position -- and feeds the new row to its own batch from
-// registers, so the attention sees it without reading it back.  Rows 1 only.
+// to q_out when given), and the wave whose batches hold slot cur mod C (cur
+// in a non-wrapping ring) ropes k, stores K and V there before its loop --
+// the head-0 block also records the slot's position -- and feeds the new row
+// to the batch that covers the slot from registers, so the attention sees it
+// without reading it back.  Rows 1 only.
 // The fused fp32 form keeps 3 waves per SIMD (at most 168 VGPRs): with
 // fewer, the local head's launches at 256 voices (3072 one-wave blocks) no
 // longer fit the chip in one round.  The bf16 forms get 4 from their
@@ -304,7 +314,7 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   constexpr int LR = 64 / VD;
   constexpr int G = VD;
   constexpr int GU = G * U;
-  constexpr int TILE = 256;
+  static_assert(GU <= 64, "one stored position per lane covers a batch");
   constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
   __shared__ float fold[MAXNW][PART];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -314,53 +324,50 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   const int g = lane / LR, sub = lane % LR;
   const int64_t cur = (int64_t)pos0[b] + r;
   const int nvalid = cur < 0 ? 0 : (int)(cur + 1 < C ? cur + 1 : C);
-  int per = (nvalid + nw - 1) / nw;
-  per = (per + GU - 1) / GU * GU;
-  const int s0 = wave * per;
-  const int s1 = min(s0 + per, nvalid);
+  // the block's waves take the window's batches in turn: wave w reads batches
+  // w, w + nw, w + 2 nw, ..., so the block streams its (sequence, head) run
+  // front to back as one sequential read
+  const int s0 = wave * GU, step = nw * GU, s1 = nvalid;
 
   const int64_t kv_off = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
   const char* kbase = (const char*)ring_k + kv_off * (KV_BF16 ? 2 : 4);
   const char* vbase = (const char*)ring_v + kv_off * (KV_BF16 ? 2 : 4);
   const int32_t* sp = slot_pos + (int64_t)b * C;
-  // Fused fp32 form (one voice's global layers, the local head): slot_pos of
-  // the wave's first 256-slot tile (4 slots per lane) is loaded before the
-  // q | k | v row, so the two round trips overlap; frames 0.8 / 0.45 / 0.45 %
-  // faster at 1 / 64 / 256 voices.  Every other tile, and the bf16 forms,
-  // load slot_pos at the tile's start: in the bf16 forms the early load made
-  // the 64-sequence C = 2048 step 2.3 % slower on one GPU (0.2 % faster on
-  // another).
-  constexpr bool kEarlySlots = APPEND && !KV_BF16;
-  int32_t spn[4];
-  if constexpr (kEarlySlots) {
+
+  // One batch = GU slots [base, base + GU): lane (g, sub) loads the K and V
+  // rows of slots base + u * G + g (u < U) as 16-byte pieces, and lane l < GU
+  // also loads the stored position of slot base + l, so one ballot gives the
+  // whole batch's liveness with no round trip of its own.  Slots past the
+  // wave's range read as empty, and their K/V loads are clamped to `base`.
+  uint4 kr[U], vr[U];
+  int32_t spl = -1;
+  auto issue = [&](int base) {
+    spl = (lane < GU && base + lane < s1) ? sp[base + lane] : -1;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const int idx = s0 + 4 * lane + c;
-      spn[c] = idx < min(s0 + TILE, s1) ? sp[idx] : -1;
+    for (int u = 0; u < U; u++) {
+      const int slot = base + u * G + g;
+      const int sl = slot < s1 ? slot : base;
+      kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
+      vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
     }
-  }
+  };
 
   float qv[VD];
   // The appended row: its slot and whether this wave's range holds it.  The
-  // owning wave issues its k and v loads here but ropes, rounds and stores
-  // them only in the batch that covers the slot, so the loads overlap the
-  // batches before it.
+  // owning wave ropes k, stores K and V into the slot before its loop and
+  // keeps the two packed rows to feed the batch that covers the slot.
   int slot_new = -1;
   bool owner = false;
-  float ki[VD], vi[VD], cs[VD / 2], sn[VD / 2];
+  uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   if (APPEND) {
     const int64_t roff = row_at(q_rows, b, r) + head * HD + sub * VD;
-    float qi[VD], qo[VD];
+    float qi[VD], qo[VD], cs[VD / 2], sn[VD / 2];
     load_n<IN_BF16, VD>(q, roff, qi);
     const bool have = cur >= 0 && cur <= INT32_MAX && (wrap || cur < C);
     const int32_t pos = (int32_t)(have ? cur : 0);
     if (have) {
       slot_new = wrap ? (int)(cur % C) : (int)cur;
-      owner = (slot_new >= s0 && slot_new < s1);
-    }
-    if (owner) {
-      load_n<IN_BF16, VD>(q, roff + D, ki);
-      load_n<IN_BF16, VD>(q, roff + 2 * D, vi);
+      owner = slot_new < s1 && (slot_new / GU) % nw == wave;
     }
 #pragma unroll
     for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
@@ -373,13 +380,33 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
     }
 #pragma unroll
     for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
+    if (s0 < s1) issue(s0);
+    if (owner) {  // wave-uniform
+      float ki[VD], vi[VD], ko[VD];
+      load_n<IN_BF16, VD>(q, roff + D, ki);
+      load_n<IN_BF16, VD>(q, roff + 2 * D, vi);
+#pragma unroll
+      for (int j = 0; j < VD / 2; j++)
+        rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
+      knew = pack16<KV_BF16>(ko);
+      vnew = pack16<KV_BF16>(vi);
+      if (g == 0) {
+        *(uint4*)((char*)ring_k + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = knew;
+        *(uint4*)((char*)ring_v + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = vnew;
+        if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
+      }
+    }
   } else {
     const float* qp = (const float*)q + row_at(q_rows, b, r) + head * HD + sub * VD;
+    float4 qt[VD / 4];
 #pragma unroll
-    for (int i = 0; i < VD; i += 4) {
-      const float4 t = *(const float4*)(qp + i);
+    for (int i = 0; i < VD / 4; i++) qt[i] = *(const float4*)(qp + 4 * i);
+    if (s0 < s1) issue(s0);
+#pragma unroll
+    for (int i = 0; i < VD / 4; i++) {
       // 0.125 = 2^-3: pre-scaling q is exact
-      qv[i] = t.x * 0.125f; qv[i + 1] = t.y * 0.125f; qv[i + 2] = t.z * 0.125f; qv[i + 3] = t.w * 0.125f;
+      qv[4 * i] = qt[i].x * 0.125f; qv[4 * i + 1] = qt[i].y * 0.125f;
+      qv[4 * i + 2] = qt[i].z * 0.125f; qv[4 * i + 3] = qt[i].w * 0.125f;
     }
   }
 
@@ -387,66 +414,38 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
 #pragma unroll
   for (int i = 0; i < VD; i++) acc[i] = 0.f;
 
-  for (int t0 = s0; t0 < s1; t0 += TILE) {
-    const int t1 = min(t0 + TILE, s1);
-    uint64_t live[4];
+  for (int base = s0; base < s1; base += step) {
+    const int64_t dlt = cur - (int64_t)spl;
+    const uint64_t live = __ballot(spl >= 0 && dlt >= 0 && dlt < C);
+    bool ok[U];
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-      const int idx = t0 + 4 * lane + c;
-      const int64_t p = kEarlySlots && t0 == s0 ? (int64_t)spn[c]
-                                                : idx < t1 ? (int64_t)sp[idx] : -1;
-      const int64_t dlt = cur - p;
-      live[c] = __ballot(p >= 0 && dlt >= 0 && dlt < C);
+    for (int u = 0; u < U; u++) ok[u] = (live >> (u * G + g)) & 1ull;
+    // the new row joins the batch that covers its slot (its loaded copy of
+    // the slot may predate the store above)
+    if (APPEND && owner && slot_new >= base && slot_new < base + GU) {  // wave-uniform
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        if (base + u * G + g == slot_new) {
+          kr[u] = knew;
+          vr[u] = vnew;
+          ok[u] = true;
+        }
+      }
     }
-    for (int base = t0; base < t1; base += GU) {
-      uint4 kr[U], vr[U];
-      bool ok[U];
+    float sc[U];
+    float mx = m;
 #pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int slot = base + u * G + g;
-        const int i = slot - t0;
-        ok[u] = slot < t1 && ((live[i & 3] >> (i >> 2)) & 1ull);
-        const int sl = slot < t1 ? slot : t0;
-        kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
-        vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
-      }
-      // the new row joins the one batch (of the one tile) that covers its slot:
-      // a batch may reach past the tile end when GU does not divide TILE, and
-      // the slots beyond t1 belong to the next tile
-      if (APPEND && owner && slot_new >= base && slot_new < min(base + GU, t1)) {  // wave-uniform
-        float ko[VD];
+    for (int u = 0; u < U; u++) {
+      float kf[VD];
+      unpack<KV_BF16>(kr[u], kf);
+      float dot = 0.f;
 #pragma unroll
-        for (int j = 0; j < VD / 2; j++)
-          rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
-        const uint4 knew = pack16<KV_BF16>(ko), vnew = pack16<KV_BF16>(vi);
-        if (g == 0) {
-          *(uint4*)((char*)ring_k + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = knew;
-          *(uint4*)((char*)ring_v + (kv_off + (int64_t)slot_new * HD) * (KV_BF16 ? 2 : 4)) = vnew;
-          if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-          if (base + u * G + g == slot_new) {
-            kr[u] = knew;
-            vr[u] = vnew;
-            ok[u] = true;
-          }
-        }
-      }
-      float sc[U];
-      float mx = m;
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        float kf[VD];
-        unpack<KV_BF16>(kr[u], kf);
-        float dot = 0.f;
-#pragma unroll
-        for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
-        dot = group_sum<LR>(dot);
-        sc[u] = ok[u] ? dot : -INFINITY;
-        mx = fmaxf(mx, sc[u]);
-      }
-      if (mx == -INFINITY) continue;  // nothing live yet in this lane group
+      for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
+      dot = group_sum<LR>(dot);
+      sc[u] = ok[u] ? dot : -INFINITY;
+      mx = fmaxf(mx, sc[u]);
+    }
+    if (mx != -INFINITY) {  // else nothing live yet in this lane group
       const float scale = __expf(m - mx);
       l *= scale;
 #pragma unroll
@@ -462,6 +461,7 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
       }
       m = mx;
     }
+    if (base + step < s1) issue(base + step);
   }
 
   // fold the G lane groups: lanes sub, sub+LR, sub+2LR, ... hold the same dims
@@ -501,19 +501,19 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
 }
 
 // Waves per block for a window of up to `max_valid` slots: one wave per
-// `per_wave` slots (180 bf16 with 64-slot batches, 256 fp32 with 48-slot
-// batches) up to 4 waves, and beyond that one wave per 820 slots, at most
-// MAXNW.  Measured on one MI355X with the fused launch (fractions of 8 TB/s,
-// several runs each):
-//   - 64 sequences, C = 2048, mixed windows: bf16 4 waves 0.69-0.71
-//     (12 waves 0.65-0.67, 2-3 waves 0.68-0.71); fp32 4-5 waves 0.73-0.75
-//     (8 waves 0.71-0.72);
-//   - 32 sequences, C = 4096, full windows: bf16 5 waves 0.68-0.70 (16 waves
-//     0.63-0.64, 4 waves 0.60);
-//   - 256 and 64 voices, C = 1024, windows 214-549: bf16 4 waves best (3 waves
-//     within 0.01; 2 waves 0.66 at 256 voices).
-// At 4-5 waves every block of the 64- and 32-sequence steps (768 and 384
-// blocks) is resident at once: the fused kernel holds 16 waves per CU.
+// `per_wave` slots (180 bf16, 256 fp32) up to 4 waves, and beyond that one
+// wave per 820 slots, at most MAXNW.  With alternating batches, measured on
+// one MI355X with the fused launch (fractions of 8 TB/s, same GPU per row):
+//   - 64 sequences, C = 2048, mixed windows, bf16, 4-load batches: 4 waves
+//     0.76, 3 waves 0.72, 2 waves 0.68, 8 waves 0.68;
+//   - 256 voices, C = 1024, windows 215-550, bf16, 8-load batches: 4 waves
+//     0.71, 3 waves 0.70, 6 waves 0.64; 4-load batches 0.69-0.70;
+//   - 32 sequences, C = 4096, full windows, bf16, 4-load batches: 5 waves
+//     0.71, 2 waves 0.46;
+//   - 64 sequences, C = 2048, fp32, 12-load batches: 4 waves 0.78 (8-load
+//     0.77).
+// Windows up to this many slots run the bf16 kernel with 8-load batches.
+constexpr int kAttnShortWindow = 1024;
 static int unit_waves(int64_t max_valid, int per_wave, int maxnw) {
   const int64_t short_rule = std::min<int64_t>(4, (max_valid + per_wave - 1) / per_wave);
   const int64_t long_rule = (max_valid + 819) / 820;
@@ -535,11 +535,17 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
   if (nq * H > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
   const dim3 grid((unsigned)(nq * H));
   if (ring.bf16) {
-    constexpr int U = 8, MAXNW = 16;
+    constexpr int MAXNW = 16;
     const int nw = unit_waves(max_valid, 180, MAXNW);
-    hipLaunchKernelGGL((k_attn_unit<true, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
-                       ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
-                       ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+    // short windows take 8-load batches, longer ones 4-load batches
+    if (max_valid <= kAttnShortWindow)
+      hipLaunchKernelGGL((k_attn_unit<true, 8, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
+                         ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+    else
+      hipLaunchKernelGGL((k_attn_unit<true, 4, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
+                         ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
   } else {
     constexpr int U = 12, MAXNW = 8;
     const int nw = unit_waves(max_valid, 256, MAXNW);
