@@ -368,6 +368,111 @@ def run_copy(nbytes=1 << 31, reps=10):
             "gbs": round(2 * nbytes / (us * 1e-6) / 1e9, 1)}
 
 
+def run_read_ceiling(nbytes=4 << 30, reps=10):
+    """The HBM read ceiling on this GPU, measured two ways: the probe kernel
+    of libmb_probe.so streaming a 4 GiB buffer (16-byte non-temporal loads,
+    each wave reading 256 KB front to back), and torch's sum over the same
+    bytes as fp32.  Both are plain reads of data resident in HBM (4 GiB is 16x
+    the last-level cache)."""
+    import ctypes
+
+    import torch
+
+    import mockbird_amd as mb
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(mb.LIB_PATH), "libmb_probe.so"))
+    lib.mbp_stream_read_bytes.argtypes = [ctypes.c_size_t]
+    lib.mbp_stream_read_bytes.restype = ctypes.c_size_t
+    lib.mbp_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                    ctypes.c_void_p]
+    lib.mbp_stream_read.restype = ctypes.c_int
+    buf = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    read = lib.mbp_stream_read_bytes(nbytes)
+    sink = torch.zeros(read // (256 << 10), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(reps)]
+        for a, b in evs:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return float(np.mean([a.elapsed_time(b) for a, b in evs]) * 1e3)
+
+    def probe():
+        rc = lib.mbp_stream_read(buf.data_ptr(), nbytes, stream.cuda_stream, sink.data_ptr())
+        if rc != 0:
+            raise RuntimeError(f"mbp_stream_read failed ({rc})")
+
+    us_probe = timed(probe)
+    us_sum = timed(lambda: buf.sum())
+    del buf, sink
+    torch.cuda.empty_cache()
+    gp = read / (us_probe * 1e-6) / 1e9
+    gs = nbytes / (us_sum * 1e-6) / 1e9
+    return {"bytes": int(read), "stream_read_us": round(us_probe, 1), "stream_read_gbs": round(gp, 1),
+            "stream_read_frac": round(gp / HBM_PEAK_GBS, 4), "torch_sum_us": round(us_sum, 1),
+            "torch_sum_gbs": round(gs, 1), "torch_sum_frac": round(gs / HBM_PEAK_GBS, 4)}
+
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def run_gemm(reps=60, sets=12):
+    """The QKV (768 -> 2304) and output (768 -> 768) projections through
+    mb_linear_dev (fp32 products and accumulation on MFMA, bias in the
+    epilogue) at the prefill size of the causal-prefill configuration
+    (M = 16 x 512 = 8192 rows) and at the 256-voice decode size (M = 256).
+    `sets` weight copies are used in turn, as a 12-layer model reads a
+    different layer's weights each time."""
+    import torch
+
+    import mockbird_amd as mb
+
+    dev = torch.device("cuda")
+    ctx = mb.Context(n_layers=1, capacity=8, max_seqs=1, max_rows=8, vocab=16)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    out = []
+    for M in (8192, 256):
+        for name, N in (("qkv", QKV), ("o", D)):
+            K = D
+            a = torch.randn((M, K), generator=g, device=dev)
+            ws = [torch.randn((K, N), generator=g, device=dev) * 0.02 for _ in range(sets)]
+            bias = torch.randn(N, generator=g, device=dev) * 0.02
+            c = torch.empty((M, N), device=dev)
+
+            def call(i):
+                ctx.linear_dev(M, N, K, a.data_ptr(), K, ws[i % sets].data_ptr(), bias.data_ptr(),
+                               c.data_ptr(), N, mb.MB_EPI_STORE)
+
+            for i in range(sets):
+                call(i)
+            torch.cuda.synchronize()
+            t0 = torch.cuda.Event(enable_timing=True)
+            t1 = torch.cuda.Event(enable_timing=True)
+            t0.record(stream)
+            for i in range(reps):
+                call(i)
+            t1.record(stream)
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) * 1e3 / reps
+            flops = 2.0 * M * K * N
+            tf = flops / (us * 1e-6) / 1e12
+            out.append({"proj": name, "M": M, "K": K, "N": N, "avg_us": round(us, 2),
+                        "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
+                        "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
+            del a, ws, c
+    ctx.close()
+    return out
+
+
 def frame_prompts(B, seed=33):
     """Voice-clone prompts with total lengths U[64, 400) (half code frames,
     the rest text ids), as the many-voice decode configuration draws them."""
@@ -494,6 +599,63 @@ def cpu_baseline_c1(seconds=12.0):
             "cpu_model": _cpu_model(), "nproc": os.cpu_count()}
 
 
+def cpu_baseline_frames(weights, seconds=8.0):
+    """Greedy decode frames/s of the oracle's fp32 build (liboracle_fp32.so:
+    the same C restatement with fp32 accumulators, -O3 AVX2/FMA, OpenMP) on
+    this host's cores: the stand-in for the reference's CPU path, ORT-wasm
+    running the published graphs, which is not available offline.
+
+    B = 1: the single-stream prompt (281 rows) is prefilled (untimed), then
+    frames -- the 17-step local head with the repetition penalty, then the
+    12-layer decode step of the frame row -- run until `seconds` have passed;
+    the GEMMs split their columns over the threads.  B = 64: one frame for
+    each of 64 voices at a time, the voices spread over the threads (each
+    voice's GEMMs on one thread), on rings filled with 300 positions of
+    placeholder K/V (the timing does not depend on their values)."""
+    from mockbird_amd import synth
+    from oracle import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    m = oracle.Model(weights, n_layers=12, vocab=32000, fp32=True)
+    out = {"unit": "frames/s", "kind": "port", "cores": threads, "cpu_model": _cpu_model(),
+           "nproc": os.cpu_count(),
+           "what": "fp32 CPU restatement of the reference graph (stand-in for ORT-wasm, "
+                   "unavailable offline)"}
+    rows = synth.prompt(0, n_frames=150, n_text=128, vocab=32000)
+    st = oracle.ModelState(m, 1, 1024)
+    h = st.prefill_all(0, rows)[-1][None]
+    pos = rows.shape[0]
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        codes, _, _ = st.local_frame(h)
+        h = st.decode_step(synth.frame_row(codes[0])[None], [pos])
+        pos += 1
+        n += 1
+    dt = time.perf_counter() - t0
+    out["B1"] = {"value": round(n / dt, 2), "sample": f"{n} frames after a 281-row prefill, "
+                 f"{dt:.1f} s, GEMM columns over {threads} threads"}
+    del st
+    B, P = 64, 300
+    st = oracle.ModelState(m, B, 1024, kv_bf16=False)
+    st.K[:] = 0.01
+    st.V[:] = 0.01
+    st.slot_pos[:, :, :P] = np.arange(P, dtype=np.int32)
+    g = np.random.default_rng(3)
+    h = g.standard_normal((B, D), dtype=np.float32)
+    pos = np.full(B, P, np.int32)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 2:
+        codes, _, _ = st.local_frame(h)
+        h = st.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
+        pos = pos + 1
+        n += 1
+    dt = time.perf_counter() - t0
+    out["B64"] = {"value": round(B * n / dt, 2), "sample": f"{n} frames of 64 voices at positions "
+                  f"300+, {dt:.1f} s, voices over {threads} threads"}
+    del st
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -505,8 +667,10 @@ def main():
     ap.add_argument("--kv", default="both", choices=["both", "bf16"])
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-frames", action="store_true")
-    ap.add_argument("--legs", default="copy,c1,voices,c4,c2,codec,frames",
-                    help="comma list of copy (plain 2 GiB HBM copy), c1 (append + decode "
+    ap.add_argument("--legs", default="copy,ceiling,c1,voices,c4,c2,gemm,codec,frames",
+                    help="comma list of copy (plain 2 GiB HBM copy), ceiling (HBM read "
+                         "ceiling: a streaming read probe and torch's sum over 4 GiB), gemm "
+                         "(QKV and O projections at M = 8192 and 256), c1 (append + decode "
                          "attention, 64 sequences, C=2048), voices (the same at 256 voices, "
                          "C=1024), c4 (the same at 32 sequences, C=4096, wrapped), c2 "
                          "(prefill attention), codec (codec decoder frames/s at 64 and 256 "
@@ -526,30 +690,38 @@ def main():
     if args.no_frames:
         legs.discard("frames")
     copy = run_copy() if "copy" in legs else None
+    ceiling = run_read_ceiling() if "ceiling" in legs else None
+    gemm = run_gemm() if "gemm" in legs else None
     voices = run_voices_attention(args) if "voices" in legs else None
     c4 = run_c4(args) if "c4" in legs else None
     codec = ([run_codec(args, 64, "f32"), run_codec(args, 256, "bf16")]
              if "codec" in legs else None)
     c2 = run_c2(args) if "c2" in legs else None
     frames = None
-    if "frames" in legs:
+    w = None
+    if "frames" in legs or not args.no_cpu_baseline:
         from mockbird_amd import synth
 
         # random-init model with the benchmark's shapes; the assistant column of
         # the text head equals the audio_end column, so no voice ever stops
         w = synth.model_weights(n_layers=12, vocab=32000, seed=0)
         w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]
+    if "frames" in legs:
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
         frames = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1])
                   for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
-        print(json.dumps({"hbm_copy": copy, "kv_attention_256_voices": voices,
+        print(json.dumps({"hbm_copy": copy, "hbm_read_ceiling": ceiling, "gemm": gemm,
+                          "kv_attention_256_voices": voices,
                           "kv_attention_c4_wrapped": c4, "prefill_attention": c2,
                           "codec": codec, "frames_detail": frames}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
-    cpu = None if args.no_cpu_baseline else cpu_baseline_c1(args.cpu_seconds)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline_c1(args.cpu_seconds)
+        cpu["frames_per_sec"] = cpu_baseline_frames(w, args.cpu_seconds * 2 / 3)
     line = {
         "metric": METRIC,
         "value": round(bf16["gbs"], 2),
@@ -589,6 +761,8 @@ def main():
             "frac": round(f32["gbs"] / HBM_PEAK_GBS, 4),
             "two_launch_gbs": round(f32["unfused_gbs"], 1)},
         "hbm_copy": copy,
+        "hbm_read_ceiling": ceiling,
+        "gemm": gemm,
         "kv_attention_256_voices": voices,
         "kv_attention_c4_wrapped": c4,
         "prefill_attention": c2,

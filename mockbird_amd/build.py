@@ -22,6 +22,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libmockbird_hip.so")
+PROBE_LIB = os.path.join(PKG, "libmb_probe.so")
 ADDON = os.path.join(PKG, "engine", "mockbird_hip.node")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
@@ -64,6 +65,15 @@ def build_lib(jobs: int = 8) -> str:
     return LIB
 
 
+def build_probe() -> str:
+    """libmb_probe.so: bench.py's HBM read-ceiling kernel (measurement only)."""
+    src = os.path.join(CSRC, "probe", "hbm_read.hip")
+    tmp = PROBE_LIB + ".tmp"
+    _run([HIPCC, *HIP_FLAGS, "-shared", src, "-o", tmp, f"-Wl,-rpath,{ROCM}/lib"])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def build_addon() -> str | None:
     """The N-API addon links libmockbird_hip.so by rpath $ORIGIN/.."""
     src = os.path.join(CSRC, "napi", "mb_napi.cc")
@@ -89,6 +99,7 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     print(build_lib(a.j))
     if not a.lib_only:
+        print(build_probe())
         addon = build_addon()
         if addon:
             print(addon)
