@@ -27,7 +27,6 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int KT = 64;    // slots per K/V tile
 constexpr int QT = 64;    // query rows per workgroup
-constexpr int KPAD = 72;  // bf16 LDS row stride (144 B) to spread banks
 constexpr int FPAD = 68;  // fp32 LDS row stride (272 B)
 
 // Workgroup -> (sequence, head, query tile).  The dispatcher deals
@@ -71,72 +70,129 @@ __device__ __forceinline__ float col_sum(float x) {
   return col_reduce(x, [](float u, float v) { return u + v; });
 }
 
-// Minimum / maximum over the 64 lanes of a wave: DPP within each row of 16
-// (quad swaps, half-row and row mirrors), then the two cross-row swaps.
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int x) {
-  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
-}
-template <bool MAX>
-__device__ __forceinline__ int wave_extreme(int x) {
-  auto op = [](int u, int v) { return MAX ? max(u, v) : min(u, v); };
-  x = op(x, dpp_i<0xB1>(x));   // quad_perm [1,0,3,2]
-  x = op(x, dpp_i<0x4E>(x));   // quad_perm [2,3,0,1]
-  x = op(x, dpp_i<0x141>(x));  // row_half_mirror
-  x = op(x, dpp_i<0x140>(x));  // row_mirror
-  const auto a = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)x, false, false);
-  x = op((int)a[0], (int)a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap((unsigned)x, (unsigned)x, false, false);
-  return op((int)b[0], (int)b[1]);
-}
-
 // ---------------------------------------------------------------- bf16 MMA
 
 // Q bf16 [B][rows_max][768] (roped), K/V bf16 ring, fp32 output.
 //
-// One workgroup = 128 query rows of one (sequence, head); each of its 4 waves
-// owns 32 of them as two 16-query column blocks, so every K or V^T fragment
-// read from LDS feeds two MFMAs.  Both products use v_mfma_f32_16x16x32_bf16:
+// One workgroup = 128 query rows of one (sequence, head).  With 4 waves
+// (the launch's choice) each wave owns 32 of them as two 16-query column
+// blocks, so every K or V^T fragment read from LDS feeds two MFMAs; with 8,
+// one block of 16.  Both products use v_mfma_f32_16x16x32_bf16:
 //  - scores: S^T[16 slots][16 queries] += K[16 slots][32 dims] Q^T[32 dims][16 queries];
 //  - P V:    O^T[16 dims][16 queries] += V^T[16 dims][32 slots] P^T[32 slots][16 queries].
 // For P V, lane l (g = l/16) must hold P^T for 8 slots of one query; the score
 // accumulators give it slots sb*16 + 4g + j (j < 4) of blocks sb = 2c and
 // 2c + 1, and the MFMA's k order is free, so those 8 slots are its k range.
-// V^T is stored in LDS with the slots of each 32-slot chunk c permuted the
-// same way (slot c*32 + h*16 + 4g + j at c*32 + 8g + 4h + j), so each A
-// fragment is one 16-byte LDS read.
 //
-// K/V tiles of 64 slots are double-buffered in LDS and the next tile's global
-// loads are issued before the current tile is computed; one barrier per
-// tile.  Per tile each wave classifies the slots against its 32 queries from
-// the tile's stored-position range: all in the future of every query (the
-// causal upper triangle: skipped), all live for every query (no per-slot
-// test), or mixed (the window rule per slot and query).
+// K/V tiles of 64 slots reach LDS without passing through registers
+// (global_load_lds_dwordx4: lane L of a load lands at the uniform LDS base +
+// 16 L), three buffers deep, two tiles ahead of the one being computed.  Rows
+// are stored in their natural [slot][dim] order with the 16-byte chunks of
+// row s XOR-swizzled by s mod 8, so the 16 rows a fragment read touches
+// spread over the banks.  V^T fragments come from the natural layout through
+// ds_read_b64_tr_b16: within each 16-lane group, lane r points at 4
+// consecutive dims of slot s0 + r/4, and lane i receives dim i of slots
+// s0 .. s0 + 3 -- four k values of the A operand; two such reads make one.
+//
+// Every wave issues the same number of loads per tile (its 1 KB pieces of K
+// and V, and the tile's 64 stored positions, which all waves write alike),
+// with every lane active -- slots past the causal end are clamped to the last
+// one and ignored by the compute -- so `vmcnt` counts tiles exactly.  Per tile
+// each wave classifies the slots against its queries with two ballots: all in
+// the future of every query (the causal upper triangle: skipped), all live
+// for every query (no per-slot test), or mixed (the window rule per slot and
+// query, against relative positions the wave reads back from its own LDS row).
+//
+// Where the time goes (16 sequences x 512 rows, 12 heads, measured by taking
+// parts out of copies of the kernel): the q reads and fp32 output writes
+// alone take 8.8 us, streaming K/V through the buffers with no arithmetic
+// 12.5 us, the whole kernel ~21.5 us; replacing either product's MFMAs with
+// a few adds changes nothing, removing the softmax saves ~3 us.  A wave's
+// tile is a dependent chain (scores -> softmax -> P V) of about 2000 cycles,
+// against about 1100 cycles of issue; software-pipelining the next tile's
+// scores under this tile's softmax needs ~210 registers (2 waves per SIMD)
+// and was slower, as were 8 waves of 16 queries and an order that keeps a
+// sequence's query tiles on one XCD.
 constexpr int BQ = 128;  // query rows per workgroup of the bf16 kernel
+constexpr int kFlashWaves = 4;  // waves per workgroup of the bf16 kernel
+constexpr int NBUF = 3;  // K/V tile buffers
 constexpr float kScoreLog2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
-constexpr int32_t kRelEmpty = 1 << 30;
+constexpr int32_t kRelEmpty = INT32_MAX;  // relative position of an empty slot
 
-__device__ __forceinline__ int vt_col(int slot) {  // slot in a 64-slot tile -> V^T column
-  return (slot & 32) | ((slot & 12) << 1) | ((slot & 16) >> 2) | (slot & 3);
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
+
+// Element offset of (slot row, 8-dim chunk x) in a swizzled 64 x 64 tile.
+__device__ __forceinline__ int swz(int row, int x) { return row * HD + ((x ^ (row & 7)) << 3); }
+
+// s_waitcnt with vmcnt = n (n < 16), expcnt and lgkmcnt left at their maxima
+// (gfx9 encoding)
+#define MB_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
+// global -> LDS loads (global_load_lds_dword / _dwordx4): lane L's bytes land
+// at LDS byte address lds + size * L.  Issued as inline assembly so the
+// compiler does not treat them as LDS writes: it would otherwise wait for
+// every outstanding load (the two tiles in flight) before each LDS read of
+// the tile being computed.  The kernel waits for them itself (MB_WAIT_VMCNT
+// before the barrier that publishes a tile).  Loads the compiler cannot see
+// only make its own vmcnt waits stricter, never looser.  m0 carries the LDS
+// base; the statement saves and restores it, so no register the compiler
+// owns changes under it.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void_t*)p;
+}
+// Each lane reads base + off (base and `lds` wave-uniform, held in SGPRs;
+// off a per-lane byte offset), the scalar-base form of the global load, so a
+// tile's addresses cost no vector instructions: the per-lane offsets are
+// fixed and the base advances with the tile.
+__device__ __forceinline__ uint64_t sgpr_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved) : "v"(off), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+      "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+      : "=&s"(saved) : "v"(off), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
+      : "memory");
 }
 
-__global__ __launch_bounds__(256, 3) void k_flash_bf16(
+template <int NW>
+__global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     const uint16_t* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, const uint16_t* __restrict__ ring_k,
     const uint16_t* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
     int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
-  __shared__ __align__(16) uint16_t Ks[2][KT * KPAD];  // [slot][dim]
-  __shared__ __align__(16) uint16_t Vt[2][HD * KPAD];  // [dim][vt_col(slot)]
-  __shared__ __align__(16) int32_t Ps[2][KT];          // stored position per slot (-1: none)
-  __shared__ int32_t Pr[2][2];           // min and max of the tile's relative positions
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int QB = BQ / (16 * NW);  // 16-query blocks per wave
+  constexpr int WQ = 16 * QB;         // queries per wave
+  constexpr int PIECES = KT / (8 * NW);  // 1 KB pieces of K (and of V) per wave per tile
+  constexpr int LOADS = 2 * PIECES + 1;  // loads per wave per tile
+  static_assert(QB >= 1 && PIECES >= 1, "wave count");
+  __shared__ __align__(16) uint16_t Ks[NBUF][KT * HD];  // [slot][dim], chunks swizzled
+  __shared__ __align__(16) uint16_t Vs[NBUF][KT * HD];  // [slot][dim], chunks swizzled
+  __shared__ __align__(16) int32_t Ps[NBUF][KT];         // stored position per slot
+  __shared__ __align__(16) int32_t Rl[NW][KT];           // per wave: relative positions
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qcol = lane & 15, grp = lane >> 4;
   int b, h, qtile;
   work_item(b, h, qtile);
   const int n = n_rows[b];
   if (qtile * BQ >= n) return;  // uniform per workgroup, before any barrier
   const int64_t p0 = pos0[b];
-  const int rw = qtile * BQ + wave * 32;  // this wave's first query row
+  const int rw = qtile * BQ + wave * WQ;  // this wave's first query row
   const bool wave_rows = rw < n;
   const int rlast = min(qtile * BQ + BQ, n) - 1;
   const int64_t kv_end64 = p0 + rlast + 1;
@@ -145,9 +201,9 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
   // B operands of the score MFMA: Q[row][32*kc + 8*grp + 0..7] as stored; the
   // 1/sqrt(64) scale is applied with log2(e) in the softmax (a power of two,
   // so the scores are the same as from a pre-scaled Q)
-  bf16x8_t qb[2][2];
+  bf16x8_t qb[QB][2];
 #pragma unroll
-  for (int qi = 0; qi < 2; qi++) {
+  for (int qi = 0; qi < QB; qi++) {
     const int r = rw + qi * 16 + qcol;
 #pragma unroll
     for (int kc = 0; kc < 2; kc++) {
@@ -156,148 +212,200 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
       qb[qi][kc] = __builtin_bit_cast(bf16x8_t, raw);
     }
   }
-  // Positions relative to the workgroup's first query, so the window test is
-  // one unsigned compare: slot positions are stored clamped to [-2^30, 2^30)
-  // and an empty slot as 2^30 (after every query); a query at relative
-  // position c sees the slot iff (unsigned)(c - rel) < W, the window (rings
-  // hold at most 2^20 slots, so a clamped position is outside every window,
-  // as it should be).
-  const int64_t base = p0 + (int64_t)qtile * BQ;
-  const int crel_lo = wave * 32, crel_hi = min(rw + 31, n - 1) - qtile * BQ;
-  int crel[2];
+  // Window test in 32 bits.  Stored positions are at most INT32_MAX (the ring
+  // write stores no larger one).  Relative to ref = min(p0 + qtile*BQ,
+  // INT32_MAX), a slot at p has rel = p - ref (an int32) and the query at row
+  // offset c within the workgroup has crel = c + ex, where ex = the part of
+  // the first query's position above INT32_MAX (0 in practice; clamped at 2^30,
+  // beyond every window).  crel - rel is then the true distance cur - p
+  // whenever that is >= 0, exactly, as an unsigned 32-bit number, and a huge
+  // one when p is in the future, so the window rule 0 <= cur - p < W is one
+  // unsigned compare.  An empty slot (or one past the causal end) has rel =
+  // INT32_MAX, which fails it for every query.
+  const int64_t first = p0 + (int64_t)qtile * BQ;
+  const int32_t ref = first < INT32_MAX ? (int32_t)first : INT32_MAX;
+  const int32_t ex = (int32_t)min(first - ref, (int64_t)1 << 30);
+  const int crel_lo = wave * WQ + ex, crel_hi = min(rw + WQ - 1, n - 1) - qtile * BQ + ex;
+  int crel[QB];
 #pragma unroll
-  for (int qi = 0; qi < 2; qi++) crel[qi] = crel_lo + qi * 16 + qcol;
+  for (int qi = 0; qi < QB; qi++) crel[qi] = crel_lo + qi * 16 + qcol;
   const uint16_t* kb = ring_k + (int64_t)b * ring_seq_stride + (int64_t)h * C * HD;
   const uint16_t* vb = ring_v + (int64_t)b * ring_seq_stride + (int64_t)h * C * HD;
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
-  // staging roles: threads 0-127 load V (4 consecutive slots x 8 dims each)
-  // and write it transposed; threads 128-255 load K (4 slots x 8 dims, rows
-  // 16 apart) in its natural layout; wave 0 also loads the slot positions
-  const bool v_role = tid < 128;
-  const int sg = tid & 15, vdc = (tid >> 4) & 7;           // V: slots 4sg.., dims 8vdc..
-  const int kt = tid - 128, ks = (kt >> 3) & 15, kdc = kt & 7;  // K: slots ks + 16i, dims 8kdc..
-  // The prefetch only issues loads; every use of what it loaded (the stash,
-  // and the slot positions' conversion to relative positions) comes after the
-  // next barrier, so the loads stay in flight under a whole tile's MFMAs.
-  uint4 pre[4];
-  int32_t praw = -1;
-  auto fetch = [&](int t0) {
+  // Tile t0 -> buffer bb: wave w loads its KT / NW rows of K and of V as
+  // 1 KB pieces (lane L: row 8 (PIECES w + p) + L/8, LDS chunk L mod 8 =
+  // global chunk (L mod 8) ^ (row mod 8)), and the 64 stored positions (every
+  // wave writes them alike, so each issues the same count of loads).  A whole
+  // tile is read from base + t0 * 64 at fixed per-lane offsets; the last,
+  // partial tile clamps each lane's slot to the last one instead.
+  int prow[PIECES], pchunk[PIECES];
+  uint32_t poff[PIECES];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int slot = t0 + (v_role ? 4 * sg + i : ks + 16 * i);
-      const uint16_t* src = v_role ? vb + (int64_t)slot * HD + vdc * 8 : kb + (int64_t)slot * HD + kdc * 8;
-      pre[i] = slot < kv_end ? *(const uint4*)src : make_uint4(0, 0, 0, 0);
+  for (int piece = 0; piece < PIECES; piece++) {
+    prow[piece] = 8 * (PIECES * wave + piece) + (lane >> 3);
+    pchunk[piece] = (lane & 7) ^ (prow[piece] & 7);
+    poff[piece] = (uint32_t)(prow[piece] * HD + pchunk[piece] * 8) * 2u;
+  }
+  auto issue = [&](int t0, int bb) {
+    if (t0 + KT <= kv_end) {  // uniform
+#pragma unroll
+      for (int piece = 0; piece < PIECES; piece++) {
+        const int loff = 8 * (PIECES * wave + piece) * HD;
+        dma16(kb + (int64_t)t0 * HD, poff[piece], lds_addr(&Ks[bb][loff]));
+        dma16(vb + (int64_t)t0 * HD, poff[piece], lds_addr(&Vs[bb][loff]));
+      }
+      dma4(sp + t0, (uint32_t)lane * 4u, lds_addr(&Ps[bb][0]));
+    } else {
+#pragma unroll
+      for (int piece = 0; piece < PIECES; piece++) {
+        const int loff = 8 * (PIECES * wave + piece) * HD;
+        const int slot = min(t0 + prow[piece], kv_end - 1);
+        const uint32_t off = (uint32_t)(slot * HD + pchunk[piece] * 8) * 2u;
+        dma16(kb, off, lds_addr(&Ks[bb][loff]));
+        dma16(vb, off, lds_addr(&Vs[bb][loff]));
+      }
+      dma4(sp, (uint32_t)min(t0 + lane, kv_end - 1) * 4u, lds_addr(&Ps[bb][0]));
     }
-    if (wave == 0) praw = t0 + lane < kv_end ? sp[t0 + lane] : -1;
   };
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[QB][4], lsum[QB];
+  float m[QB];
 #pragma unroll
-  for (int qi = 0; qi < 2; qi++)
+  for (int qi = 0; qi < QB; qi++) {
 #pragma unroll
     for (int d = 0; d < 4; d++) acc[qi][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  f32x4_t lsum[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
-  float m[2] = {-INFINITY, -INFINITY};
+    lsum[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    m[qi] = -INFINITY;
+  }
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.f;
+  // P V: lane r of each 16-lane group points at dims 16d + 4(r mod 4) .. + 3
+  // of slot 32c + 4 grp + r/4 (and 16 slots later for the second half),
+  // which the transposed read turns into V^T[16d + r][those 4 slots]
+  const int trow = grp * 4 + (qcol >> 2), tdim = (qcol & 3) * 4;
 
-  fetch(0);
-  // Wait here for every load issued so far (q and the first tile): the
-  // compiler cannot tell at the loop head that q's loads are complete, and
-  // would otherwise wait for all loads (the next tile's prefetch included)
-  // before each tile's first MFMA.  s_waitcnt vmcnt(0), expcnt and lgkmcnt
-  // left at their maxima (gfx9 encoding).
-  __builtin_amdgcn_s_waitcnt(0x0F70);
+  // the first tile and q, then every later tile two tiles ahead of its use
+  issue(0, 0);
+  MB_WAIT_VMCNT(0);
   int buf = 0;
-  for (int t0 = 0; t0 < kv_end; t0 += KT, buf ^= 1) {
-    // the buffer written here was last read two tiles ago, before the
-    // previous barrier
-    if (v_role) {
-      const uint32_t* w = (const uint32_t*)pre;  // w[4 j + k]: slot 4sg + j, dims 2k, 2k + 1
-      uint16_t* dst = &Vt[buf][vdc * 8 * KPAD + vt_col(4 * sg)];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        // v_perm_b32 byte selectors: low halves of (a, b) -> b.lo | a.lo << 16,
-        // high halves -> b.hi | a.hi << 16
-        const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-        const int k = i >> 1;
-        *(uint2*)(dst + i * KPAD) = make_uint2(__builtin_amdgcn_perm(w[4 + k], w[k], sel),
-                                               __builtin_amdgcn_perm(w[12 + k], w[8 + k], sel));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) *(uint4*)&Ks[buf][(ks + 16 * i) * KPAD + kdc * 8] = pre[i];
+  for (int t0 = 0; t0 < kv_end; t0 += KT, buf = buf == NBUF - 1 ? 0 : buf + 1) {
+    // this tile's loads are done once at most the next tile's are
+    // outstanding (vmcnt counts in issue order)
+    if (t0 > 0) {
+      if (t0 + KT < kv_end)
+        MB_WAIT_VMCNT(LOADS);
+      else
+        MB_WAIT_VMCNT(0);
     }
-    if (wave == 0) {
-      const int64_t d = (int64_t)praw - base;
-      const int32_t ppre =
-          praw < 0 ? kRelEmpty : (int32_t)(d < -kRelEmpty ? -kRelEmpty : d >= kRelEmpty ? kRelEmpty - 1 : d);
-      Ps[buf][lane] = ppre;
-      const int lo = wave_extreme<false>(ppre);
-      const int hi = wave_extreme<true>(ppre);
-      if (lane == 0) {
-        Pr[buf][0] = lo;
-        Pr[buf][1] = hi;
-      }
-    }
+    // every wave's part of this tile is in LDS, and every wave is done with
+    // the buffer the next issue overwrites (read two tiles ago)
     __syncthreads();
-    if (t0 + KT < kv_end) fetch(t0 + KT);
+    if (t0 == 0 && KT < kv_end) issue(KT, 1);  // uniform per workgroup
+    if (t0 + 2 * KT < kv_end) issue(t0 + 2 * KT, buf == 0 ? NBUF - 1 : buf - 1);
     if (!wave_rows) continue;
-    const int lo = Pr[buf][0], hi = Pr[buf][1];
-    if (lo > crel_hi) continue;  // every stored position is after every query here
-    const bool all_live = hi <= crel_lo && crel_hi - lo < W;
+    // The slot positions, then (with registers to spare: two query blocks
+    // per wave) the K fragments (A of the score MFMA = K[slot sb*16 +
+    // qcol][dims 32 kc + 8 grp ..]), issued before the classification so
+    // their LDS latency runs under it; the empty asm keeps the compiler from
+    // sinking them below the skip branch.
+    const int32_t praw = Ps[buf][lane];
+    auto kfrag = [&](int sb, int kc) {
+      return *(const bf16x8_t*)&Ks[buf][swz(sb * 16 + qcol, kc * 4 + grp)];
+    };
+    bf16x8_t ka[4][2];
+    if constexpr (QB > 1) {
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++) ka[sb][kc] = kfrag(sb, kc);
+      asm volatile("" ::: "memory");
+    }
+    // per slot: after every query of this wave, or live for every one of them
+    // (rel <= crel_lo <= crel_hi makes the unsigned difference exact)
+    const int32_t rel_l = praw < 0 || t0 + lane >= kv_end ? kRelEmpty : praw - ref;
+    if (__ballot(rel_l <= crel_hi) == 0) continue;  // the causal upper triangle
+    const bool all_live =
+        __ballot(!(rel_l <= crel_lo && (uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W)) == 0;
 
     // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
-    f32x4_t s[2][4];
+    f32x4_t s[QB][4];
 #pragma unroll
-    for (int sb = 0; sb < 4; sb++) {
-      s[0][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      s[1][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int sb = 0; sb < 4; sb++)
 #pragma unroll
-      for (int kc = 0; kc < 2; kc++) {
-        const bf16x8_t a = *(const bf16x8_t*)&Ks[buf][(sb * 16 + qcol) * KPAD + kc * 32 + grp * 8];
-        s[0][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[0][kc], s[0][sb], 0, 0, 0);
-        s[1][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[1][kc], s[1][sb], 0, 0, 0);
+      for (int qi = 0; qi < QB; qi++) {
+        s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
+          s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(QB > 1 ? ka[sb][kc] : kfrag(sb, kc),
+                                                              qb[qi][kc], s[qi][sb], 0, 0, 0);
       }
+    // V^T fragments (with registers to spare, now, so their LDS latency runs
+    // under the softmax)
+    auto vfrag = [&](int c, int d) {
+      const int dim = d * 16 + tdim;
+      const int e0 = swz(c * 32 + trow, dim >> 3) + (dim & 7);
+      const int e1 = swz(c * 32 + 16 + trow, dim >> 3) + (dim & 7);
+      const bf16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)&Vs[buf][e0]);
+      const bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)&Vs[buf][e1]);
+      return bf16x8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+    };
+    bf16x8_t va[2][4];
+    if constexpr (QB > 1) {
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int d = 0; d < 4; d++) va[c][d] = vfrag(c, d);
     }
     if (!all_live) {
+      // the wave's own row of relative positions: lane l reads back the four
+      // slots sb*16 + 4*grp + j its score elements stand for
+      Rl[wave][lane] = rel_l;
 #pragma unroll
       for (int sb = 0; sb < 4; sb++) {
-        const int4 pv = *(const int4*)&Ps[buf][sb * 16 + grp * 4];
+        const int4 pv = *(const int4*)&Rl[wave][sb * 16 + grp * 4];
         const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-          for (int qi = 0; qi < 2; qi++)
-            if ((unsigned)(crel[qi] - pj[j]) >= (unsigned)W) s[qi][sb][j] = -INFINITY;
+          for (int qi = 0; qi < QB; qi++)
+            if ((uint32_t)(crel[qi] - pj[j]) >= (uint32_t)W) s[qi][sb][j] = -INFINITY;
       }
     }
     // Online softmax in log2 units.  The running maximum m only moves when a
     // tile's maximum exceeds it by more than 8 (the conditional rescaling of
     // FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
-    // rescale of the accumulators, a wave-uniform branch, is rare after the
-    // first tiles.  The result is the same softmax: acc and the weight sum
-    // always share one m.
-    bf16x8_t pb[2][2];
+    // rescale of the accumulators, a wave-uniform branch taken for all query
+    // blocks at once, is rare after the first tiles.  The result is the same
+    // softmax: acc and the weight sum always share one m.
+    float mt[QB];
+    bool grow[QB], any = false;
 #pragma unroll
-    for (int qi = 0; qi < 2; qi++) {
-      float mt = -INFINITY;
+    for (int qi = 0; qi < QB; qi++) {
+      float x = -INFINITY;
 #pragma unroll
       for (int sb = 0; sb < 4; sb++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) mt = fmaxf(mt, s[qi][sb][j]);
-      mt = col_max(mt) * kScoreLog2;
-      const bool grow = mt > m[qi] + 8.f;
-      if (__ballot(grow)) {
-        const float mn = grow ? mt : m[qi];
-        const float scale = grow ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
+        for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
+      mt[qi] = col_max(x) * kScoreLog2;
+      grow[qi] = mt[qi] > m[qi] + 8.f;
+      any = any || grow[qi];
+    }
+    if (__ballot(any)) {
+#pragma unroll
+      for (int qi = 0; qi < QB; qi++) {
+        const float mn = grow[qi] ? mt[qi] : m[qi];
+        const float scale = grow[qi] ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
         m[qi] = mn;
 #pragma unroll
         for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
         lsum[qi] *= scale;
       }
+    }
+    bf16x8_t pb[QB][2];
+#pragma unroll
+    for (int qi = 0; qi < QB; qi++) {
       const float mu = m[qi] == -INFINITY ? 0.f : m[qi];
 #pragma unroll
       for (int c = 0; c < 2; c++)
@@ -305,23 +413,25 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
         for (int e = 0; e < 8; e++)
           pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, -mu));
     }
-    // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those slots][queries];
-    // the weight sum is one more MFMA with an all-ones A, so it adds the same
-    // rounded weights the products use
+    // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those slots][queries].
+    // The weight sum is one more MFMA with an all-ones A, so it adds the same
+    // rounded weights the products use.
 #pragma unroll
     for (int c = 0; c < 2; c++) {
 #pragma unroll
       for (int d = 0; d < 4; d++) {
-        const bf16x8_t a = *(const bf16x8_t*)&Vt[buf][(d * 16 + qcol) * KPAD + c * 32 + grp * 8];
-        acc[0][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][c], acc[0][d], 0, 0, 0);
-        acc[1][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][c], acc[1][d], 0, 0, 0);
+        const bf16x8_t a = QB > 1 ? va[c][d] : vfrag(c, d);
+#pragma unroll
+        for (int qi = 0; qi < QB; qi++)
+          acc[qi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][c], acc[qi][d], 0, 0, 0);
       }
-      lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0][c], lsum[0], 0, 0, 0);
-      lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1][c], lsum[1], 0, 0, 0);
+#pragma unroll
+      for (int qi = 0; qi < QB; qi++)
+        lsum[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qi][c], lsum[qi], 0, 0, 0);
     }
   }
 #pragma unroll
-  for (int qi = 0; qi < 2; qi++) {
+  for (int qi = 0; qi < QB; qi++) {
     const int r = rw + qi * 16 + qcol;
     if (r >= n) continue;
     const float l = lsum[qi][0];
@@ -333,6 +443,7 @@ __global__ __launch_bounds__(256, 3) void k_flash_bf16(
                                                       acc[qi][d][2] * inv, acc[qi][d][3] * inv);
   }
 }
+#undef MB_WAIT_VMCNT
 
 // ---------------------------------------------------------------- fp32 MMA
 
@@ -768,8 +879,9 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
   const unsigned nh = (unsigned)ring.heads;
   dim3 grid((unsigned)((rows_max + QT - 1) / QT), nh, (unsigned)B);
   if (q_dtype == MB_DT_BF16)
-    hipLaunchKernelGGL(k_flash_bf16, dim3((unsigned)((rows_max + BQ - 1) / BQ), nh, (unsigned)B),
-                       dim3(256), 0, ctx->stream, (const uint16_t*)q, q_rows,
+    hipLaunchKernelGGL(k_flash_bf16<kFlashWaves>,
+                       dim3((unsigned)((rows_max + BQ - 1) / BQ), nh, (unsigned)B),
+                       dim3(64 * kFlashWaves), 0, ctx->stream, (const uint16_t*)q, q_rows,
                        pos0, n_rows, (const uint16_t*)ring.k, (const uint16_t*)ring.v, ring.sp,
                        ring.seq_stride, ring.C, ring.window, out, out_rows);
   else if (ring.bf16)
