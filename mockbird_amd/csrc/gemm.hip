@@ -15,6 +15,7 @@
 // before the current slice's MFMAs.
 #include <type_traits>
 
+#include "kv_types.h"
 #include "mb_internal.h"
 
 namespace mb {
@@ -202,6 +203,27 @@ static void gemm_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const
 constexpr int kStreamMaxM = 1024;
 constexpr int kStreamChunk = 16;  // k rows per wave per pipeline stage
 constexpr int kStreamMaxSplit = 8;
+
+// epilogue4 on operands already in registers: b = bias (or the scale of
+// EPI_SCALE_ADD), has_bias = whether there is one, c = the output's old value
+template <int EPI>
+__device__ __forceinline__ float4 epilogue_regs(float4 v, float4 b, bool has_bias, float4 c) {
+  if (EPI == EPI_SCALE_ADD)
+    return make_float4(c.x + b.x * v.x, c.y + b.y * v.y, c.z + b.z * v.z, c.w + b.w * v.w);
+  if (has_bias) {
+    v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+  }
+  if (EPI == EPI_GELU) {
+    v.x = gelu_tanh(v.x); v.y = gelu_tanh(v.y); v.z = gelu_tanh(v.z); v.w = gelu_tanh(v.w);
+  }
+  if (EPI == EPI_GELU_ERF) {
+    v.x = gelu_erf(v.x); v.y = gelu_erf(v.y); v.z = gelu_erf(v.z); v.w = gelu_erf(v.w);
+  }
+  if (EPI == EPI_ADD) {
+    v.x = c.x + v.x; v.y = c.y + v.y; v.z = c.z + v.z; v.w = c.w + v.w;
+  }
+  return v;
+}
 
 template <int EPI>
 __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ bias, int n,
@@ -509,6 +531,385 @@ static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) 
   }
 }
 
+// ---------------------------------------------------------------------------
+// GEMV-sized M (at most kGemvMaxM rows) on row-major or column-block-major
+// weights (mb_linear_dev, the codec's few-voice projections; the model's
+// decode layers read k-major copies instead, k_gemv_k below).  The product
+// reads each weight once and does a few multiply-adds per weight, so its
+// time is the weight bytes over the bandwidth the launch reaches, which
+// takes many CUs loading at once with every load in flight:
+// the streaming kernel puts N / 64 workgroups on the chip at M = 1 (12 for
+// the O projection) and walks k in dependent pipeline steps.  Here a
+// workgroup owns a strip of SW = 16 columns and all of k, so the grid is
+// N / 16 workgroups of NW waves (4, or 8 for k >= 2048).
+// Lane (c = lane mod CL, q = lane / CL; CL = SW / 4) of wave w owns columns
+// 4c .. 4c + 3 of the strip and, in each block of k, the four rows
+// WR w + 4q .. + 3 (WR = 256 / CL rows per wave per block): four float4
+// loads of W and one float4 of A per row of A.  A lane issues the loads of
+// RB blocks before its first multiply-add (the finishing threads' bias,
+// residual and LayerNorm-fold operands before those); its sums run in k
+// order, then fold over q (lane swaps) and over the waves (LDS, wave order),
+// so every output is the same fixed-order sum on every run.  The strips of
+// a 64-column block are numbered 8 apart, so the dispatcher's round-robin
+// puts them on one XCD and they share the L2 lines (128 bytes = 32 columns)
+// of the weight rows.
+//
+// With LNF the rows are the raw residual stream and the LayerNorm is folded
+// in (Wg, c, d as for the streaming kernel): the workgroup sees every k of
+// its rows, and the lanes of column group 0 add up x - x0 and (x - x0)^2 from
+// the A values they load anyway (x0 = x[m][0], so the variance does not
+// cancel).
+template <int EPI, bool LNF, bool TILED, int MR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemv(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ W, int N, int K,
+    const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
+    const float* __restrict__ lnc, const float* __restrict__ lnd) {
+  constexpr int RB = MR <= 2 ? 6 : MR <= 4 ? 4 : NW == 8 ? 2 : 3;  // k blocks per round of loads
+  constexpr int SW = 16;                             // strip width (columns)
+  constexpr int CL = SW / 4;                         // lanes (float4 column groups) per row
+  constexpr int WR = 256 / CL;                       // rows of k per wave per block
+  constexpr int KB = WR * NW;                        // rows of k per block
+  constexpr int P = 64 / SW;                         // strips per 64-column block
+  __shared__ float4 red[NW][MR][CL];
+  __shared__ float2 rowst[LNF ? NW : 1][MR];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane % CL, q = lane / CL;
+  // strip: the four strips of 64-column block G are workgroups 32 (G / 8) +
+  // 8 s + G mod 8 (s = 0..3); a last group of fewer than 32 strips in order
+  const int L = blockIdx.x, strips = N / SW, full = strips - strips % (8 * P);
+  const int strip = L < full ? ((L / (8 * P)) * 8 + (L & 7)) * P + ((L >> 3) % P) : L;
+  const int n = strip * SW + 4 * c;  // this lane's first column
+  const float* Wp = TILED ? W + (int64_t)(n >> 6) * K * 64 + (n & 63) : W + n;
+  const int64_t wrow = TILED ? 64 : N;
+  // the finishing threads' epilogue operands, loaded under the main loop
+  const bool fin = tid < CL * M;
+  const int om = tid / CL, oc = tid % CL;
+  const int on = strip * SW + 4 * oc;
+  float4 ep_bias = make_float4(0.f, 0.f, 0.f, 0.f), ep_c = ep_bias, ep_cv = ep_bias, ep_dv = ep_bias;
+  float ep_x0 = 0.f;
+  if (fin) {
+    if (bias) ep_bias = *(const float4*)(bias + on);
+    if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = *(const float4*)(Cm + (int64_t)om * ldc + on);
+    if (LNF) {
+      ep_cv = *(const float4*)(lnc + on);
+      ep_dv = *(const float4*)(lnd + on);
+      ep_x0 = A[(int64_t)om * lda];
+    }
+  }
+
+  float acc[MR][4];
+  float s1[MR], s2[MR], x0[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[m][j] = 0.f;
+    s1[m] = s2[m] = 0.f;
+    x0[m] = LNF && m < M ? A[(int64_t)m * lda] : 0.f;
+  }
+  const int nblk = (K + KB - 1) / KB;
+  for (int b0 = 0; b0 < nblk; b0 += RB) {
+    float4 w[RB][4], a[RB][MR];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int k = (b0 + rb) * KB + wave * WR + 4 * q;
+      if (b0 + rb < nblk && k < K) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) w[rb][r] = *(const float4*)(Wp + (int64_t)(k + r) * wrow);
+      }
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int k = (b0 + rb) * KB + wave * WR + 4 * q;
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+        a[rb][m] = b0 + rb < nblk && k < K && m < M ? *(const float4*)(A + (int64_t)m * lda + k)
+                                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int k = (b0 + rb) * KB + wave * WR + 4 * q;
+      if (b0 + rb >= nblk || k >= K) continue;
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        const float av[4] = {a[rb][m].x, a[rb][m].y, a[rb][m].z, a[rb][m].w};
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          acc[m][0] = fmaf(av[r], w[rb][r].x, acc[m][0]);
+          acc[m][1] = fmaf(av[r], w[rb][r].y, acc[m][1]);
+          acc[m][2] = fmaf(av[r], w[rb][r].z, acc[m][2]);
+          acc[m][3] = fmaf(av[r], w[rb][r].w, acc[m][3]);
+          if (LNF) {
+            const float e = av[r] - x0[m];
+            s1[m] += e;
+            s2[m] = fmaf(e, e, s2[m]);
+          }
+        }
+      }
+    }
+  }
+  // fold q (lanes with the same column group c)
+  auto fold = [](float v) {
+#pragma unroll
+    for (int sh = CL; sh < 16; sh <<= 1) v += __shfl_xor(v, sh);
+    return col_sum(v);
+  };
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m >= M) break;
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[m][j] = fold(acc[m][j]);
+    if (LNF) {
+      s1[m] = fold(s1[m]);
+      s2[m] = fold(s2[m]);
+    }
+  }
+  if (q == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      if (m >= M) break;
+      red[wave][m][c] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+      if (LNF && c == 0) rowst[wave][m] = make_float2(s1[m], s2[m]);
+    }
+  }
+  __syncthreads();
+  // thread t < CL M finishes row t / CL, columns 4 (t mod CL) .. + 3 of the strip
+  if (!fin) return;
+  float4 o = red[0][om][oc];
+#pragma unroll
+  for (int w2 = 1; w2 < NW; w2++) {
+    const float4 v = red[w2][om][oc];
+    o.x += v.x; o.y += v.y; o.z += v.z; o.w += v.w;
+  }
+  if (LNF) {
+    const float inv_k = 1.f / (float)K;
+    float t1 = rowst[0][om].x, t2 = rowst[0][om].y;
+#pragma unroll
+    for (int w2 = 1; w2 < NW; w2++) {
+      t1 += rowst[w2][om].x;
+      t2 += rowst[w2][om].y;
+    }
+    const float ms = t1 * inv_k;  // mean of x - x0
+    const float var = fmaxf(t2 * inv_k - ms * ms, 0.f);
+    const float mean = ep_x0 + ms;
+    const float rstd = 1.f / sqrtf(var + 1e-5f);
+    o.x = rstd * (o.x - mean * ep_cv.x) + ep_dv.x;
+    o.y = rstd * (o.y - mean * ep_cv.y) + ep_dv.y;
+    o.z = rstd * (o.z - mean * ep_cv.z) + ep_dv.z;
+    o.w = rstd * (o.w - mean * ep_cv.w) + ep_dv.w;
+  }
+  *(float4*)(Cm + (int64_t)om * ldc + on) = epilogue_regs<EPI>(o, ep_bias, bias != nullptr, ep_c);
+}
+
+template <bool LNF>
+static int gemv_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N,
+                       int K, const float* bias, float* Cm, int64_t ldc, int M, bool tiled,
+                       const float* lnc, const float* lnd) {
+  if (LNF && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
+    return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  // Deep k (fc_out's 3072) runs on 8 waves, so one round of loads covers
+  // more of it.  (8- and 4-column strips, for more workgroups at small N,
+  // were slower on every decode shape but 768 x 3072: their 32- and 16-byte
+  // row pieces read HBM less efficiently.)
+  const dim3 grid((unsigned)(N / 16));
+  const bool deep = K >= 2048;
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    auto go = [&](auto mr) {
+      constexpr int MRv = decltype(mr)::value;
+      auto launch = [&](auto nw) {
+        constexpr int NWv = decltype(nw)::value;
+        if constexpr (LNF) {
+          if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
+            hipLaunchKernelGGL((k_gemv<E, true, true, MRv, NWv>), grid, dim3(64 * NWv), 0,
+                               ctx->stream, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd);
+        } else if (tiled) {
+          hipLaunchKernelGGL((k_gemv<E, false, true, MRv, NWv>), grid, dim3(64 * NWv), 0,
+                             ctx->stream, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd);
+        } else {
+          hipLaunchKernelGGL((k_gemv<E, false, false, MRv, NWv>), grid, dim3(64 * NWv), 0,
+                             ctx->stream, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd);
+        }
+      };
+      if (deep) launch(std::integral_constant<int, 8>{});
+      else launch(std::integral_constant<int, 4>{});
+    };
+    if (M <= 1) go(std::integral_constant<int, 1>{});
+    else if (M <= 2) go(std::integral_constant<int, 2>{});
+    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+  });
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV on k-major weights: Wk[n][k] = W[k][n] (launch_kmajor_w), for the
+// model's decode-sized projections, which keep such a copy.  A column's
+// weights are then one contiguous run of K floats, so wave w of workgroup g
+// computes column n = 4g + w alone: lane l reads the float4s at k = 4l +
+// 256i (a wave reads 1 KB contiguous per load) and the matching float4 of
+// every A row, all issued before the first multiply-add, and the wave folds
+// its 64 lanes (lane swaps) -- no LDS, no barrier.  With LNF the wave also
+// sums x - x0 and (x - x0)^2 over the rows it loads (x0 = x[m][0]) and
+// applies the folded LayerNorm itself.  The grid is N / 4 workgroups (192
+// for 768 outputs, 768 for 3072), and every output is a fixed-order sum.
+template <int EPI, bool LNF, int MR>
+__global__ __launch_bounds__(256) void k_gemv_k(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ Wk, int N, int K,
+    const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
+    const float* __restrict__ lnc, const float* __restrict__ lnd) {
+  constexpr int RI = MR <= 2 ? 12 : MR <= 4 ? 6 : 3;  // k steps (256 rows each) per round of loads
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + wave;
+  const float* wp = Wk + (int64_t)n * K + 4 * lane;
+  // lane m < M finishes row m: its epilogue operands, loaded under the main loop
+  float ep_b = 0.f, ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
+  if (lane < M) {
+    if (bias) ep_b = bias[n];
+    if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)lane * ldc + n];
+    if (LNF) {
+      ep_cv = lnc[n];
+      ep_dv = lnd[n];
+    }
+  }
+  float acc[MR], s1[MR], s2[MR], x0[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    acc[m] = s1[m] = s2[m] = 0.f;
+    x0[m] = LNF && m < M ? A[(int64_t)m * lda] : 0.f;
+  }
+  const int steps = (K + 255) >> 8;
+  for (int i0 = 0; i0 < steps; i0 += RI) {
+    float4 w[RI], a[RI][MR];
+#pragma unroll
+    for (int i = 0; i < RI; i++) {
+      const int k = (i0 + i) * 256 + 4 * lane;
+      if (i0 + i < steps && k < K) w[i] = *(const float4*)(wp + (int64_t)(i0 + i) * 256);
+    }
+#pragma unroll
+    for (int i = 0; i < RI; i++) {
+      const int k = (i0 + i) * 256 + 4 * lane;
+#pragma unroll
+      for (int m = 0; m < MR; m++)
+        a[i][m] = i0 + i < steps && k < K && m < M ? *(const float4*)(A + (int64_t)m * lda + k)
+                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < RI; i++) {
+      if (i0 + i >= steps || (i0 + i) * 256 + 4 * lane >= K) continue;
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        acc[m] = fmaf(a[i][m].x, w[i].x, acc[m]);
+        acc[m] = fmaf(a[i][m].y, w[i].y, acc[m]);
+        acc[m] = fmaf(a[i][m].z, w[i].z, acc[m]);
+        acc[m] = fmaf(a[i][m].w, w[i].w, acc[m]);
+        if (LNF) {
+          const float e[4] = {a[i][m].x - x0[m], a[i][m].y - x0[m], a[i][m].z - x0[m],
+                              a[i][m].w - x0[m]};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            s1[m] += e[j];
+            s2[m] = fmaf(e[j], e[j], s2[m]);
+          }
+        }
+      }
+    }
+  }
+  auto fold = [](float v) {
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) v += __shfl_xor(v, sh);
+    return col_sum(v);
+  };
+  float mine = 0.f, m1 = 0.f, m2 = 0.f, mx0 = 0.f;
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m >= M) break;
+    const float t = fold(acc[m]);
+    if (lane == m) mine = t;
+    if (LNF) {
+      const float u1 = fold(s1[m]), u2 = fold(s2[m]);
+      if (lane == m) {
+        m1 = u1;
+        m2 = u2;
+        mx0 = x0[m];
+      }
+    }
+  }
+  if (lane >= M) return;
+  float o = mine;
+  if (LNF) {
+    const float inv_k = 1.f / (float)K;
+    const float ms = m1 * inv_k;  // mean of x - x0
+    const float var = fmaxf(m2 * inv_k - ms * ms, 0.f);
+    const float rstd = 1.f / sqrtf(var + 1e-5f);
+    o = rstd * (o - (mx0 + ms) * ep_cv) + ep_dv;
+  }
+  if (EPI == EPI_SCALE_ADD) {
+    o = ep_c + ep_b * o;
+  } else {
+    if (bias) o += ep_b;
+    if (EPI == EPI_GELU) o = gelu_tanh(o);
+    if (EPI == EPI_GELU_ERF) o = gelu_erf(o);
+    if (EPI == EPI_ADD) o = ep_c + o;
+  }
+  Cm[(int64_t)lane * ldc + n] = o;
+}
+
+int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* Wk, int N, int K,
+                  const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                  const float* lnd) {
+  if (M <= 0) return MB_OK;
+  const bool lnf = lnc != nullptr;
+  if (M > kGemvMaxM || N % 4 || K % 4 || lda % 4 || ((uintptr_t)A & 15) || ((uintptr_t)Wk & 15) ||
+      (lnf && !lnd))
+    return fail(ctx, MB_ERR_ARG, "k-major gemv shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  if (lnf && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
+    return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  const dim3 grid((unsigned)(N / 4));
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    auto go = [&](auto mr) {
+      constexpr int MRv = decltype(mr)::value;
+      if (lnf) {
+        if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
+          hipLaunchKernelGGL((k_gemv_k<E, true, MRv>), grid, dim3(256), 0, ctx->stream, A, lda, Wk,
+                             N, K, bias, Cm, ldc, M, lnc, lnd);
+      } else {
+        hipLaunchKernelGGL((k_gemv_k<E, false, MRv>), grid, dim3(256), 0, ctx->stream, A, lda, Wk,
+                           N, K, bias, Cm, ldc, M, lnc, lnd);
+      }
+    };
+    if (M <= 1) go(std::integral_constant<int, 1>{});
+    else if (M <= 2) go(std::integral_constant<int, 2>{});
+    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+  });
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// Wk[n][k] = gamma[k] * W[k][n] (W [K][N] row-major; gamma null: 1), one
+// thread per output element, rounded as k_fold_ln rounds its product, so a
+// folded k-major copy holds the same values as the folded tiled one.
+__global__ __launch_bounds__(256) void k_kmajor_w(const float* __restrict__ W, int K, int N,
+                                                  const float* __restrict__ gamma,
+                                                  float* __restrict__ Wk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)K * N) return;
+  const int k = (int)(i % K);
+  const int64_t n = i / K;
+  const float w = W[(int64_t)k * N + n];
+  Wk[i] = gamma ? __fmul_rn(gamma[k], w) : w;
+}
+
+int launch_kmajor_w(mb_ctx* ctx, const float* W, int K, int N, const float* gamma, float* Wk) {
+  const int64_t n = (int64_t)K * N;
+  hipLaunchKernelGGL(k_kmajor_w, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, W,
+                     K, N, gamma, Wk);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
 // W' = diag(gamma) W, c = column sums of W', d = beta W: the folded form of
 // "LayerNorm, then x W" used by the LNF streaming kernel.  One thread per
 // column; c and d are summed in double in k order and rounded once.  W' is
@@ -585,6 +986,7 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
   if (K % 64 || N % 64 || ldx % 4 || ldc % 4 || ((uintptr_t)x & 15) || ((uintptr_t)Wg & 15) ||
       ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) || ((uintptr_t)c & 15) || ((uintptr_t)d & 15))
     return fail(ctx, MB_ERR_ARG, "folded gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  if (M <= kGemvMaxM) return gemv_launch<true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, true, c, d);
   int mt, S;
   stream_shape(M, N, K, true, mt, S);
   switch (mt) {
@@ -595,7 +997,8 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
   }
 }
 
-// M < kStreamMaxM, or few enough 64-row tiles: the streaming kernel.  Its
+// At most kGemvMaxM rows: the GEMV kernel.  M < kStreamMaxM, or few enough
+// 64-row tiles: the streaming kernel.  Its
 // row tile is the smallest of
 // 16 / 32 / 48 / 64 rows that keeps the grid at most one workgroup per CU
 // (256 CUs), so the projection runs as one round; K = 3072 projections with
@@ -609,6 +1012,7 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // chip (256 CUs) a block per CU (128 x 128 only from K = 512 up), else the
 // smallest tile.
 size_t gemm_partial_floats(int M, int N, int K) {
+  if (M <= kGemvMaxM) return 0;
   if (M <= 0 || !gemm_streams(M, N)) return 0;
   int mt, S;
   stream_shape(M, N, K, false, mt, S);
@@ -624,6 +1028,8 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
   if (N % 64 || K % 64 || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
       ((uintptr_t)W & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15))
     return fail(ctx, MB_ERR_ARG, "gemm shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  if (M <= kGemvMaxM)
+    return gemv_launch<false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, w_tiled, nullptr, nullptr);
   if (gemm_streams(M, N)) {
     int mt, S;
     stream_shape(M, N, K, false, mt, S);

@@ -1,6 +1,6 @@
 // Element conversions and 16-byte vector load/store helpers for fp32 and bf16
-// rows.  bf16 is stored as the upper 16 bits of an fp32 pattern; the store
-// rounds to nearest, ties to even.
+// rows (bf16 is stored as the upper 16 bits of an fp32 pattern; the store
+// rounds to nearest, ties to even), and cross-lane folds.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -69,6 +69,25 @@ __device__ __forceinline__ void store8(void* base, int64_t off, const float* in)
     *(float4*)p = make_float4(in[0], in[1], in[2], in[3]);
     *(float4*)(p + 4) = make_float4(in[4], in[5], in[6], in[7]);
   }
+}
+
+// Reduce over the four lane groups that share a column (lanes i, i^16,
+// i^32, i^48) with the gfx950 cross-row swaps: v_permlane32_swap pairs lane
+// i with i^32 and v_permlane16_swap pairs i with i^16, both without an LDS
+// round trip.  Each step combines the two values of a pair in the same order
+// on both lanes, so all four lanes end with bit-identical results.
+template <class Op>
+__device__ __forceinline__ float col_reduce(float x, Op op) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float col_max(float x) {
+  return col_reduce(x, [](float u, float v) { return fmaxf(u, v); });
+}
+__device__ __forceinline__ float col_sum(float x) {
+  return col_reduce(x, [](float u, float v) { return u + v; });
 }
 
 }  // namespace mb

@@ -71,12 +71,14 @@ struct AudioTables {
 // plus the LayerNorm-folded forms of the two projections that follow a
 // LayerNorm (W' = diag(gamma) W, c = column sums of W', d = beta W; W'
 // column-block-major) and column-block-major copies of the other two, which
-// the streaming kernel reads at decode sizes.
+// the streaming kernel reads at decode sizes, and k-major copies of all four
+// (the folded ones folded), which the GEMV kernel reads at up to kGemvMaxM rows.
 struct LayerW {
   const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
   const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
   const float *attn_wg, *attn_c, *attn_d, *fc_in_wg, *fc_in_c, *fc_in_d;
   const float *proj_wt, *fc_out_wt;
+  const float *attn_wk, *fc_in_wk, *proj_wk, *fc_out_wk;
 };
 
 // Every weight a model call needs, resolved from the uploaded tensors.
@@ -87,8 +89,8 @@ struct ModelW {
   LayerW local;
   const float *local_lnf_w, *local_lnf_b, *text_head;
   AudioTables audio_heads;
-  // the audio heads with the local ln_f folded in
-  AudioTables head_wg, head_c, head_d;
+  // the audio heads with the local ln_f folded in (column-block-major and k-major)
+  AudioTables head_wg, head_c, head_d, head_wk;
 };
 
 // Projections with fewer rows than this run with their LayerNorm folded in.
@@ -277,7 +279,9 @@ enum { EPI_STORE = 0, EPI_GELU = 1, EPI_ADD = 2, EPI_SCALE_ADD = 3, EPI_GELU_ERF
 // MB_ERR_STATE).
 // `part` (optional, part_cap floats) takes the streaming kernel's split-K
 // partials in place of the context's growable scratch; a split that needs
-// more is MB_ERR_ARG.
+// more is MB_ERR_ARG.  M <= kGemvMaxM rows take the GEMV kernel, which needs
+// no scratch.
+constexpr int kGemvMaxM = 8;
 int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* W, int N, int K,
                 const float* bias, float* Cm, int64_t ldc, int M, bool w_tiled = false,
                 float* part = nullptr, size_t part_cap = 0);
@@ -288,6 +292,15 @@ size_t gemm_partial_floats(int M, int N, int K);
 // context's (current) device, once per device.
 int noalloc_init(mb_ctx* ctx);
 int launch_tile_w(mb_ctx* ctx, const float* W, int K, int N, float* Wt);
+// Wk[n][k] = gamma[k] W[k][n] (gamma null: 1), the k-major copy launch_gemv_k
+// reads; with gamma it holds the values launch_fold_ln's Wg holds.
+int launch_kmajor_w(mb_ctx* ctx, const float* W, int K, int N, const float* gamma, float* Wk);
+// C = epi(A Wk^T + bias) for M <= kGemvMaxM rows on a k-major weight copy;
+// with lnc (and lnd) the rows are the raw residual stream and the LayerNorm
+// is folded in (c, d from launch_fold_ln, Wk from launch_kmajor_w with gamma).
+int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* Wk, int N, int K,
+                  const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                  const float* lnd);
 
 // LayerNorm folded into the projection after it: Wg, c, d from
 // launch_fold_ln (Wg column-block-major, as launch_tile_w writes it);

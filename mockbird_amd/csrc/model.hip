@@ -54,12 +54,26 @@ int tile(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, con
   return launch_tile_w(ctx, W, K, N, p);
 }
 
+// A k-major copy Wk[n][k] = gamma[k] W[k][n] of the [K][N] projection W
+// (launch_kmajor_w; gamma null: the plain transpose).
+int kmajor(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, const float* gamma,
+           const float*& wk) {
+  float* p = internal_tensor(ctx, name, (int64_t)K * N);
+  if (!p) return fail(ctx, MB_ERR_NOMEM, "k-major weight allocation failed (%s)", name.c_str());
+  wk = p;
+  return launch_kmajor_w(ctx, W, K, N, gamma, p);
+}
+
 int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
   int rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
                 w.attn_d);
   if (rc) return rc;
   if ((rc = tile(ctx, key + ".proj.t", w.proj_w, D, D, w.proj_wt))) return rc;
   if ((rc = tile(ctx, key + ".fc_out.t", w.fc_out_w, FFN, D, w.fc_out_wt))) return rc;
+  if ((rc = kmajor(ctx, key + ".attn.k", w.attn_w, D, QKV, w.ln1_w, w.attn_wk))) return rc;
+  if ((rc = kmajor(ctx, key + ".fc_in.k", w.fc_in_w, D, FFN, w.ln2_w, w.fc_in_wk))) return rc;
+  if ((rc = kmajor(ctx, key + ".proj.k", w.proj_w, D, D, nullptr, w.proj_wk))) return rc;
+  if ((rc = kmajor(ctx, key + ".fc_out.k", w.fc_out_w, FFN, D, nullptr, w.fc_out_wk))) return rc;
   return fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
               w.fc_in_d);
 }
@@ -103,7 +117,8 @@ int resolve(mb_ctx* ctx, bool global, bool local) {
     for (int k = 0; k < NVQ; k++) {
       const std::string p = "#fold/head" + std::to_string(k);
       if ((rc = fold(ctx, p, m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.local_lnf_b,
-                     m.head_wg.t[k], m.head_c.t[k], m.head_d.t[k])))
+                     m.head_wg.t[k], m.head_c.t[k], m.head_d.t[k])) ||
+          (rc = kmajor(ctx, p + ".k", m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.head_wk.t[k])))
         return rc;
     }
     ctx->model_ok = true;
@@ -145,9 +160,15 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
               const int32_t* pos0, const int32_t* n_rows, const int32_t* row_off, bool prefill,
               int64_t max_valid, Act& a) {
   int rc;
-  // decode-sized M: each LayerNorm is folded into the projection after it
+  // decode-sized M: each LayerNorm is folded into the projection after it;
+  // up to kGemvMaxM rows the projections read the k-major copies
   const bool folded = M < kFoldMaxM;
-  if (folded) {
+  const bool gemv = M <= kGemvMaxM;
+  if (gemv) {
+    if ((rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
+                            (int)M, w.attn_c, w.attn_d)))
+      return rc;
+  } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, w.attn_wg, QKV, D, w.attn_c, w.attn_d,
                              w.attn_b, a.qkv, QKV, (int)M)))
       return rc;
@@ -180,10 +201,16 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   if (rc) return rc;
   // decode sizes read the column-block-major copies of O and fc_out
   const bool tiled = gemm_streams((int)M, D);
-  if ((rc = launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b, a.x,
-                        D, (int)M, tiled)))
+  if ((rc = gemv ? launch_gemv_k(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
+                                 nullptr, nullptr)
+                 : launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b,
+                               a.x, D, (int)M, tiled)))
     return rc;
-  if (folded) {
+  if (gemv) {
+    if ((rc = launch_gemv_k(ctx, EPI_GELU, a.x, D, w.fc_in_wk, FFN, D, w.fc_in_b, a.ffn, FFN,
+                            (int)M, w.fc_in_c, w.fc_in_d)))
+      return rc;
+  } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_GELU, a.x, D, w.fc_in_wg, FFN, D, w.fc_in_c, w.fc_in_d,
                              w.fc_in_b, a.ffn, FFN, (int)M)))
       return rc;
@@ -192,6 +219,9 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
     if ((rc = launch_gemm(ctx, EPI_GELU, a.norm, D, w.fc_in_w, FFN, D, w.fc_in_b, a.ffn, FFN, (int)M)))
       return rc;
   }
+  if (gemv)
+    return launch_gemv_k(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wk, D, FFN, w.fc_out_b, a.x, D, (int)M,
+                         nullptr, nullptr);
   return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, tiled ? w.fc_out_wt : w.fc_out_w, D, FFN, w.fc_out_b,
                      a.x, D, (int)M, tiled);
 }
@@ -323,7 +353,10 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
       const int ch = step - 1;
       float* lg = pick ? a.logits : probe->logits + (int64_t)ch * CODES;
       const int64_t ldl = pick ? CODES : (int64_t)NVQ * CODES;
-      if (folded_head)
+      if (folded_head && B <= kGemvMaxM)
+        rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, m.head_wk.t[ch], CODES, D, nullptr, lg, ldl, B,
+                           m.head_c.t[ch], m.head_d.t[ch]);
+      else if (folded_head)
         rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, m.head_wg.t[ch], CODES, D, m.head_c.t[ch],
                             m.head_d.t[ch], nullptr, lg, ldl, B);
       else

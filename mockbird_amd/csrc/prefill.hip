@@ -51,24 +51,6 @@ __device__ __forceinline__ bool live_slot(int32_t p, int64_t cur, int C) {
   return p >= 0 && d >= 0 && d < C;
 }
 
-// Reduce over the four lane groups that share a query column (lanes i, i^16,
-// i^32, i^48) with the gfx950 cross-row swaps: v_permlane32_swap pairs lane
-// i with i^32 and v_permlane16_swap pairs i with i^16, both without an LDS
-// round trip.  Each step combines the two values of a pair in the same order
-// on both lanes, so all four lanes end with bit-identical results.
-template <class Op>
-__device__ __forceinline__ float col_reduce(float x, Op op) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  x = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float col_max(float x) {
-  return col_reduce(x, [](float u, float v) { return fmaxf(u, v); });
-}
-__device__ __forceinline__ float col_sum(float x) {
-  return col_reduce(x, [](float u, float v) { return u + v; });
-}
 
 // ---------------------------------------------------------------- bf16 MMA
 

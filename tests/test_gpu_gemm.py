@@ -138,3 +138,33 @@ def test_linear_scale_add_needs_the_scale(ctx):
     with pytest.raises(mb.MbError) as e:
         ctx.linear_dev(4, 256, 256, 16, 256, 16, None, 16, 256, mb.MB_EPI_SCALE_ADD)
     assert e.value.code == mb.MB_ERR_ARG
+
+
+def test_gemv_rows_1_to_8(ctx):
+    """Up to 8 rows take the GEMV kernel: 16-column strips over all of k, the
+    four strips of a 64-column block numbered 8 apart, a last group of fewer
+    than 32 strips in order.  Every row count 1..8 at shapes from one
+    64-column block (N = 64) to 144 strips (2304) and 3072-deep k, each call
+    made twice: both within 1e-4 of the oracle and bit-identical."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    for N, K in ((64, 64), (128, 768), (2304, 768), (768, 3072), (1024, 192)):
+        say(f"gemv N={N} K={K} M=1..8")
+        g = np.random.default_rng([N, K, 11])
+        W = g.standard_normal((K, N), dtype=np.float32) * np.float32(0.05)
+        bias = g.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+        tW, tb = torch.from_numpy(W).to(dev), torch.from_numpy(bias).to(dev)
+        for M in range(1, 9):
+            A = g.standard_normal((M, K), dtype=np.float32)
+            tA = torch.from_numpy(A).to(dev)
+            want = oracle.gemm(A, W, bias)
+            outs = []
+            for _ in range(2):
+                tC = torch.full((M, N), 7.0, device=dev)
+                ctx.linear_dev(M, N, K, tA.data_ptr(), K, tW.data_ptr(), tb.data_ptr(), tC.data_ptr(), N)
+                torch.cuda.synchronize()
+                outs.append(tC.cpu().numpy())
+            assert np.array_equal(outs[0], outs[1]), (M, N, K)
+            err = float(np.abs(outs[0] - want).max())
+            assert err < 1e-4, (M, N, K, err)
