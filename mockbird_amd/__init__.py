@@ -33,7 +33,7 @@ EXPORTS = (
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_local_logits", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
-    "mb_linear_dev", "mb_linear_noalloc_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
+    "mb_linear_dev", "mb_split_weights_dev", "mb_linear_split_dev", "mb_linear_noalloc_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
     "mb_append_attend_dev", "mb_codec_init", "mb_codec_reset", "mb_codec_decode",
     "mb_codec_decode_dev", "mb_codec_read_ring",
 )
@@ -120,6 +120,9 @@ def load():
                            C.c_int64, C.c_int], C.c_int),
         "mb_linear_noalloc_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int64, _vp, _vp, _vp,
                                    C.c_int64, C.c_int], C.c_int),
+        "mb_split_weights_dev": ([_vp, _vp, C.c_int, C.c_int, _vp], C.c_int),
+        "mb_linear_split_dev": ([_vp, C.c_int, C.c_int, C.c_int, _vp, C.c_int64, _vp, _vp, _vp,
+                                 C.c_int64, C.c_int], C.c_int),
         "mb_decode_frames_dev": ([_vp, C.c_int, C.c_int, _vp, _vp, _i32, _vp, _vp], C.c_int),
         "mb_decode_frames": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
         "mb_append_attend": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
@@ -356,6 +359,13 @@ class Context:
     def linear_dev(self, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc, epi=0):
         self.check(self.lib.mb_linear_dev(self.h, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc,
                                           epi))
+
+    def split_weights_dev(self, w_ptr, K, N, wx_ptr):
+        self.check(self.lib.mb_split_weights_dev(self.h, w_ptr, K, N, wx_ptr))
+
+    def linear_split_dev(self, M, N, K, a_ptr, lda, wx_ptr, bias_ptr, c_ptr, ldc, epi=0):
+        self.check(self.lib.mb_linear_split_dev(self.h, M, N, K, a_ptr, lda, wx_ptr, bias_ptr,
+                                                c_ptr, ldc, epi))
 
     def linear_noalloc_dev(self, M, N, K, a_ptr, lda, w_ptr, bias_ptr, c_ptr, ldc, epi=0):
         self.check(self.lib.mb_linear_noalloc_dev(self.h, M, N, K, a_ptr, lda, w_ptr, bias_ptr,

@@ -21,6 +21,7 @@
 namespace mb {
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int GBK = 16;   // K slice
 constexpr int GPAD = 20;  // LDS row stride in floats (16 + 4)
@@ -249,7 +250,102 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
   return v;
 }
 
-//
+// The end of a streaming tile, shared by k_gemm_stream and k_gemm_x3: the
+// four waves' partial sums of an MT x 64 tile (acc[i][j][e] = row 16i + 4r +
+// e, column n + j of the wave's k range) are added in wave order and the
+// tile is stored (S == 1: epilogue; S > 1: this split's partial).  With LNF,
+// sx / sxx / x0 are the lane's sums of x - x0 and (x - x0)^2 over the A
+// values it streamed (rows 16i + l16, k group r of every k step) and K is
+// the row width.
+template <int MI, int EPI, bool LNF>
+__device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)[MI],
+                                              float (&sxx)[MI], const float (&x0)[MI], int K,
+                                              const float* __restrict__ bias,
+                                              float* __restrict__ Cm, int64_t ldc, int M,
+                                              int N, float* __restrict__ part,
+                                              const float* __restrict__ lnc,
+                                              const float* __restrict__ lnd) {
+  __shared__ float red[4][2][4][4][64];  // [wave][block][column block][element][lane]
+  __shared__ float4 stat[LNF ? 4 : 1][MI][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, r = lane >> 4;
+  const int n = blockIdx.x * 64 + 4 * l16;
+  const int m0 = blockIdx.y * (16 * MI);
+  const int S = gridDim.z, split = blockIdx.z;
+  if (LNF) {
+    // a row's four k groups sit in lanes l16 + 16r: fold them, then lanes
+    // r = 0 publish the wave's quarter of the row sums
+#pragma unroll
+    for (int i = 0; i < MI; i++) {
+      sx[i] += __shfl_xor(sx[i], 16);
+      sx[i] += __shfl_xor(sx[i], 32);
+      sxx[i] += __shfl_xor(sxx[i], 16);
+      sxx[i] += __shfl_xor(sxx[i], 32);
+      if (lane < 16) stat[wave][i][lane] = make_float4(sx[i], sxx[i], x0[i], 0.f);
+    }
+  }
+
+  // Add the four waves' sums and finish the tile on all four waves: the
+  // partial tiles go through LDS two 16-row blocks at a time, and wave w
+  // takes element w of every accumulator -- row 16i + 4r + w, columns
+  // n .. n+3 -- summing the waves in wave order (the same order on every run).
+  const float inv_k = 1.f / (float)K;
+  float4 cv = make_float4(0.f, 0.f, 0.f, 0.f), dv = cv;
+  if (LNF) {
+    cv = *(const float4*)(lnc + n);
+    dv = *(const float4*)(lnd + n);
+  }
+#pragma unroll
+  for (int i0 = 0; i0 < MI; i0 += 2) {
+    if (i0 > 0) __syncthreads();  // the previous group's reads are done
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++) {
+      if (i0 + ii >= MI) break;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) red[wave][ii][j][e][lane] = acc[i0 + ii][j][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++) {
+      const int i = i0 + ii;
+      if (i >= MI) break;
+      float o[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float t = red[0][ii][j][wave][lane];
+        t += red[1][ii][j][wave][lane];
+        t += red[2][ii][j][wave][lane];
+        t += red[3][ii][j][wave][lane];
+        o[j] = t;
+      }
+      const int rl = 4 * r + wave;
+      const int row = m0 + 16 * i + rl;
+      if (LNF) {
+        const float4 q0 = stat[0][i][rl], q1 = stat[1][i][rl], q2 = stat[2][i][rl], q3 = stat[3][i][rl];
+        const float s1 = ((q0.x + q1.x) + q2.x) + q3.x;
+        const float s2 = ((q0.y + q1.y) + q2.y) + q3.y;
+        const float ms = s1 * inv_k;  // mean of x - x0
+        const float var = fmaxf(s2 * inv_k - ms * ms, 0.f);
+        const float mean = q0.z + ms;
+        const float rstd = 1.f / sqrtf(var + 1e-5f);
+        o[0] = rstd * (o[0] - mean * cv.x) + dv.x;
+        o[1] = rstd * (o[1] - mean * cv.y) + dv.y;
+        o[2] = rstd * (o[2] - mean * cv.z) + dv.z;
+        o[3] = rstd * (o[3] - mean * cv.w) + dv.w;
+      }
+      if (row >= M) continue;
+      if (S > 1) {
+        *(float4*)(part + ((int64_t)split * M + row) * N + n) = make_float4(o[0], o[1], o[2], o[3]);
+        continue;
+      }
+      float* cp = Cm + (int64_t)row * ldc + n;
+      *(float4*)cp = epilogue4<EPI>(make_float4(o[0], o[1], o[2], o[3]), bias, n, cp);
+    }
+  }
+}
+
 // With LNF the A rows are the raw residual stream x and the LayerNorm in
 // front of the projection is folded in: W holds diag(gamma) * W, and
 //   LN(x) W = rstd (x W' - mean c) + d,   c = 1 W',  d = beta W
@@ -263,8 +359,6 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd) {
   constexpr int MI = MT / 16;
-  __shared__ float red[4][2][4][4][64];  // [wave][block][column block][element][lane]
-  __shared__ float4 stat[LNF ? 4 : 1][MI][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, r = lane >> 4;
   const int n = blockIdx.x * 64 + 4 * l16;
@@ -330,94 +424,169 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
     // Prefetch ST - 1 chunks, then per chunk: issue the load ST - 1 ahead and
     // run the MFMAs of the oldest stage.  Past the end the last chunk is
     // re-read (in bounds, unused), so the loop body has no load branch and
-    // each stage's MFMAs wait only for that stage's loads.
+    // each stage's MFMAs wait only for that stage's loads.  The main loop
+    // runs whole groups of ST chunks with no branch inside: a stage skipped
+    // on some path would leave its load pending at the loop header, and the
+    // compiler then drains every load in flight there (vmcnt(0)) on every
+    // iteration.  The nc mod ST chunks left over (already in flight) follow.
     const int k0 = (split * 4 + wave) * kw, k1 = k0 + kw, nc = kw / kStreamChunk;
 #pragma unroll
     for (int s = 0; s < ST - 1; s++) load(s, min(k0 + s * kStreamChunk, k1 - kStreamChunk));
-    for (int c = 0; c < nc; c += ST) {
+    int c = 0;
+    for (; c + ST <= nc; c += ST) {
 #pragma unroll
       for (int s = 0; s < ST; s++) {
-        if (c + s < nc) {
-          load((s + ST - 1) % ST, min(k0 + (c + s + ST - 1) * kStreamChunk, k1 - kStreamChunk));
-          __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
-          mma(s);
-        }
+        load((s + ST - 1) % ST, min(k0 + (c + s + ST - 1) * kStreamChunk, k1 - kStreamChunk));
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+        mma(s);
       }
     }
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++)
+      if (c + s < nc) mma(s);
   }
 
-  if (LNF) {
-    // a row's four k groups sit in lanes l16 + 16r: fold them, then lanes
-    // r = 0 publish the wave's quarter of the row sums
+  stream_finish<MI, EPI, LNF>(acc, sx, sxx, x0, 4 * S * kw, bias, Cm, ldc, M, N, part, lnc, lnd);
+}
+
+// ---------------------------------------------------------------------------
+// Split-bf16 streaming GEMM, the decode-sized projections of bf16-KV
+// contexts.  The streaming kernel's tiling (MT rows x 64 columns per
+// workgroup, the four waves on consecutive quarters of each split's k range,
+// stream_finish), with each fp32 product taken as three bf16 products on
+// v_mfma_f32_16x16x32_bf16: a = ah + al and w = wh + wl with ah = bf16(a),
+// al = bf16(a - ah) (likewise w), and a w ~ al wh + ah wl + ah wh summed in
+// fp32.  What is left out -- al wl and the rounding of al and wl -- is
+// within about 2^-16 |a w| per product (an fp32 product keeps 2^-24).  A
+// 32-deep k block costs three 16-cycle MFMAs where fp32 takes eight of 32
+// cycles, for the same bytes streamed: W is split once into its two bf16
+// halves (launch_split_w), A on the fly.
+//
+// Wx (launch_split_w): per 64-column strip s and 32-deep k block kb, 8 KB as
+// [column block j][half h (hi, lo)][lane][8 bf16], lane l of block j holding
+// W[32 kb + 8 (l >> 4) + t][64 s + 4 (l & 15) + j] for t = 0..7: the B
+// operand of one MFMA, one 16-byte load per lane.  MFMA column c of block j
+// is real column 4c + j, as in the streaming kernel, so stream_finish writes
+// four adjacent columns per lane.  Lane (l16, r) feeds A[row 16i + l16]
+// [32 kb + 8r .. + 7], two float4 loads, a full 128-byte line per row.
+constexpr int kX3Block = 32;  // k per MFMA step
+constexpr int kX3BlockU4 = 512;  // uint4 per 64-column x 32-deep block (8 KB)
+
+template <int MT, int ST, int EPI, bool LNF>
+__global__ __launch_bounds__(256) void k_gemm_x3(
+    const float* __restrict__ A, int64_t lda, const uint4* __restrict__ Wx, int N, int kw,
+    const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
+    float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd) {
+  constexpr int MI = MT / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, r = lane >> 4;
+  const int m0 = blockIdx.y * MT;
+  const int S = gridDim.z, split = blockIdx.z;
+  const int K = 4 * S * kw;
+
+  f32x4_t acc[MI][4];
 #pragma unroll
-    for (int i = 0; i < MI; i++) {
-      sx[i] += __shfl_xor(sx[i], 16);
-      sx[i] += __shfl_xor(sx[i], 32);
-      sxx[i] += __shfl_xor(sxx[i], 16);
-      sxx[i] += __shfl_xor(sxx[i], 32);
-      if (lane < 16) stat[wave][i][lane] = make_float4(sx[i], sxx[i], x0[i], 0.f);
+  for (int i = 0; i < MI; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float x0[MI], sx[MI], sxx[MI];
+
+  {
+    // Rows past M read row M - 1 (in bounds, no branch); their sums are
+    // never stored.
+    const float* Ap[MI];
+#pragma unroll
+    for (int i = 0; i < MI; i++) Ap[i] = A + (int64_t)min(m0 + 16 * i + l16, M - 1) * lda + 8 * r;
+    if (LNF) {
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        x0[i] = Ap[i][-8 * r];
+        sx[i] = 0.f;
+        sxx[i] = 0.f;
+      }
     }
-  }
-
-  // Add the four waves' sums and finish the tile on all four waves: the
-  // partial tiles go through LDS two 16-row blocks at a time, and wave w
-  // takes element w of every accumulator -- row 16i + 4r + w, columns
-  // n .. n+3 -- summing the waves in wave order (the same order on every run).
-  const float inv_k = 1.f / (float)(4 * kw);
-  float4 cv = make_float4(0.f, 0.f, 0.f, 0.f), dv = cv;
-  if (LNF) {
-    cv = *(const float4*)(lnc + n);
-    dv = *(const float4*)(lnd + n);
-  }
-#pragma unroll
-  for (int i0 = 0; i0 < MI; i0 += 2) {
-    if (i0 > 0) __syncthreads();  // the previous group's reads are done
-#pragma unroll
-    for (int ii = 0; ii < 2; ii++) {
-      if (i0 + ii >= MI) break;
+    const uint4* Wb = Wx + (int64_t)blockIdx.x * (K / kX3Block) * kX3BlockU4 + lane;
+    float4 a[ST][MI][2];
+    uint4 w[ST][4][2];
+    auto load = [&](int st, int kb) {
 #pragma unroll
       for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) red[wave][ii][j][e][lane] = acc[i0 + ii][j][e];
-    }
-    __syncthreads();
+        for (int h = 0; h < 2; h++) w[st][j][h] = Wb[(int64_t)kb * kX3BlockU4 + (2 * j + h) * 64];
 #pragma unroll
-    for (int ii = 0; ii < 2; ii++) {
-      const int i = i0 + ii;
-      if (i >= MI) break;
-      float o[4];
+      for (int i = 0; i < MI; i++) {
+        a[st][i][0] = *(const float4*)(Ap[i] + kb * kX3Block);
+        a[st][i][1] = *(const float4*)(Ap[i] + kb * kX3Block + 4);
+      }
+    };
+    auto mma = [&](int st) {
+      bf16x8_t ah[MI], al[MI];
+#pragma unroll
+      for (int i = 0; i < MI; i++) {
+        const float v[8] = {a[st][i][0].x, a[st][i][0].y, a[st][i][0].z, a[st][i][0].w,
+                            a[st][i][1].x, a[st][i][1].y, a[st][i][1].z, a[st][i][1].w};
+        if (LNF) {
+          float s1 = 0.f, s2 = sxx[i];
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const float d = v[e] - x0[i];
+            s1 += d;
+            s2 = fmaf(d, d, s2);
+          }
+          sx[i] += s1;
+          sxx[i] = s2;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const __bf16 hi = (__bf16)v[e];
+          ah[i][e] = hi;
+          al[i][e] = (__bf16)(v[e] - (float)hi);
+        }
+      }
+      // the three products of every (i, j) in turn, so consecutive MFMAs are
+      // independent; each accumulator takes them in the same order
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        float t = red[0][ii][j][wave][lane];
-        t += red[1][ii][j][wave][lane];
-        t += red[2][ii][j][wave][lane];
-        t += red[3][ii][j][wave][lane];
-        o[j] = t;
+        const bf16x8_t wh = __builtin_bit_cast(bf16x8_t, w[st][j][0]);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], wh, acc[i][j], 0, 0, 0);
       }
-      const int rl = 4 * r + wave;
-      const int row = m0 + 16 * i + rl;
-      if (LNF) {
-        const float4 q0 = stat[0][i][rl], q1 = stat[1][i][rl], q2 = stat[2][i][rl], q3 = stat[3][i][rl];
-        const float s1 = ((q0.x + q1.x) + q2.x) + q3.x;
-        const float s2 = ((q0.y + q1.y) + q2.y) + q3.y;
-        const float ms = s1 * inv_k;  // mean of x - x0
-        const float var = fmaxf(s2 * inv_k - ms * ms, 0.f);
-        const float mean = q0.z + ms;
-        const float rstd = 1.f / sqrtf(var + 1e-5f);
-        o[0] = rstd * (o[0] - mean * cv.x) + dv.x;
-        o[1] = rstd * (o[1] - mean * cv.y) + dv.y;
-        o[2] = rstd * (o[2] - mean * cv.z) + dv.z;
-        o[3] = rstd * (o[3] - mean * cv.w) + dv.w;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const bf16x8_t wl = __builtin_bit_cast(bf16x8_t, w[st][j][1]);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], wl, acc[i][j], 0, 0, 0);
       }
-      if (row >= M) continue;
-      if (S > 1) {
-        *(float4*)(part + ((int64_t)split * M + row) * N + n) = make_float4(o[0], o[1], o[2], o[3]);
-        continue;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const bf16x8_t wh = __builtin_bit_cast(bf16x8_t, w[st][j][0]);
+#pragma unroll
+        for (int i = 0; i < MI; i++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], wh, acc[i][j], 0, 0, 0);
       }
-      float* cp = Cm + (int64_t)row * ldc + n;
-      *(float4*)cp = epilogue4<EPI>(make_float4(o[0], o[1], o[2], o[3]), bias, n, cp);
+    };
+    // The streaming kernel's pipeline over 32-deep k blocks: ST - 1 blocks in
+    // flight, whole groups of ST with no branch inside, the rest after.
+    const int nc = kw / kX3Block, kb0 = (split * 4 + wave) * nc, kb1 = kb0 + nc - 1;
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++) load(s, min(kb0 + s, kb1));
+    int c = 0;
+    for (; c + ST <= nc; c += ST) {
+#pragma unroll
+      for (int s = 0; s < ST; s++) {
+        load((s + ST - 1) % ST, min(kb0 + c + s + ST - 1, kb1));
+        __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
+        mma(s);
+      }
     }
+#pragma unroll
+    for (int s = 0; s < ST - 1; s++)
+      if (c + s < nc) mma(s);
   }
+
+  stream_finish<MI, EPI, LNF>(acc, sx, sxx, x0, K, bias, Cm, ldc, M, N, part, lnc, lnd);
 }
 
 // C = epi(sum over splits of part, in split order, + bias); one float4 per thread.
@@ -528,6 +697,73 @@ static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) 
         break;
       }
     }
+  }
+}
+
+template <int MT, int ST, bool LNF>
+static int x3_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint4* Wx, int N,
+                     int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
+                     const float* lnc, const float* lnd) {
+  float* part = nullptr;
+  if (S > 1) {
+    part = (float*)scratch(ctx, "gemm_part", (size_t)S * M * N * 4);
+    if (!part) return fail(ctx, MB_ERR_NOMEM, "gemm split-K partials (%d x %d x %d)", S, M, N);
+  }
+  const dim3 grid((unsigned)(N / 64), (unsigned)((M + MT - 1) / MT), (unsigned)S);
+  const int kw = K / (4 * S);
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    if constexpr (LNF) {
+      if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
+        hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, true>), grid, dim3(256), 0, ctx->stream, A, lda,
+                           Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    } else {
+      hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, false>), grid, dim3(256), 0, ctx->stream, A, lda,
+                         Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+    }
+  });
+  if (S > 1) {
+    const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
+    with_epi(epi, [&](auto e) {
+      hipLaunchKernelGGL(k_gemm_reduce<decltype(e)::value>, dim3(rb), dim3(256), 0, ctx->stream,
+                         part, S, M, N, bias, Cm, ldc);
+    });
+  }
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
+                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                   const float* lnd) {
+  if (M <= 0) return MB_OK;
+  if (M <= kGemvMaxM || !gemm_streams(M, N))
+    return fail(ctx, MB_ERR_STATE, "split-bf16 gemm takes the streaming shapes (M %d N %d)", M, N);
+  if (N % 64 || K % (4 * kX3Block) || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
+      ((uintptr_t)Wx & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) ||
+      ((uintptr_t)lnc & 15) || ((uintptr_t)lnd & 15))
+    return fail(ctx, MB_ERR_ARG, "split-bf16 gemm shape/alignment unsupported (M %d N %d K %d)", M,
+                N, K);
+  const bool lnf = lnc != nullptr;
+  if (lnf && (!lnd || (epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)))
+    return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  int mt, S;
+  stream_shape(M, N, K, lnf, mt, S);
+  while (S > 1 && K % (4 * kX3Block * S)) S--;
+  const uint4* W = (const uint4*)Wx;
+  if (lnf) {
+    switch (mt) {
+      case 16: return x3_launch<16, 4, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+      case 32: return x3_launch<32, 3, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+      case 48: return x3_launch<48, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+      default: return x3_launch<64, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+    }
+  }
+  switch (mt) {
+    case 16: return x3_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    case 32: return x3_launch<32, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    case 48: return x3_launch<48, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    default: return x3_launch<64, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
   }
 }
 
@@ -931,6 +1167,41 @@ int launch_tile_w(mb_ctx* ctx, const float* W, int K, int N, float* Wt) {
   const int64_t n = (int64_t)K * N;
   hipLaunchKernelGGL(k_tile_w, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, W, K,
                      N, Wt);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// The split-bf16 operand layout of k_gemm_x3 from an fp32 W, column-block-
+// major [N / 64][K][64] (tiled) or row-major [K][N]: one thread per 16-byte
+// piece (strip, k block, column block j, half h, lane), 8 bf16 of one column.
+__global__ __launch_bounds__(256) void k_split_w(const float* __restrict__ Wt, int K, int N,
+                                                 bool tiled, uint4* __restrict__ Wx) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= (int64_t)(N / 64) * (K / kX3Block) * kX3BlockU4) return;
+  const int lane = (int)(u & 63), h = (int)((u >> 6) & 1), j = (int)((u >> 7) & 3);
+  const int64_t blk = u >> 9;  // strip * (K / 32) + k block
+  const int nkb = K / kX3Block;
+  const int64_t strip = blk / nkb;
+  const int kb = (int)(blk % nkb);
+  const int64_t k = kb * kX3Block + 8 * (lane >> 4), ld = tiled ? 64 : N;
+  const float* src = (tiled ? Wt + strip * K * 64 : Wt + strip * 64) + k * ld + 4 * (lane & 15) + j;
+  bf16x8_t out;
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    const float v = src[t * ld];
+    const __bf16 hi = (__bf16)v;
+    out[t] = h ? (__bf16)(v - (float)hi) : hi;
+  }
+  Wx[u] = __builtin_bit_cast(uint4, out);
+}
+
+int launch_split_w(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled) {
+  if (N % 64 || K % kX3Block)
+    return fail(ctx, MB_ERR_ARG, "split-bf16 weights need N %% 64 == 0 and K %% 32 == 0 (K %d N %d)",
+                K, N);
+  const int64_t n = (int64_t)(N / 64) * (K / kX3Block) * kX3BlockU4;
+  hipLaunchKernelGGL(k_split_w, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, Wt, K,
+                     N, tiled, (uint4*)Wx);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

@@ -487,6 +487,29 @@ int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
   return launch_gemm(ctx, epi, A, lda, W, N, K, bias, C, ldc, M);
 }
 
+int mb_split_weights_dev(mb_ctx* ctx, const float* W, int K, int N, void* Wx) {
+  MB_DEVICE_GUARD(ctx);
+  if (!ctx) return MB_ERR_ARG;
+  if (K < 1 || N < 1) return fail(ctx, MB_ERR_ARG, "split weights shape K %d N %d", K, N);
+  if (!W || !Wx) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (((uintptr_t)Wx & 15)) return fail(ctx, MB_ERR_ARG, "Wx must be 16-byte aligned");
+  return launch_split_w(ctx, W, K, N, Wx, false);
+}
+
+int mb_linear_split_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
+                        const void* Wx, const float* bias, float* C, int64_t ldc, int epi) {
+  MB_DEVICE_GUARD(ctx);
+  if (!ctx) return MB_ERR_ARG;
+  if (M < 0 || N < 1 || K < 1) return fail(ctx, MB_ERR_ARG, "linear shape M %d N %d K %d", M, N, K);
+  if (epi < EPI_STORE || epi > EPI_GELU_ERF) return fail(ctx, MB_ERR_ARG, "unknown epilogue %d", epi);
+  if (epi == EPI_SCALE_ADD && !bias)
+    return fail(ctx, MB_ERR_ARG, "MB_EPI_SCALE_ADD needs the scale vector in `bias`");
+  if (M == 0) return MB_OK;
+  if (!A || !Wx || !C) return fail(ctx, MB_ERR_ARG, "null pointer");
+  if (lda < K || ldc < N) return fail(ctx, MB_ERR_ARG, "leading dimension below the row width");
+  return launch_gemm_x3(ctx, epi, A, lda, Wx, N, K, bias, C, ldc, M, nullptr, nullptr);
+}
+
 // ---------------------------------------------------------- host pointers
 
 int mb_ring_write_rows(mb_ctx* ctx, int layer, int B, int rows_max, const float* qkv,

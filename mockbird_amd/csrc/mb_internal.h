@@ -73,12 +73,15 @@ struct AudioTables {
 // column-block-major) and column-block-major copies of the other two, which
 // the streaming kernel reads at decode sizes, and k-major copies of all four
 // (the folded ones folded), which the GEMV kernel reads at up to kGemvMaxM rows.
+// In bf16-KV contexts the four column-block-major forms also have split-bf16
+// copies (launch_split_w), which decode-sized projections read there.
 struct LayerW {
   const float *ln1_w, *ln1_b, *attn_w, *attn_b, *proj_w, *proj_b;
   const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
   const float *attn_wg, *attn_c, *attn_d, *fc_in_wg, *fc_in_c, *fc_in_d;
   const float *proj_wt, *fc_out_wt;
   const float *attn_wk, *fc_in_wk, *proj_wk, *fc_out_wk;
+  const void *attn_wx, *fc_in_wx, *proj_wx, *fc_out_wx;  // null in fp32-KV contexts
 };
 
 // Every weight a model call needs, resolved from the uploaded tensors.
@@ -89,8 +92,10 @@ struct ModelW {
   LayerW local;
   const float *local_lnf_w, *local_lnf_b, *text_head;
   AudioTables audio_heads;
-  // the audio heads with the local ln_f folded in (column-block-major and k-major)
+  // the audio heads with the local ln_f folded in (column-block-major and k-major;
+  // split-bf16 in bf16-KV contexts, else null)
   AudioTables head_wg, head_c, head_d, head_wk;
+  const void* head_wx[NVQ];
 };
 
 // Projections with fewer rows than this run with their LayerNorm folded in.
@@ -313,6 +318,19 @@ int launch_fold_ln(mb_ctx* ctx, const float* W, int K, int N, const float* gamma
 int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const float* Wg, int N,
                    int K, const float* c, const float* d, const float* bias, float* Cm,
                    int64_t ldc, int M);
+// Split-bf16 projections (bf16-KV contexts): Wx, 2 K N bf16 values, holds
+// each weight of an fp32 W -- column-block-major [N / 64][K][64] (tiled:
+// launch_tile_w, launch_fold_ln's Wg) or row-major [K][N] -- as a bf16 high
+// part and a bf16 remainder, and
+// launch_gemm_x3 computes C = epi(A W + bias) with every product as three
+// bf16 products summed in fp32 (within about 2^-16 of the fp32 product).
+// Takes kGemvMaxM < M with gemm_streams(M, N), else MB_ERR_STATE; with lnc
+// (and lnd) A is the raw residual stream and the LayerNorm is folded in, as
+// for launch_gemm_ln.  K a multiple of 128.
+int launch_split_w(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled = true);
+int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
+                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                   const float* lnd);
 
 // layers.hip
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,

@@ -64,6 +64,17 @@ int kmajor(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, c
   return launch_kmajor_w(ctx, W, K, N, gamma, p);
 }
 
+// The split-bf16 copy (launch_split_w) of a column-block-major [K][N]
+// projection Wt, for bf16-KV contexts; null in fp32-KV contexts.
+int split(mb_ctx* ctx, const std::string& name, const float* Wt, int K, int N, const void*& wx) {
+  wx = nullptr;
+  if (ctx->cfg.kv_dtype != MB_KV_BF16) return MB_OK;
+  float* p = internal_tensor(ctx, name, (int64_t)K * N);  // 2 K N bf16
+  if (!p) return fail(ctx, MB_ERR_NOMEM, "split weight allocation failed (%s)", name.c_str());
+  wx = p;
+  return launch_split_w(ctx, Wt, K, N, p);
+}
+
 int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
   int rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
                 w.attn_d);
@@ -74,8 +85,14 @@ int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
   if ((rc = kmajor(ctx, key + ".fc_in.k", w.fc_in_w, D, FFN, w.ln2_w, w.fc_in_wk))) return rc;
   if ((rc = kmajor(ctx, key + ".proj.k", w.proj_w, D, D, nullptr, w.proj_wk))) return rc;
   if ((rc = kmajor(ctx, key + ".fc_out.k", w.fc_out_w, FFN, D, nullptr, w.fc_out_wk))) return rc;
-  return fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
-              w.fc_in_d);
+  if ((rc = fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
+                 w.fc_in_d)))
+    return rc;
+  if ((rc = split(ctx, key + ".attn.x", w.attn_wg, D, QKV, w.attn_wx)) ||
+      (rc = split(ctx, key + ".fc_in.x", w.fc_in_wg, D, FFN, w.fc_in_wx)) ||
+      (rc = split(ctx, key + ".proj.x", w.proj_wt, D, D, w.proj_wx)))
+    return rc;
+  return split(ctx, key + ".fc_out.x", w.fc_out_wt, FFN, D, w.fc_out_wx);
 }
 
 // Resolve every weight once per upload (gpu.ts:339-343 throws "weight not
@@ -118,7 +135,8 @@ int resolve(mb_ctx* ctx, bool global, bool local) {
       const std::string p = "#fold/head" + std::to_string(k);
       if ((rc = fold(ctx, p, m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.local_lnf_b,
                      m.head_wg.t[k], m.head_c.t[k], m.head_d.t[k])) ||
-          (rc = kmajor(ctx, p + ".k", m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.head_wk.t[k])))
+          (rc = kmajor(ctx, p + ".k", m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.head_wk.t[k])) ||
+          (rc = split(ctx, p + ".x", m.head_wg.t[k], D, CODES, m.head_wx[k])))
         return rc;
     }
     ctx->model_ok = true;
@@ -164,9 +182,15 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   // up to kGemvMaxM rows the projections read the k-major copies
   const bool folded = M < kFoldMaxM;
   const bool gemv = M <= kGemvMaxM;
+  // bf16-KV contexts: decode-sized projections as split-bf16 products
+  const bool x3 = !gemv && folded && w.attn_wx && gemm_streams((int)M, D);
   if (gemv) {
     if ((rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
                             (int)M, w.attn_c, w.attn_d)))
+      return rc;
+  } else if (x3) {
+    if ((rc = launch_gemm_x3(ctx, EPI_STORE, a.x, D, w.attn_wx, QKV, D, w.attn_b, a.qkv, QKV,
+                             (int)M, w.attn_c, w.attn_d)))
       return rc;
   } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, w.attn_wg, QKV, D, w.attn_c, w.attn_d,
@@ -203,12 +227,18 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   const bool tiled = gemm_streams((int)M, D);
   if ((rc = gemv ? launch_gemv_k(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
                                  nullptr, nullptr)
-                 : launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b,
-                               a.x, D, (int)M, tiled)))
+           : x3 ? launch_gemm_x3(ctx, EPI_ADD, a.att, D, w.proj_wx, D, D, w.proj_b, a.x, D, (int)M,
+                                 nullptr, nullptr)
+                : launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b,
+                              a.x, D, (int)M, tiled)))
     return rc;
   if (gemv) {
     if ((rc = launch_gemv_k(ctx, EPI_GELU, a.x, D, w.fc_in_wk, FFN, D, w.fc_in_b, a.ffn, FFN,
                             (int)M, w.fc_in_c, w.fc_in_d)))
+      return rc;
+  } else if (x3) {
+    if ((rc = launch_gemm_x3(ctx, EPI_GELU, a.x, D, w.fc_in_wx, FFN, D, w.fc_in_b, a.ffn, FFN,
+                             (int)M, w.fc_in_c, w.fc_in_d)))
       return rc;
   } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_GELU, a.x, D, w.fc_in_wg, FFN, D, w.fc_in_c, w.fc_in_d,
@@ -222,6 +252,9 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   if (gemv)
     return launch_gemv_k(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wk, D, FFN, w.fc_out_b, a.x, D, (int)M,
                          nullptr, nullptr);
+  if (x3)
+    return launch_gemm_x3(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wx, D, FFN, w.fc_out_b, a.x, D, (int)M,
+                          nullptr, nullptr);
   return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, tiled ? w.fc_out_wt : w.fc_out_w, D, FFN, w.fc_out_b,
                      a.x, D, (int)M, tiled);
 }
@@ -356,6 +389,9 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
       if (folded_head && B <= kGemvMaxM)
         rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, m.head_wk.t[ch], CODES, D, nullptr, lg, ldl, B,
                            m.head_c.t[ch], m.head_d.t[ch]);
+      else if (folded_head && m.head_wx[ch] && gemm_streams(B, CODES))
+        rc = launch_gemm_x3(ctx, EPI_STORE, a.x, D, m.head_wx[ch], CODES, D, nullptr, lg, ldl, B,
+                            m.head_c.t[ch], m.head_d.t[ch]);
       else if (folded_head)
         rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, m.head_wg.t[ch], CODES, D, m.head_c.t[ch],
                             m.head_d.t[ch], nullptr, lg, ldl, B);

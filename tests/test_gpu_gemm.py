@@ -168,3 +168,79 @@ def test_gemv_rows_1_to_8(ctx):
             assert np.array_equal(outs[0], outs[1]), (M, N, K)
             err = float(np.abs(outs[0] - want).max())
             assert err < 1e-4, (M, N, K, err)
+
+
+SPLIT_SHAPES = [  # (M, N, K): 16 / 32 / 48 / 64-row tiles, k split in two, ragged M
+    (9, 2304, 768), (64, 768, 768), (100, 768, 3072), (256, 2304, 768), (256, 3072, 768),
+    (256, 768, 3072), (256, 1024, 768), (300, 768, 768), (1000, 768, 768),
+]
+
+
+def _bf16(x):
+    """float32 -> bf16 (round to nearest even), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_SHAPES)
+def test_linear_split_bf16(ctx, M, N, K):
+    """mb_linear_split_dev on weights from mb_split_weights_dev.  Each product
+    a w is ah wh + ah wl + al wh (ah = bf16(a), al = bf16(a - ah), likewise
+    w); with bf16's 8-bit significand the terms left out are each within
+    2^-18 |a w|, so every output is within 2^-16 sum_k |a_k w_k| (+ fp32
+    accumulation) of the exact product -- checked elementwise against the
+    oracle's GEMM.  Plain bf16 products (ah wh alone) miss by ~2^-9 |a w|:
+    the split must land at least 30x closer, which a dropped term fails.
+    Two calls are bit-identical."""
+    torch = pytest.importorskip("torch")
+    say(f"linear split-bf16 M={M} N={N} K={K}")
+    g = np.random.default_rng([M, N, K, 3])
+    A = g.standard_normal((M, K), dtype=np.float32)
+    W = g.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+    bias = g.standard_normal(N, dtype=np.float32) * np.float32(0.1)
+    C0 = g.standard_normal((M, N), dtype=np.float32)
+    dev = torch.device("cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    tA, tW, tb = (torch.from_numpy(x).to(dev) for x in (A, W, bias))
+    tWx = torch.empty(2 * K * N, dtype=torch.bfloat16, device=dev)
+    ctx.split_weights_dev(tW.data_ptr(), K, N, tWx.data_ptr())
+    lin = oracle.gemm(A, W, bias).astype(np.float64)
+    absprod = np.abs(A.astype(np.float64)) @ np.abs(W.astype(np.float64))
+    bound = 2.0 ** -16 * absprod + 2e-6 * (1.0 + np.abs(lin))
+    plain = (_bf16(A).astype(np.float64) @ _bf16(W).astype(np.float64)) + bias
+    plain_err = float(np.abs(plain - lin).max())
+    for epi in (mb.MB_EPI_STORE, mb.MB_EPI_GELU, mb.MB_EPI_ADD):
+        outs = []
+        for _ in range(2):
+            tC = torch.from_numpy(C0).to(dev)
+            ctx.linear_split_dev(M, N, K, tA.data_ptr(), K, tWx.data_ptr(), tb.data_ptr(),
+                                 tC.data_ptr(), N, epi)
+            torch.cuda.synchronize()
+            outs.append(tC.cpu().numpy())
+        assert np.array_equal(outs[0], outs[1]), epi
+        got = outs[0].astype(np.float64)
+        if epi == mb.MB_EPI_STORE:
+            err = np.abs(got - lin)
+            assert (err <= bound).all(), float((err / bound).max())
+            assert float(err.max()) * 30 < plain_err, (float(err.max()), plain_err)
+        elif epi == mb.MB_EPI_GELU:  # |gelu'| <= 1.13
+            want = oracle.gelu(lin.astype(np.float32)).astype(np.float64)
+            assert (np.abs(got - want) <= 1.2 * bound + 1e-6).all()
+        else:
+            want = C0.astype(np.float64) + lin
+            assert (np.abs(got - want) <= bound + 2.0 ** -23 * np.abs(want)).all()
+
+
+def test_linear_split_rejects_bad_shapes(ctx):
+    """GEMV-sized M, K not a multiple of 128 and misaligned weights are
+    refused before any launch."""
+    with pytest.raises(mb.MbError) as e:
+        ctx.linear_split_dev(8, 768, 768, 16, 768, 16, None, 16, 768)  # M <= 8: the GEMV's
+    assert e.value.code == mb.MB_ERR_STATE
+    with pytest.raises(mb.MbError) as e:
+        ctx.linear_split_dev(64, 768, 704, 16, 704, 16, None, 16, 768)  # K % 128 != 0
+    assert e.value.code == mb.MB_ERR_ARG
+    with pytest.raises(mb.MbError) as e:
+        ctx.split_weights_dev(16, 768, 768, 24)  # Wx not 16-byte aligned
+    assert e.value.code == mb.MB_ERR_ARG
