@@ -14,6 +14,7 @@
 // product in a different order).  The next slice's global loads are issued
 // before the current slice's MFMAs.
 #include <type_traits>
+#include <utility>
 
 #include "kv_types.h"
 #include "mb_internal.h"
@@ -62,6 +63,18 @@ static void with_epi(int epi, F f) {
     case EPI_GELU_ERF: f(std::integral_constant<int, EPI_GELU_ERF>{}); break;
     default: f(std::integral_constant<int, EPI_STORE>{}); break;
   }
+}
+
+// f(std::integral_constant<int, i>{}) for i = 0 .. N - 1, so a body can index
+// register arrays with a compile-time i however large it is (an unrolled loop
+// may be left rolled, and the arrays then live in scratch memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 template <int TM, int TN, int EPI>
@@ -250,6 +263,19 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
   return v;
 }
 
+// Two floats stored, and four loaded, as device-coherent accesses
+// (agent-scope relaxed atomics: sc1 stores and loads on gfx950).
+__device__ __forceinline__ void store_coherent(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4 load_coherent(const float* p) {
+  const uint64_t lo = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint64_t hi = __hip_atomic_load((const uint64_t*)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float4(__uint_as_float((uint32_t)lo), __uint_as_float((uint32_t)(lo >> 32)),
+                     __uint_as_float((uint32_t)hi), __uint_as_float((uint32_t)(hi >> 32)));
+}
+
 // The end of a streaming tile, shared by k_gemm_stream and k_gemm_x3: the
 // four waves' partial sums of an MT x 64 tile (acc[i][j][e] = row 16i + 4r +
 // e, column n + j of the wave's k range) are added in wave order and the
@@ -257,6 +283,18 @@ __device__ __forceinline__ float4 epilogue4(float4 v, const float* __restrict__ 
 // sx / sxx / x0 are the lane's sums of x - x0 and (x - x0)^2 over the A
 // values it streamed (rows 16i + l16, k group r of every k step) and K is
 // the row width.
+//
+// With tile counters (cnt, S > 1) the splits finish the tile themselves: each
+// writes its partial and counts itself in on its tile's counter; the one that
+// counts last adds the S partials in split order (whichever split that is,
+// the sum is the same), applies the epilogue and sets the counter back to
+// zero for the next launch.  Without counters k_gemm_reduce does that in a
+// second launch.  The splits of a tile run on different XCDs, whose L2 caches
+// are not coherent with each other; a device-scope fence would write back and
+// invalidate the whole L2 of every workgroup's XCD, so instead the partials
+// move with device-coherent accesses: agent-scope relaxed atomic stores and
+// loads (global_store / global_load with sc1), the stores waited for
+// (vmcnt(0)) before the counter's atomic add.
 template <int MI, int EPI, bool LNF>
 __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)[MI],
                                               float (&sxx)[MI], const float (&x0)[MI], int K,
@@ -264,7 +302,8 @@ __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)
                                               float* __restrict__ Cm, int64_t ldc, int M,
                                               int N, float* __restrict__ part,
                                               const float* __restrict__ lnc,
-                                              const float* __restrict__ lnd) {
+                                              const float* __restrict__ lnd,
+                                              int32_t* __restrict__ cnt = nullptr) {
   __shared__ float red[4][2][4][4][64];  // [wave][block][column block][element][lane]
   __shared__ float4 stat[LNF ? 4 : 1][MI][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -337,13 +376,44 @@ __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)
       }
       if (row >= M) continue;
       if (S > 1) {
-        *(float4*)(part + ((int64_t)split * M + row) * N + n) = make_float4(o[0], o[1], o[2], o[3]);
+        float* pp = part + ((int64_t)split * M + row) * N + n;
+        if (cnt) {
+          store_coherent(pp, o[0], o[1]);
+          store_coherent(pp + 2, o[2], o[3]);
+        } else {
+          *(float4*)pp = make_float4(o[0], o[1], o[2], o[3]);
+        }
         continue;
       }
       float* cp = Cm + (int64_t)row * ldc + n;
       *(float4*)cp = epilogue4<EPI>(make_float4(o[0], o[1], o[2], o[3]), bias, n, cp);
     }
   }
+  if (S == 1 || !cnt) return;
+  __shared__ int last;
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0): this split's partial stores are done
+  __syncthreads();
+  const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(&cnt[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+  __syncthreads();
+  if (!last) return;
+  const int64_t stride = (int64_t)M * N;
+#pragma unroll
+  for (int u = 0; u < MI; u++) {
+    const int q = threadIdx.x + 256 * u;  // float4 of the 16 MI x 64 tile
+    const int row = m0 + (q >> 4), col = blockIdx.x * 64 + (q & 15) * 4;
+    if (row >= M) continue;
+    const float* pp = part + (int64_t)row * N + col;
+    float4 sum = load_coherent(pp);
+    for (int sp = 1; sp < S; sp++) {
+      const float4 v = load_coherent(pp + sp * stride);
+      sum.x += v.x; sum.y += v.y; sum.z += v.z; sum.w += v.w;
+    }
+    float* cp = Cm + (int64_t)row * ldc + col;
+    *(float4*)cp = epilogue4<EPI>(sum, bias, col, cp);
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(&cnt[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // With LNF the A rows are the raw residual stream x and the LayerNorm in
@@ -467,8 +537,17 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
 // W[32 kb + 8 (l >> 4) + t][64 s + 4 (l & 15) + j] for t = 0..7: the B
 // operand of one MFMA, one 16-byte load per lane.  MFMA column c of block j
 // is real column 4c + j, as in the streaming kernel, so stream_finish writes
-// four adjacent columns per lane.  Lane (l16, r) feeds A[row 16i + l16]
-// [32 kb + 8r .. + 7], two float4 loads, a full 128-byte line per row.
+// four adjacent columns per lane.
+//
+// A: lane (l16, r) feeds A[row 16i + l16][32 kb + 8r .. + 7] to the MFMAs,
+// but loading that directly puts 16 rows (16 cache lines) in each quarter
+// wave of a load -- four times the W loads' lines per byte, and measured the
+// slower stream.  So A is loaded row-contiguous (8 lanes per 128-byte row
+// line, load p covering rows 8p .. 8p + 7 of the tile's 32-deep block) and
+// each wave passes its block through its own slice of LDS: written 16-byte
+// chunk c of row R at chunk c ^ (R & 7), read back as the MFMA fragments
+// (both conflict-free).  A wave only reads what it wrote, so this needs no
+// barrier; the compiler sees every load and orders the LDS traffic.
 constexpr int kX3Block = 32;  // k per MFMA step
 constexpr int kX3BlockU4 = 512;  // uint4 per 64-column x 32-deep block (8 KB)
 
@@ -476,8 +555,10 @@ template <int MT, int ST, int EPI, bool LNF>
 __global__ __launch_bounds__(256) void k_gemm_x3(
     const float* __restrict__ A, int64_t lda, const uint4* __restrict__ Wx, int N, int kw,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
-    float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd) {
-  constexpr int MI = MT / 16;
+    float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd,
+    int32_t* __restrict__ cnt) {
+  constexpr int MI = MT / 16, AL = MT / 8;  // row blocks; A loads per block (8 rows each)
+  __shared__ f32x4_t Ablk[4][MT * 8];       // per wave: MT rows x 8 chunks of 4 floats
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, r = lane >> 4;
   const int m0 = blockIdx.y * MT;
@@ -494,37 +575,46 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
   {
     // Rows past M read row M - 1 (in bounds, no branch); their sums are
     // never stored.
-    const float* Ap[MI];
-#pragma unroll
-    for (int i = 0; i < MI; i++) Ap[i] = A + (int64_t)min(m0 + 16 * i + l16, M - 1) * lda + 8 * r;
     if (LNF) {
 #pragma unroll
       for (int i = 0; i < MI; i++) {
-        x0[i] = Ap[i][-8 * r];
+        x0[i] = A[(int64_t)min(m0 + 16 * i + l16, M - 1) * lda];
         sx[i] = 0.f;
         sxx[i] = 0.f;
       }
     }
+    // row-contiguous load order: load p, lane (crow, cchunk) = row 8p + crow,
+    // chunk cchunk; element offsets fit 32 bits (launch_gemm_x3 checks M lda)
+    const int crow = lane >> 3, cchunk = lane & 7;
+    uint32_t aoff[AL];
+#pragma unroll
+    for (int p = 0; p < AL; p++) aoff[p] = (uint32_t)(min(m0 + 8 * p + crow, M - 1) * lda + 4 * cchunk);
+    // (8p + crow) & 7 == crow and (16i + l16) & 7 == l16 & 7: one swizzled
+    // base per lane, rows apart by immediate offsets
+    f32x4_t* const Aw = Ablk[wave] + crow * 8 + (cchunk ^ crow);
+    const f32x4_t* const Ar0 = Ablk[wave] + l16 * 8 + ((2 * r) ^ (l16 & 7));
+    const f32x4_t* const Ar1 = Ablk[wave] + l16 * 8 + ((2 * r + 1) ^ (l16 & 7));
     const uint4* Wb = Wx + (int64_t)blockIdx.x * (K / kX3Block) * kX3BlockU4 + lane;
-    float4 a[ST][MI][2];
+    f32x4_t a[ST][AL];
     uint4 w[ST][4][2];
-    auto load = [&](int st, int kb) {
+    auto load = [&](auto st_, int kb) {
+      constexpr int st = decltype(st_)::value;
 #pragma unroll
       for (int j = 0; j < 4; j++)
 #pragma unroll
         for (int h = 0; h < 2; h++) w[st][j][h] = Wb[(int64_t)kb * kX3BlockU4 + (2 * j + h) * 64];
 #pragma unroll
-      for (int i = 0; i < MI; i++) {
-        a[st][i][0] = *(const float4*)(Ap[i] + kb * kX3Block);
-        a[st][i][1] = *(const float4*)(Ap[i] + kb * kX3Block + 4);
-      }
+      for (int p = 0; p < AL; p++) a[st][p] = *(const f32x4_t*)(A + kb * kX3Block + aoff[p]);
     };
-    auto mma = [&](int st) {
+    auto mma = [&](auto st_) {
+      constexpr int st = decltype(st_)::value;
+#pragma unroll
+      for (int p = 0; p < AL; p++) Aw[p * 64] = a[st][p];
       bf16x8_t ah[MI], al[MI];
 #pragma unroll
       for (int i = 0; i < MI; i++) {
-        const float v[8] = {a[st][i][0].x, a[st][i][0].y, a[st][i][0].z, a[st][i][0].w,
-                            a[st][i][1].x, a[st][i][1].y, a[st][i][1].z, a[st][i][1].w};
+        const f32x4_t v0 = Ar0[i * 128], v1 = Ar1[i * 128];
+        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         if (LNF) {
           float s1 = 0.f, s2 = sxx[i];
 #pragma unroll
@@ -570,23 +660,25 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
     // The streaming kernel's pipeline over 32-deep k blocks: ST - 1 blocks in
     // flight, whole groups of ST with no branch inside, the rest after.
     const int nc = kw / kX3Block, kb0 = (split * 4 + wave) * nc, kb1 = kb0 + nc - 1;
-#pragma unroll
-    for (int s = 0; s < ST - 1; s++) load(s, min(kb0 + s, kb1));
+    static_for<ST - 1>([&](auto s_) {
+      constexpr int s = decltype(s_)::value;
+      load(std::integral_constant<int, s>{}, min(kb0 + s, kb1));
+    });
     int c = 0;
     for (; c + ST <= nc; c += ST) {
-#pragma unroll
-      for (int s = 0; s < ST; s++) {
-        load((s + ST - 1) % ST, min(kb0 + c + s + ST - 1, kb1));
+      static_for<ST>([&](auto s_) {
+        constexpr int s = decltype(s_)::value;
+        load(std::integral_constant<int, (s + ST - 1) % ST>{}, min(kb0 + c + s + ST - 1, kb1));
         __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the MFMAs
-        mma(s);
-      }
+        mma(s_);
+      });
     }
-#pragma unroll
-    for (int s = 0; s < ST - 1; s++)
-      if (c + s < nc) mma(s);
+    static_for<ST - 1>([&](auto s_) {
+      if (c + decltype(s_)::value < nc) mma(s_);
+    });
   }
 
-  stream_finish<MI, EPI, LNF>(acc, sx, sxx, x0, K, bias, Cm, ldc, M, N, part, lnc, lnd);
+  stream_finish<MI, EPI, LNF>(acc, sx, sxx, x0, K, bias, Cm, ldc, M, N, part, lnc, lnd, cnt);
 }
 
 // C = epi(sum over splits of part, in split order, + bias); one float4 per thread.
@@ -700,35 +792,46 @@ static void stream_shape(int M, int N, int K, bool whole_rows, int& mt, int& S) 
   }
 }
 
+// Per-tile arrival counters of the split-K tiles that finish themselves
+// (stream_finish), zero between launches: zeroed once when allocated (a fill
+// kernel), and each tile's last split sets its counter back to zero.
+constexpr int kTileCounters = 8192;
+static int tile_counters(mb_ctx* ctx, int32_t*& cnt) {
+  const bool fresh = !ctx->scratch["gemm_tile_cnt"].ptr;
+  cnt = (int32_t*)scratch(ctx, "gemm_tile_cnt", kTileCounters * sizeof(int32_t));
+  if (!cnt) return fail(ctx, MB_ERR_NOMEM, "split gemm tile counters");
+  return fresh ? launch_fill_i32(ctx, cnt, kTileCounters, 0) : MB_OK;
+}
+
 template <int MT, int ST, bool LNF>
 static int x3_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint4* Wx, int N,
                      int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
                      const float* lnc, const float* lnd) {
-  float* part = nullptr;
-  if (S > 1) {
-    part = (float*)scratch(ctx, "gemm_part", (size_t)S * M * N * 4);
-    if (!part) return fail(ctx, MB_ERR_NOMEM, "gemm split-K partials (%d x %d x %d)", S, M, N);
-  }
   const dim3 grid((unsigned)(N / 64), (unsigned)((M + MT - 1) / MT), (unsigned)S);
+  float* part = nullptr;
+  int32_t* cnt = nullptr;
+  if (S > 1) {
+    // its own buffer: only device-coherent accesses ever touch it
+    part = (float*)scratch(ctx, "gemm_part_coherent", (size_t)S * M * N * 4);
+    if (!part) return fail(ctx, MB_ERR_NOMEM, "gemm split-K partials (%d x %d x %d)", S, M, N);
+    if ((int64_t)grid.x * grid.y > kTileCounters)
+      return fail(ctx, MB_ERR_ARG, "split gemm has %u tiles, the counters cover %d", grid.x * grid.y,
+                  kTileCounters);
+    int rc = tile_counters(ctx, cnt);
+    if (rc) return rc;
+  }
   const int kw = K / (4 * S);
   with_epi(epi, [&](auto e) {
     constexpr int E = decltype(e)::value;
     if constexpr (LNF) {
       if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
         hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, true>), grid, dim3(256), 0, ctx->stream, A, lda,
-                           Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+                           Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt);
     } else {
       hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, false>), grid, dim3(256), 0, ctx->stream, A, lda,
-                         Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd);
+                         Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt);
     }
   });
-  if (S > 1) {
-    const unsigned rb = (unsigned)(((int64_t)M * (N / 4) + 255) / 256);
-    with_epi(epi, [&](auto e) {
-      hipLaunchKernelGGL(k_gemm_reduce<decltype(e)::value>, dim3(rb), dim3(256), 0, ctx->stream,
-                         part, S, M, N, bias, Cm, ldc);
-    });
-  }
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
@@ -739,7 +842,8 @@ int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void
   if (M <= 0) return MB_OK;
   if (M <= kGemvMaxM || !gemm_streams(M, N))
     return fail(ctx, MB_ERR_STATE, "split-bf16 gemm takes the streaming shapes (M %d N %d)", M, N);
-  if (N % 64 || K % (4 * kX3Block) || lda % 4 || ldc % 4 || ((uintptr_t)A & 15) ||
+  if (N % 64 || K % (4 * kX3Block) || lda % 4 || ldc % 4 || (int64_t)M * lda >= INT32_MAX ||
+      ((uintptr_t)A & 15) ||
       ((uintptr_t)Wx & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) ||
       ((uintptr_t)lnc & 15) || ((uintptr_t)lnd & 15))
     return fail(ctx, MB_ERR_ARG, "split-bf16 gemm shape/alignment unsupported (M %d N %d K %d)", M,
