@@ -500,6 +500,131 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? o / L : 0.f;
 }
 
+// Fused append + attention for windows of at most kShortWindow slots in an
+// fp32 non-wrapping ring (the local head's 17-slot ring): k_attn_unit's
+// one-wave path with each wave its own (query, head) -- four heads per
+// 256-thread block, so 256 voices are 768 blocks instead of 3072 one-wave
+// blocks -- and no cross-wave fold.  The window fits one batch (GU = 20
+// slots: lane group g of 16 lanes holds slots g, g + 4, ..., g + 16), the
+// computation per lane group and the group merge are k_attn_unit's, and the
+// slots past the window enter as p = 0 terms there, so the outputs are the
+// same bits k_attn_unit gives (its 48-slot batch adds only more zero terms).
+constexpr int kShortWindow = 20;
+template <bool IN_BF16>
+__global__ __launch_bounds__(256) void k_attn_short(
+    const void* __restrict__ qkv, Rows q_rows, const int32_t* __restrict__ pos0, int nunits,
+    float* __restrict__ ring_k, float* __restrict__ ring_v, int32_t* __restrict__ slot_pos,
+    int64_t ring_seq_stride, int C, const float2* __restrict__ rope_tab,
+    float* __restrict__ q_out, Rows qo_rows, float* __restrict__ out, Rows out_rows) {
+  constexpr int VD = 4, LR = 16, G = 4, U = kShortWindow / G, GU = G * U;
+  constexpr int ROWB = HD * 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int unit = blockIdx.x * 4 + wave;
+  if (unit >= nunits) return;  // per wave: no barrier below
+  const int b = unit / H, head = unit % H;
+  const int g = lane / LR, sub = lane % LR;
+  const int64_t cur = pos0[b];
+  const int nvalid = cur < 0 ? 0 : (int)(cur + 1 < C ? cur + 1 : C);
+  const int64_t kv_off = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
+  const char* kbase = (const char*)(ring_k + kv_off);
+  const char* vbase = (const char*)(ring_v + kv_off);
+  const int32_t* sp = slot_pos + (int64_t)b * C;
+
+  // the window's K and V rows and stored positions, issued before the append
+  uint4 kr[U], vr[U];
+  const int32_t spl = (lane < GU && lane < nvalid) ? sp[lane] : -1;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int slot = u * G + g;
+    const int sl = slot < nvalid ? slot : 0;
+    kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
+    vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
+  }
+
+  const int64_t roff = row_at(q_rows, b, 0) + head * HD + sub * VD;
+  float qi[VD], qo[VD], cs[VD / 2], sn[VD / 2], qv[VD];
+  load_n<IN_BF16, VD>(qkv, roff, qi);
+  const bool have = cur >= 0 && cur < C;
+  const int32_t pos = (int32_t)(have ? cur : 0);
+  const int slot_new = have ? (int)cur : -1;
+#pragma unroll
+  for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+#pragma unroll
+  for (int j = 0; j < VD / 2; j++) rope_pair(qi[2 * j], qi[2 * j + 1], cs[j], sn[j], qo[2 * j], qo[2 * j + 1]);
+  if (q_out && g == 0) {
+    float* op = q_out + row_at(qo_rows, b, 0) + head * HD + sub * VD;
+    *(float4*)op = make_float4(qo[0], qo[1], qo[2], qo[3]);
+  }
+#pragma unroll
+  for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
+  uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
+  if (slot_new >= 0) {  // wave-uniform
+    float ki[VD], vi[VD], ko[VD];
+    load_n<IN_BF16, VD>(qkv, roff + D, ki);
+    load_n<IN_BF16, VD>(qkv, roff + 2 * D, vi);
+#pragma unroll
+    for (int j = 0; j < VD / 2; j++)
+      rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
+    knew = pack16<false>(ko);
+    vnew = pack16<false>(vi);
+    if (g == 0) {
+      *(uint4*)(ring_k + kv_off + (int64_t)slot_new * HD) = knew;
+      *(uint4*)(ring_v + kv_off + (int64_t)slot_new * HD) = vnew;
+      if (head == 0 && sub == 0) slot_pos[(int64_t)b * C + slot_new] = (int32_t)cur;
+    }
+  }
+
+  const int64_t dlt = cur - (int64_t)spl;
+  const uint64_t live = __ballot(spl >= 0 && dlt >= 0 && dlt < C);
+  float sc[U], mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    bool ok = (live >> (u * G + g)) & 1ull;
+    if (u * G + g == slot_new) {  // the new row, from registers
+      kr[u] = knew;
+      vr[u] = vnew;
+      ok = true;
+    }
+    float kf[VD];
+    unpack<false>(kr[u], kf);
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < VD; i++) dot = fmaf(qv[i], kf[i], dot);
+    dot = group_sum<LR>(dot);
+    sc[u] = ok ? dot : -INFINITY;
+    mx = fmaxf(mx, sc[u]);
+  }
+  float m = -INFINITY, l = 0.f, acc[VD];
+#pragma unroll
+  for (int i = 0; i < VD; i++) acc[i] = 0.f;
+  if (mx != -INFINITY) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float p = __expf(sc[u] - mx);
+      l += p;
+      float vf[VD];
+      unpack<false>(vr[u], vf);
+#pragma unroll
+      for (int i = 0; i < VD; i++) acc[i] = fmaf(p, vf[i], acc[i]);
+    }
+    m = mx;
+  }
+#pragma unroll
+  for (int off = LR; off < 64; off <<= 1) {
+    const float mo = __shfl_xor(m, off);
+    const float lo = __shfl_xor(l, off);
+    float ao[VD];
+#pragma unroll
+    for (int i = 0; i < VD; i++) ao[i] = __shfl_xor(acc[i], off);
+    merge_state<VD>(m, l, acc, mo, lo, ao);
+  }
+  if (g == 0) {
+    float* op = out + row_at(out_rows, b, 0) + head * HD + sub * VD;
+    *(float4*)op = l > 0.f ? make_float4(acc[0] / l, acc[1] / l, acc[2] / l, acc[3] / l)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 // Waves per block for a window of up to `max_valid` slots: one wave per
 // `per_wave` slots (180 bf16, 256 fp32) up to 4 waves, and beyond that one
 // wave per 820 slots, at most MAXNW.  With alternating batches, measured on
@@ -533,6 +658,14 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
   const int64_t nq = (int64_t)B * rows;
   if (nq == 0) return MB_OK;
   if (nq * H > INT32_MAX) return fail(ctx, MB_ERR_ARG, "too many queries in one call");
+  if (APPEND && rows == 1 && !ring.bf16 && !ring.wrap && C <= kShortWindow) {
+    const int nunits = (int)(nq * H);
+    hipLaunchKernelGGL(k_attn_short<IN_BF16>, dim3((unsigned)((nunits + 3) / 4)), dim3(256), 0,
+                       ctx->stream, q, q_rows, pos0, nunits, (float*)ring.k, (float*)ring.v,
+                       ring.sp, ring.seq_stride, C, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+    MB_HIP(ctx, hipGetLastError());
+    return MB_OK;
+  }
   const dim3 grid((unsigned)(nq * H));
   if (ring.bf16) {
     constexpr int MAXNW = 16;
