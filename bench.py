@@ -420,6 +420,7 @@ def run_read_ceiling(nbytes=4 << 30, reps=10):
 
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
 
 
 def run_gemm(reps=60, sets=12):
@@ -469,6 +470,44 @@ def run_gemm(reps=60, sets=12):
                         "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
                         "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
             del a, ws, c
+    # The 256-voice decode step's projections as bf16-KV contexts run them:
+    # split-bf16 products (mb_linear_split_dev, three bf16 MFMAs per fp32
+    # product) on weights split once by mb_split_weights_dev.  FLOPs are the
+    # fp32 product's 2 M N K; the matrix cores execute three times that.
+    M = 256
+    for name, N, K in (("qkv", QKV, D), ("o", D, D), ("fc_in", 4 * D, D), ("fc_out", D, 4 * D)):
+        a = torch.randn((M, K), generator=g, device=dev)
+        wxs = []
+        for _ in range(sets):
+            w = torch.randn((K, N), generator=g, device=dev) * 0.02
+            wx = torch.empty(2 * K * N, dtype=torch.bfloat16, device=dev)
+            ctx.split_weights_dev(w.data_ptr(), K, N, wx.data_ptr())
+            wxs.append(wx)
+            del w
+        bias = torch.randn(N, generator=g, device=dev) * 0.02
+        c = torch.empty((M, N), device=dev)
+
+        def call_split(i):
+            ctx.linear_split_dev(M, N, K, a.data_ptr(), K, wxs[i % sets].data_ptr(),
+                                 bias.data_ptr(), c.data_ptr(), N, mb.MB_EPI_STORE)
+
+        for i in range(sets):
+            call_split(i)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(stream)
+        for i in range(reps):
+            call_split(i)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        us = t0.elapsed_time(t1) * 1e3 / reps
+        flops = 2.0 * M * K * N
+        tf = flops / (us * 1e-6) / 1e12
+        out.append({"proj": name, "M": M, "K": K, "N": N, "products": "split-bf16",
+                    "avg_us": round(us, 2), "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
+                    "frac_bf16_mfma_peak": round(3 * tf / BF16_MFMA_PEAK_TFLOPS, 4)})
+        del a, wxs, c
     ctx.close()
     return out
 
