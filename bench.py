@@ -302,8 +302,11 @@ def run_codec(args, B, kv_name, warm=216, frames=24):
 def run_c2(args):
     """Causal prefill attention, B=16, S=512, 12 heads x 64, bf16 q/k/v with
     fp32 accumulation (bf16 MFMA), RoPE at pos = row, ring C=1024 from slot 0.
-    Returns the attention launch's mean time and TFLOP/s (algorithmic FLOPs
-    B*H*4*64*S(S+1)/2, causal half only)."""
+    Returns the attention launch's mean time over `reps` back-to-back
+    launches between two events (as the other legs time their launches) and
+    TFLOP/s (algorithmic FLOPs B*H*4*64*S(S+1)/2, causal half only), and
+    beside it the mean of the same launch timed alone between two events of
+    its own (`isolated_us`, which adds the launch's dispatch gap)."""
     import torch
 
     import mockbird_amd as mb
@@ -334,11 +337,20 @@ def run_c2(args):
                                   q_dtype=mb.MB_DT_BF16)
         b.record(stream)
     torch.cuda.synchronize()
-    us = float(np.mean([a.elapsed_time(b) for a, b in evs]) * 1e3)
+    iso = float(np.mean([a.elapsed_time(b) for a, b in evs]) * 1e3)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(reps):
+        ctx.prefill_attention_dev(0, B, S, q.data_ptr(), p0.data_ptr(), n.data_ptr(), out.data_ptr(),
+                                  q_dtype=mb.MB_DT_BF16)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    us = t0.elapsed_time(t1) * 1e3 / reps
     flops = B * H * 4 * HD * S * (S + 1) / 2
     ctx.close()
     return {"workload": "causal prefill attention B=16 S=512 12x64 bf16 (fp32 acc)",
-            "avg_us": round(us, 2), "gflop": round(flops / 1e9, 3),
+            "avg_us": round(us, 2), "isolated_us": round(iso, 2), "gflop": round(flops / 1e9, 3),
             "tflops": round(flops / (us * 1e-6) / 1e12, 1),
             "frac_bf16_peak": round(flops / (us * 1e-6) / 2.5e15, 4)}
 

@@ -858,18 +858,23 @@ int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void
   // chip: 3072 x 768 at 256 rows, W streamed from HBM, took 11.2-12.0 us on
   // 32-row tiles (384 workgroups) against 11.8-12.3 us on 64-row tiles.
   if (mt == 64 && (int64_t)(N / 64) * ((M + 31) / 32) <= 384) mt = 32;
+  // Two register stages (one 32-deep block in flight) at every tile height:
+  // at 64 and 256 rows every projection shape ran fastest that way (at 256
+  // rows O 4.9 us against 5.4 with 4 stages, fc_in on 32-row tiles 11.2
+  // against 11.7 with 3; deeper prologues spend longer issuing loads before
+  // the first MFMA, and the per-CU load rate, not latency, bounds the rest).
   const uint4* W = (const uint4*)Wx;
   if (lnf) {
     switch (mt) {
-      case 16: return x3_launch<16, 4, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
-      case 32: return x3_launch<32, 3, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+      case 16: return x3_launch<16, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+      case 32: return x3_launch<32, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
       case 48: return x3_launch<48, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
       default: return x3_launch<64, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
     }
   }
   switch (mt) {
-    case 16: return x3_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-    case 32: return x3_launch<32, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    case 16: return x3_launch<16, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    case 32: return x3_launch<32, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
     case 48: return x3_launch<48, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
     default: return x3_launch<64, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
   }

@@ -244,3 +244,33 @@ def test_linear_split_rejects_bad_shapes(ctx):
     with pytest.raises(mb.MbError) as e:
         ctx.split_weights_dev(16, 768, 768, 24)  # Wx not 16-byte aligned
     assert e.value.code == mb.MB_ERR_ARG
+
+
+def test_linear_split_counters_reset_between_calls(ctx):
+    """K = 3072 split-bf16 projections finish their k-split tiles in the
+    kernel: the last split of a tile to count in on the tile's counter adds
+    the partials and sets the counter back to zero.  Ten calls in a row over
+    changing row counts (so the tiles and counters differ from call to call),
+    each checked against the oracle: a counter left non-zero would make a
+    later call skip or double a tile."""
+    torch = pytest.importorskip("torch")
+    dev = torch.device("cuda")
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    N, K = 768, 3072
+    g = np.random.default_rng(77)
+    W = g.standard_normal((K, N), dtype=np.float32) * np.float32(0.02)
+    tW = torch.from_numpy(W).to(dev)
+    tWx = torch.empty(2 * K * N, dtype=torch.bfloat16, device=dev)
+    ctx.split_weights_dev(tW.data_ptr(), K, N, tWx.data_ptr())
+    absW = np.abs(W.astype(np.float64))
+    for M in (256, 100, 256, 64, 9, 300, 256, 128, 17, 256):
+        say(f"split-bf16 K=3072 M={M}")
+        A = g.standard_normal((M, K), dtype=np.float32)
+        tA = torch.from_numpy(A).to(dev)
+        tC = torch.full((M, N), 5.0, device=dev)
+        ctx.linear_split_dev(M, N, K, tA.data_ptr(), K, tWx.data_ptr(), None, tC.data_ptr(), N)
+        torch.cuda.synchronize()
+        want = oracle.gemm(A, W).astype(np.float64)
+        bound = 2.0 ** -16 * (np.abs(A.astype(np.float64)) @ absW) + 2e-6 * (1.0 + np.abs(want))
+        err = np.abs(tC.cpu().numpy().astype(np.float64) - want)
+        assert (err <= bound).all(), (M, float((err / bound).max()))
