@@ -667,9 +667,16 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
     return MB_OK;
   }
   const dim3 grid((unsigned)(nq * H));
+  // Few blocks (one or a few voices) leave most of the chip idle, and each
+  // wave's batches are a chain of load round trips: there, enough waves to
+  // take the whole window in one batch each.
+  const bool few = nq * H <= 128;
+  auto short_waves = [&](int nw, int gu, int maxnw) {
+    return few ? std::max<int>(nw, (int)std::min<int64_t>(maxnw, (max_valid + gu - 1) / gu)) : nw;
+  };
   if (ring.bf16) {
     constexpr int MAXNW = 16;
-    const int nw = unit_waves(max_valid, 180, MAXNW);
+    const int nw = short_waves(unit_waves(max_valid, 180, MAXNW), max_valid <= kAttnShortWindow ? 64 : 32, MAXNW);
     // short windows take 8-load batches, longer ones 4-load batches
     if (max_valid <= kAttnShortWindow)
       hipLaunchKernelGGL((k_attn_unit<true, 8, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
@@ -681,7 +688,7 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
                          ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
   } else {
     constexpr int U = 12, MAXNW = 8;
-    const int nw = unit_waves(max_valid, 256, MAXNW);
+    const int nw = short_waves(unit_waves(max_valid, 256, MAXNW), 4 * U, MAXNW);
     hipLaunchKernelGGL((k_attn_unit<false, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                        ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
                        ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
