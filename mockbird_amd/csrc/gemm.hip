@@ -1374,10 +1374,10 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
   int mt, S;
   stream_shape(M, N, K, true, mt, S);
   switch (mt) {
-    case 16: return stream_launch<16, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
-    case 32: return stream_launch<32, 4, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
-    case 48: return stream_launch<48, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
-    default: return stream_launch<64, 3, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    case 16: return stream_launch<16, 2, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    case 32: return stream_launch<32, 2, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    case 48: return stream_launch<48, 2, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
+    default: return stream_launch<64, 2, true>(ctx, epi, x, ldx, Wg, N, K, bias, Cm, ldc, M, 1, c, d, true);
   }
 }
 
@@ -1390,8 +1390,11 @@ int launch_gemm_ln(mb_ctx* ctx, int epi, const float* x, int64_t ldx, const floa
 // tiles from 96 rows up (stream_shape).  Measured
 // on the decode projections (M = 1, 64, 256; N x K = 2304 x 768, 768 x 768,
 // 3072 x 768, 768 x 3072, 1024 x 768) these choices were the fastest of a
-// sweep over tile, pipeline depth and split; 16-deep chunks in 4 register
-// stages (3 for 48- and 64-row tiles, whose stages are wider).
+// sweep over tile, pipeline depth and split; 16-deep chunks in two register
+// stages (one chunk in flight): re-measured once the loop no longer drained
+// its loads at every iteration, two stages matched or beat three and four
+// (QKV at 256 rows 12.6 against 13.1 us; the codec's 64-voice frame 1.22
+// against 1.25 ms).
 // Larger M: the LDS-tiled kernel with the largest tile that still gives the
 // chip (256 CUs) a block per CU (128 x 128 only from K = 512 up), else the
 // smallest tile.
@@ -1418,10 +1421,10 @@ int launch_gemm(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* 
     int mt, S;
     stream_shape(M, N, K, false, mt, S);
     switch (mt) {
-      case 16: return stream_launch<16, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
-      case 32: return stream_launch<32, 4, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
-      case 48: return stream_launch<48, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
-      default: return stream_launch<64, 3, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      case 16: return stream_launch<16, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      case 32: return stream_launch<32, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      case 48: return stream_launch<48, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
+      default: return stream_launch<64, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr, w_tiled, part, part_cap);
     }
   }
   auto blocks = [&](int bm, int bn) { return (int64_t)((M + bm - 1) / bm) * (N / bn); };
