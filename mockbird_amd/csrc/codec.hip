@@ -52,6 +52,9 @@ struct CodecLayerW {
   const float *ln1_w, *ln1_b, *qkv, *o, *ln2_w, *ln2_b, *f1, *f2, *s1, *s2;
   // norm1 folded into qkv and norm2 into f1 (launch_fold_ln): W', c, d
   const float *qkv_g, *qkv_c, *qkv_d, *f1_g, *f1_c, *f1_d;
+  // bf16 rings: split-bf16 copies of the folded qkv / f1 and of o / f2
+  // (launch_split_w) for the frames whose rows the streaming kernel takes
+  const void *qkv_x = nullptr, *o_x = nullptr, *f1_x = nullptr, *f2_x = nullptr;
 };
 
 struct CodecStageW {
@@ -284,6 +287,19 @@ int codec_resolve(mb_ctx* ctx) {
       const std::string key = "#codec/s" + std::to_string(s) + "l" + std::to_string(i);
       int frc = fold(key + ".qkv", w.qkv, 3 * kD, w.ln1_w, w.ln1_b, w.qkv_g, w.qkv_c, w.qkv_d);
       if (!frc) frc = fold(key + ".f1", w.f1, kFfn, w.ln2_w, w.ln2_b, w.f1_g, w.f1_c, w.f1_d);
+      if (!frc && cs.cfg.kv_dtype == MB_KV_BF16) {
+        auto split = [&](const std::string& name, const float* W, int K, int N, bool tiled,
+                         const void*& wx) {
+          float* p = internal_tensor(ctx, name, (int64_t)K * N);  // 2 K N bf16
+          if (!p) return fail(ctx, MB_ERR_NOMEM, "codec split weights (%s)", name.c_str());
+          wx = p;
+          return launch_split_w(ctx, W, K, N, p, tiled);
+        };
+        frc = split(key + ".qkv.x", w.qkv_g, kD, 3 * kD, true, w.qkv_x);
+        if (!frc) frc = split(key + ".f1.x", w.f1_g, kD, kFfn, true, w.f1_x);
+        if (!frc) frc = split(key + ".o.x", w.o, kD, kD, false, w.o_x);
+        if (!frc) frc = split(key + ".f2.x", w.f2, kFfn, kD, false, w.f2_x);
+      }
       if (frc) return frc;
     }
 
@@ -365,24 +381,43 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
       const CodecLayerW& w = st.layers[i];
       const RingView ring = codec_ring(ctx, cs, cs.layer0[s] + i, s);
       // norm1 / norm2 are folded into the projection where the streaming
-      // kernel takes the rows, else run apart
+      // kernel takes the rows, else run apart; with bf16 rings those rows
+      // take the split-bf16 products
       const bool fold_qkv = gemm_streams(M, 3 * kD), fold_f1 = gemm_streams(M, kFfn);
-      if ((rc = fold_qkv ? launch_gemm_ln(ctx, EPI_STORE, cs.x, kD, w.qkv_g, 3 * kD, kD, w.qkv_c,
-                                          w.qkv_d, nullptr, cs.qkv, 3 * kD, M)
-                         : launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln1_w, w.ln1_b, cs.h, kD, kD)) ||
-          (!fold_qkv &&
-           (rc = launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M))) ||
+      const bool x3 = w.qkv_x && M > kGemvMaxM;
+      const bool x3_d = x3 && gemm_streams(M, kD);
+      auto qkv_proj = [&]() {
+        if (x3 && fold_qkv)
+          return launch_gemm_x3(ctx, EPI_STORE, cs.x, kD, w.qkv_x, 3 * kD, kD, nullptr, cs.qkv,
+                                3 * kD, M, w.qkv_c, w.qkv_d);
+        if (fold_qkv)
+          return launch_gemm_ln(ctx, EPI_STORE, cs.x, kD, w.qkv_g, 3 * kD, kD, w.qkv_c, w.qkv_d,
+                                nullptr, cs.qkv, 3 * kD, M);
+        int r = launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln1_w, w.ln1_b, cs.h, kD, kD);
+        return r ? r : launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M);
+      };
+      auto f1_proj = [&]() {
+        if (x3 && fold_f1)
+          return launch_gemm_x3(ctx, EPI_GELU_ERF, cs.x, kD, w.f1_x, kFfn, kD, nullptr, cs.ffn,
+                                kFfn, M, w.f1_c, w.f1_d);
+        if (fold_f1)
+          return launch_gemm_ln(ctx, EPI_GELU_ERF, cs.x, kD, w.f1_g, kFfn, kD, w.f1_c, w.f1_d,
+                                nullptr, cs.ffn, kFfn, M);
+        int r = launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln2_w, w.ln2_b, cs.h, kD, kD);
+        return r ? r : launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M);
+      };
+      if ((rc = qkv_proj()) ||
           (rc = launch_ring_write(ctx, ring, B, n, cs.qkv, MB_DT_F32, dense_rows(3 * kD, n), pos,
                                   nrow, cs.q, MB_DT_F32, dense_rows(kD, n))) ||
           (rc = launch_window_attention(ctx, ring, B, n, cs.q, dense_rows(kD, n), pos, nrow,
                                         cs.att, dense_rows(kD, n))) ||
-          (rc = launch_gemm(ctx, EPI_SCALE_ADD, cs.att, kD, w.o, kD, kD, w.s1, cs.x, kD, M)) ||
-          (rc = fold_f1 ? launch_gemm_ln(ctx, EPI_GELU_ERF, cs.x, kD, w.f1_g, kFfn, kD, w.f1_c,
-                                         w.f1_d, nullptr, cs.ffn, kFfn, M)
-                        : launch_layernorm(ctx, cs.x, kD, nullptr, M, w.ln2_w, w.ln2_b, cs.h, kD, kD)) ||
-          (!fold_f1 &&
-           (rc = launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M))) ||
-          (rc = launch_gemm(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2, kD, kFfn, w.s2, cs.x, kD, M)))
+          (rc = x3_d ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.att, kD, w.o_x, kD, kD, w.s1, cs.x, kD,
+                                      M, nullptr, nullptr)
+                     : launch_gemm(ctx, EPI_SCALE_ADD, cs.att, kD, w.o, kD, kD, w.s1, cs.x, kD, M)) ||
+          (rc = f1_proj()) ||
+          (rc = x3_d ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2_x, kD, kFfn, w.s2, cs.x,
+                                      kD, M, nullptr, nullptr)
+                     : launch_gemm(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2, kD, kFfn, w.s2, cs.x, kD, M)))
         return rc;
     }
     const int out_w = s == kStages - 1 ? kD : kRvqOut;
