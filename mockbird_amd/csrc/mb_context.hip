@@ -167,6 +167,16 @@ int mb_create(const mb_config* cfg, mb_ctx** out) {
   do {
     hipError_t e = hipSetDevice(cfg->device);
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipSetDevice"); break; }
+    {
+      int cus = 0, xccs = 0;
+      if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, cfg->device) ==
+              hipSuccess &&
+          hipDeviceGetAttribute(&xccs, hipDeviceAttributeNumberOfXccs, cfg->device) == hipSuccess &&
+          xccs > 0 && cus >= xccs) {
+        ctx->xcds = xccs;
+        ctx->cus_per_xcd = cus / xccs;
+      }
+    }
     if ((rc = noalloc_init(ctx))) break;
     e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
     if (e != hipSuccess) { rc = hip_fail(ctx, e, "hipStreamCreate"); break; }

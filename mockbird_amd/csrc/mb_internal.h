@@ -106,6 +106,10 @@ constexpr int kFoldMaxM = 1024;
 struct mb_ctx {
   mb_config cfg{};
   int device = 0;
+  // XCDs of the device and CUs per XCD (hipDeviceAttributeNumberOfXccs,
+  // MultiprocessorCount / that); cus_per_xcd stays 0 when unknown
+  int xcds = 8;
+  int cus_per_xcd = 0;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   std::string err;

@@ -29,19 +29,34 @@ constexpr int KT = 64;    // slots per K/V tile
 constexpr int QT = 64;    // query rows per workgroup
 constexpr int FPAD = 68;  // fp32 LDS row stride (272 B)
 
-// Workgroup -> (sequence, head, query tile).  The dispatcher deals
-// consecutive workgroups round-robin to the 8 XCDs, so workgroup L lands on
-// XCD L % 8 and runs in the order L / 8 there.  Query tile t of a causal
-// prefill costs about t + 1 K/V tiles; numbering the work latest tile first,
-// all (sequence, head) pairs of one tile before the next, gives every XCD an
-// equal share of every tile length and starts the longest ones first.  (With
-// the tile index as the fastest grid coordinate, an 8-tile grid would send
-// all of tile t to one XCD.)
-__device__ __forceinline__ void work_item(int& b, int& h, int& qtile) {
+// Workgroup -> (sequence, head, query tile).  Query tile t of a causal
+// prefill costs about t + 1 K/V tiles, so the work is numbered latest tile
+// first, all (sequence, head) pairs of one tile before the next: every XCD
+// gets an equal share of every tile length and the longest start first.
+// (With the tile index as the fastest grid coordinate, an 8-tile grid would
+// send all of tile t to one XCD.)
+//
+// The dispatcher deals consecutive workgroups round-robin to the nxcd XCDs
+// (workgroup L to XCD L % nxcd, as that XCD's (L / nxcd)-th) and, within an
+// XCD, round-robin to its cpx CUs: when a launch fits at once, a CU holds
+// the XCD's workgroups c, c + cpx, c + 2 cpx, ...  Handing out the work in
+// rounds of cpx, every second full round in reverse (a snake), pairs the
+// long tiles with short ones on each CU.  Work item g = nxcd * j + x stays
+// on XCD x, so a (sequence, head) pair's tiles share one L2 whenever the
+// pair count is a multiple of nxcd.  cpx = 0 hands out the work in order.
+__device__ __forceinline__ void work_item(int& b, int& h, int& qtile, int nxcd, int cpx) {
   const int64_t L = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
   const int64_t pairs = (int64_t)gridDim.y * gridDim.z;
-  qtile = gridDim.x - 1 - (int)(L / pairs);
-  const int64_t hb = L % pairs;
+  int64_t g = L;
+  if (cpx > 0) {
+    const int64_t total = pairs * gridDim.x;
+    const int64_t x = L % nxcd, i = L / nxcd, nx = (total - x + nxcd - 1) / nxcd;
+    const int64_t r = i / cpx, c = i % cpx;
+    const int64_t j = ((r & 1) && (r + 1) * cpx <= nx) ? r * cpx + (cpx - 1 - c) : i;
+    g = nxcd * j + x;
+  }
+  qtile = gridDim.x - 1 - (int)(g / pairs);
+  const int64_t hb = g % pairs;
   h = (int)(hb % gridDim.y);
   b = (int)(hb / gridDim.y);
 }
@@ -105,6 +120,18 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
+// Maximum over the four lanes of a column, with plain v_max_f32: fmaxf
+// wraps both values that come out of each cross-lane swap in a canonicalising
+// max (four more instructions per column); the plain instruction returns the
+// same maximum for every input but signalling NaNs, which no score is.
+__device__ __forceinline__ float col_max_plain(float x) {
+  return col_reduce(x, [](float u, float v) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(u), "v"(v));
+    return r;
+  });
+}
+
 // Element offset of (slot row, 8-dim chunk x) in a swizzled 64 x 64 tile.
 __device__ __forceinline__ int swz(int row, int x) { return row * HD + ((x ^ (row & 7)) << 3); }
 
@@ -156,7 +183,8 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     const uint16_t* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, const uint16_t* __restrict__ ring_k,
     const uint16_t* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
+    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows, int nxcd,
+    int cpx) {
   constexpr int QB = BQ / (16 * NW);  // 16-query blocks per wave
   constexpr int WQ = 16 * QB;         // queries per wave
   constexpr int PIECES = KT / (8 * NW);  // 1 KB pieces of K (and of V) per wave per tile
@@ -170,7 +198,7 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int qcol = lane & 15, grp = lane >> 4;
   int b, h, qtile;
-  work_item(b, h, qtile);
+  work_item(b, h, qtile, nxcd, cpx);
   const int n = n_rows[b];
   if (qtile * BQ >= n) return;  // uniform per workgroup, before any barrier
   const int64_t p0 = pos0[b];
@@ -260,6 +288,7 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     lsum[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     m[qi] = -INFINITY;
   }
+  bool started = false;  // a tile of this wave has set m
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.f;
@@ -304,27 +333,17 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
         for (int kc = 0; kc < 2; kc++) ka[sb][kc] = kfrag(sb, kc);
       asm volatile("" ::: "memory");
     }
-    // per slot: after every query of this wave, or live for every one of them
-    // (rel <= crel_lo <= crel_hi makes the unsigned difference exact)
+    // Per slot (lane): not after every query of this wave (else it is in
+    // the causal upper triangle: a tile of such slots only is skipped), and
+    // not live for every one of them (`partial`; rel <= crel_lo <= crel_hi
+    // makes the unsigned difference exact).  Only the 16-slot blocks holding
+    // a partial slot apply the per-slot window test.
     const int32_t rel_l = praw < 0 || t0 + lane >= kv_end ? kRelEmpty : praw - ref;
-    if (__ballot(rel_l <= crel_hi) == 0) continue;  // the causal upper triangle
-    const bool all_live =
-        __ballot(!(rel_l <= crel_lo && (uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W)) == 0;
+    if (__ballot(rel_l <= crel_hi) == 0) continue;
+    const uint64_t partial =
+        __ballot(!(rel_l <= crel_lo && (uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W));
 
-    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
-    f32x4_t s[QB][4];
-#pragma unroll
-    for (int sb = 0; sb < 4; sb++)
-#pragma unroll
-      for (int qi = 0; qi < QB; qi++) {
-        s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 2; kc++)
-          s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(QB > 1 ? ka[sb][kc] : kfrag(sb, kc),
-                                                              qb[qi][kc], s[qi][sb], 0, 0, 0);
-      }
-    // V^T fragments (with registers to spare, now, so their LDS latency runs
-    // under the softmax)
+    // the A operand of P V for 32-slot chunk c and dim block d
     auto vfrag = [&](int c, int d) {
       const int dim = d * 16 + tdim;
       const int e0 = swz(c * 32 + trow, dim >> 3) + (dim & 7);
@@ -333,96 +352,137 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
       const bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)&Vs[buf][e1]);
       return bf16x8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
     };
-    bf16x8_t va[2][4];
-    if constexpr (QB > 1) {
+    {
+      constexpr int NC = 2;  // 32-slot chunks of the tile
+      // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
+      f32x4_t s[QB][2 * NC];
 #pragma unroll
-      for (int c = 0; c < 2; c++)
+      for (int sb = 0; sb < 2 * NC; sb++)
 #pragma unroll
-        for (int d = 0; d < 4; d++) va[c][d] = vfrag(c, d);
-    }
-    if (!all_live) {
-      // the wave's own row of relative positions: lane l reads back the four
-      // slots sb*16 + 4*grp + j its score elements stand for
-      Rl[wave][lane] = rel_l;
+        for (int qi = 0; qi < QB; qi++) {
+          s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int sb = 0; sb < 4; sb++) {
-        const int4 pv = *(const int4*)&Rl[wave][sb * 16 + grp * 4];
-        const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
+          for (int kc = 0; kc < 2; kc++)
+            s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                QB > 1 ? ka[sb][kc] : kfrag(sb, kc), qb[qi][kc], s[qi][sb], 0, 0, 0);
+        }
+      // (with registers to spare, the V^T fragments are read now, so their
+      // LDS latency runs under the softmax)
+      bf16x8_t va[NC][4];
+      if constexpr (QB > 1) {
 #pragma unroll
-        for (int j = 0; j < 4; j++)
+        for (int c = 0; c < NC; c++)
 #pragma unroll
-          for (int qi = 0; qi < QB; qi++)
-            if ((uint32_t)(crel[qi] - pj[j]) >= (uint32_t)W) s[qi][sb][j] = -INFINITY;
+          for (int d = 0; d < 4; d++) va[c][d] = vfrag(c, d);
       }
-    }
-    // Online softmax in log2 units.  The running maximum m only moves when a
-    // tile's maximum exceeds it by more than 8 (the conditional rescaling of
-    // FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
-    // rescale of the accumulators, a wave-uniform branch taken for all query
-    // blocks at once, is rare after the first tiles.  The result is the same
-    // softmax: acc and the weight sum always share one m.
-    float mt[QB];
-    bool grow[QB], any = false;
+      if (partial) {  // uniform
+        // the wave's own row of relative positions: lane l's four score
+        // elements of block sb stand for slots sb*16 + 4*grp + j
+        Rl[wave][lane] = rel_l;
 #pragma unroll
-    for (int qi = 0; qi < QB; qi++) {
-      float x = -INFINITY;
+        for (int sb = 0; sb < 2 * NC; sb++) {
+          if ((partial >> (16 * sb)) & 0xFFFFu) {  // uniform
+            const int4 pv = *(const int4*)&Rl[wave][sb * 16 + grp * 4];
+            const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
 #pragma unroll
-      for (int sb = 0; sb < 4; sb++)
+            for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
-      mt[qi] = col_max(x) * kScoreLog2;
-      grow[qi] = mt[qi] > m[qi] + 8.f;
-      any = any || grow[qi];
-    }
-    if (__ballot(any)) {
+              for (int qi = 0; qi < QB; qi++)
+                if ((uint32_t)(crel[qi] - pj[j]) >= (uint32_t)W) s[qi][sb][j] = -INFINITY;
+          }
+        }
+      }
+      // Online softmax in log2 units.  The running maximum m only moves when
+      // a tile's maximum exceeds it by more than 8 (the conditional rescaling
+      // of FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
+      // rescale of the accumulators, a wave-uniform branch taken for all
+      // query blocks at once, is rare after the first tiles (and skipped on
+      // the wave's first tile, where acc and the weight sum are still zero).
+      // The result is the same softmax: acc and the weight sum always share
+      // one m.
+      float mt[QB];
+      bool grow[QB], any = false;
 #pragma unroll
       for (int qi = 0; qi < QB; qi++) {
-        const float mn = grow[qi] ? mt[qi] : m[qi];
-        const float scale = grow[qi] ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
-        m[qi] = mn;
+        float x = -INFINITY;
 #pragma unroll
-        for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
-        lsum[qi] *= scale;
+        for (int sb = 0; sb < 2 * NC; sb++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
+        mt[qi] = col_max_plain(x) * kScoreLog2;
+        grow[qi] = mt[qi] > m[qi] + 8.f;
+        any = any || grow[qi];
       }
-    }
-    bf16x8_t pb[QB][2];
+      if (!started) {
 #pragma unroll
-    for (int qi = 0; qi < QB; qi++) {
-      const float mu = m[qi] == -INFINITY ? 0.f : m[qi];
+        for (int qi = 0; qi < QB; qi++) m[qi] = grow[qi] ? mt[qi] : m[qi];
+        started = true;
+      } else if (__ballot(any)) {
 #pragma unroll
-      for (int c = 0; c < 2; c++)
+        for (int qi = 0; qi < QB; qi++) {
+          const float mn = grow[qi] ? mt[qi] : m[qi];
+          const float scale = grow[qi] ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
+          m[qi] = mn;
 #pragma unroll
-        for (int e = 0; e < 8; e++)
-          pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, -mu));
-    }
-    // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those slots][queries].
-    // The weight sum is one more MFMA with an all-ones A, so it adds the same
-    // rounded weights the products use.
+          for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
+          lsum[qi] *= scale;
+        }
+      }
+      bf16x8_t pb[QB][NC];
 #pragma unroll
-    for (int c = 0; c < 2; c++) {
+      for (int qi = 0; qi < QB; qi++) {
+        const float mu = m[qi] == -INFINITY ? 0.f : m[qi];
 #pragma unroll
-      for (int d = 0; d < 4; d++) {
-        const bf16x8_t a = QB > 1 ? va[c][d] : vfrag(c, d);
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+          for (int e = 0; e < 8; e++)
+            pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(
+                fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, -mu));
+      }
+      // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those
+      // slots][queries].  The weight sum is one more MFMA with an all-ones A,
+      // so it adds the same rounded weights the products use.
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+          const bf16x8_t a = QB > 1 ? va[c][d] : vfrag(c, d);
+#pragma unroll
+          for (int qi = 0; qi < QB; qi++)
+            acc[qi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][c], acc[qi][d], 0, 0, 0);
+        }
 #pragma unroll
         for (int qi = 0; qi < QB; qi++)
-          acc[qi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][c], acc[qi][d], 0, 0, 0);
+          lsum[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qi][c], lsum[qi], 0, 0, 0);
       }
-#pragma unroll
-      for (int qi = 0; qi < QB; qi++)
-        lsum[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qi][c], lsum[qi], 0, 0, 0);
     }
   }
+  // The output goes through LDS so that every store writes whole rows: each
+  // wave stages its WQ x 64 fp32 block (rows FPAD floats apart) in the K/V
+  // buffers, which the barrier frees, and reads it back 16 lanes per row.
+  // The stores are non-temporal: this kernel never reads the rows again, and
+  // rows kept out of the L2 leave nothing to write back when the kernel
+  // ends (16 sequences x 512 rows: 18.9 us with the former 64-byte pieces
+  // through the L2, 16.9 us whole rows non-temporal; non-temporal 64-byte
+  // pieces gain as much there but lose 4 us at 64 sequences).
+  static_assert((NW / 2) * WQ * FPAD * 4 <= (int)sizeof(Ks), "output stage");
+  __syncthreads();
+  float* stage = (wave < NW / 2 ? (float*)&Ks[0][0] : (float*)&Vs[0][0]) + (wave % (NW / 2)) * WQ * FPAD;
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
-    const int r = rw + qi * 16 + qcol;
-    if (r >= n) continue;
     const float l = lsum[qi][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    float* op = out + row_at(out_rows, b, r) + h * HD;
 #pragma unroll
     for (int d = 0; d < 4; d++)
-      *(float4*)(op + d * 16 + grp * 4) = make_float4(acc[qi][d][0] * inv, acc[qi][d][1] * inv,
-                                                      acc[qi][d][2] * inv, acc[qi][d][3] * inv);
+      *(f32x4_t*)&stage[(qi * 16 + qcol) * FPAD + d * 16 + grp * 4] = acc[qi][d] * inv;
+  }
+  const int64_t rs = out_rows.row_stride;
+  float* ob = out + row_at(out_rows, b, rw) + h * HD + (lane >> 4) * rs + (lane & 15) * 4;
+#pragma unroll
+  for (int i = 0; i < WQ / 4; i++) {
+    const int row = i * 4 + (lane >> 4);
+    const f32x4_t v = *(const f32x4_t*)&stage[row * FPAD + (lane & 15) * 4];
+    if (rw + row < n) __builtin_nontemporal_store(v, (f32x4_t*)(ob + i * 4 * rs));
   }
 }
 #undef MB_WAIT_VMCNT
@@ -447,7 +507,7 @@ __global__ __launch_bounds__(256) void k_flash_f32(
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int qcol = lane & 15, grp = lane >> 4;
   int b, h, qtile;
-  work_item(b, h, qtile);
+  work_item(b, h, qtile, 8, 0);
   const int n = n_rows[b];
   if (qtile * QT >= n) return;
   const int r = qtile * QT + wave * 16 + qcol;
@@ -865,7 +925,8 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
                        dim3((unsigned)((rows_max + BQ - 1) / BQ), nh, (unsigned)B),
                        dim3(64 * kFlashWaves), 0, ctx->stream, (const uint16_t*)q, q_rows,
                        pos0, n_rows, (const uint16_t*)ring.k, (const uint16_t*)ring.v, ring.sp,
-                       ring.seq_stride, ring.C, ring.window, out, out_rows);
+                       ring.seq_stride, ring.C, ring.window, out, out_rows, ctx->xcds,
+                       ctx->cus_per_xcd);
   else if (ring.bf16)
     hipLaunchKernelGGL(k_flash_f32<true>, grid, dim3(256), 0, ctx->stream, (const float*)q, q_rows,
                        pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.window,
