@@ -16,6 +16,8 @@
 // window rule of kernels-decode.ts:608-611, which implies p <= cur: causal).
 // Slots are visited in physical order, 64 at a time, up to
 // min(last position in the tile + 1, C).
+#include <type_traits>
+
 #include "kv_types.h"
 #include "mb_internal.h"
 
@@ -114,6 +116,7 @@ constexpr int BQ = 128;  // query rows per workgroup of the bf16 kernel
 constexpr int kFlashWaves = 4;  // waves per workgroup of the bf16 kernel
 constexpr int NBUF = 3;  // K/V tile buffers
 constexpr float kScoreLog2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
+constexpr float kInvScoreLog2 = 8.f * 0.6931471805599453f;   // its inverse, sqrt(64) * ln(2)
 constexpr int32_t kRelEmpty = INT32_MAX;  // relative position of an empty slot
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -236,6 +239,7 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   const int32_t ref = first < INT32_MAX ? (int32_t)first : INT32_MAX;
   const int32_t ex = (int32_t)min(first - ref, (int64_t)1 << 30);
   const int crel_lo = wave * WQ + ex, crel_hi = min(rw + WQ - 1, n - 1) - qtile * BQ + ex;
+  const int lane_lim = kv_end - lane;  // t0 >= lane_lim: this lane's slot is past the end
   int crel[QB];
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) crel[qi] = crel_lo + qi * 16 + qcol;
@@ -280,15 +284,18 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   };
 
   f32x4_t acc[QB][4], lsum[QB];
-  float m[QB];
+  // running maximum m (log2 units) per query column, with the rescale
+  // threshold (m + 8 in raw score units) and the exponent's offset -m (0
+  // while m = -inf)
+  float m[QB], lim[QB], mneg[QB];
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
 #pragma unroll
     for (int d = 0; d < 4; d++) acc[qi][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     lsum[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    m[qi] = -INFINITY;
+    m[qi] = lim[qi] = -INFINITY;
+    mneg[qi] = 0.f;
   }
-  bool started = false;  // a tile of this wave has set m
   bf16x8_t ones;
 #pragma unroll
   for (int i = 0; i < 8; i++) ones[i] = (__bf16)1.f;
@@ -297,14 +304,15 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   // which the transposed read turns into V^T[16d + r][those 4 slots]
   const int trow = grp * 4 + (qcol >> 2), tdim = (qcol & 3) * 4;
 
-  // the first tile and q, then every later tile two tiles ahead of its use
-  issue(0, 0);
-  MB_WAIT_VMCNT(0);
-  int buf = 0;
-  for (int t0 = 0; t0 < kv_end; t0 += KT, buf = buf == NBUF - 1 ? 0 : buf + 1) {
+  // One tile: wait for its loads, publish it, refill the buffer read two
+  // tiles ago, then scores, softmax and P V.  FIRST = the wave's first tile
+  // (tile 0), which needs no rescale: acc and the weight sum are still zero.
+  auto step = [&](int t0, auto bufc, auto first) {
+    constexpr int buf = decltype(bufc)::value;  // a constant: LDS offsets fold into the reads
+    constexpr bool FIRST = decltype(first)::value;
     // this tile's loads are done once at most the next tile's are
     // outstanding (vmcnt counts in issue order)
-    if (t0 > 0) {
+    if (!FIRST) {
       if (t0 + KT < kv_end)
         MB_WAIT_VMCNT(LOADS);
       else
@@ -313,9 +321,9 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     // every wave's part of this tile is in LDS, and every wave is done with
     // the buffer the next issue overwrites (read two tiles ago)
     __syncthreads();
-    if (t0 == 0 && KT < kv_end) issue(KT, 1);  // uniform per workgroup
-    if (t0 + 2 * KT < kv_end) issue(t0 + 2 * KT, buf == 0 ? NBUF - 1 : buf - 1);
-    if (!wave_rows) continue;
+    if (FIRST && KT < kv_end) issue(KT, 1);  // uniform per workgroup
+    if (t0 + 2 * KT < kv_end) issue(t0 + 2 * KT, (buf + NBUF - 1) % NBUF);
+    if (!wave_rows) return;
     // The slot positions, then (with registers to spare: two query blocks
     // per wave) the K fragments (A of the score MFMA = K[slot sb*16 +
     // qcol][dims 32 kc + 8 grp ..]), issued before the classification so
@@ -338,12 +346,28 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     // not live for every one of them (`partial`; rel <= crel_lo <= crel_hi
     // makes the unsigned difference exact).  Only the 16-slot blocks holding
     // a partial slot apply the per-slot window test.
-    const int32_t rel_l = praw < 0 || t0 + lane >= kv_end ? kRelEmpty : praw - ref;
-    if (__ballot(rel_l <= crel_hi) == 0) continue;
+    const int32_t rel_l = praw < 0 || t0 >= lane_lim ? kRelEmpty : praw - ref;
+    if (__ballot(rel_l <= crel_hi) == 0) return;
+    // (every lane is active here, so the complement of a ballot is the
+    // ballot of the complement)
     const uint64_t partial =
-        __ballot(!(rel_l <= crel_lo && (uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W));
+        ~(__ballot(rel_l <= crel_lo) & __ballot((uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W));
 
-    // the A operand of P V for 32-slot chunk c and dim block d
+    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
+    f32x4_t s[QB][4];
+#pragma unroll
+    for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+      for (int qi = 0; qi < QB; qi++) {
+        s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
+          s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(QB > 1 ? ka[sb][kc] : kfrag(sb, kc),
+                                                              qb[qi][kc], s[qi][sb], 0, 0, 0);
+      }
+    // The A operand of P V for 32-slot chunk c and dim block d; with
+    // registers to spare they are read now, so their LDS latency runs under
+    // the softmax.
     auto vfrag = [&](int c, int d) {
       const int dim = d * 16 + tdim;
       const int e0 = swz(c * 32 + trow, dim >> 3) + (dim & 7);
@@ -352,136 +376,140 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
       const bf16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)&Vs[buf][e1]);
       return bf16x8_t{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
     };
-    {
-      constexpr int NC = 2;  // 32-slot chunks of the tile
-      // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
-      f32x4_t s[QB][2 * NC];
+    bf16x8_t va[2][4];
+    if constexpr (QB > 1) {
 #pragma unroll
-      for (int sb = 0; sb < 2 * NC; sb++)
+      for (int c = 0; c < 2; c++)
 #pragma unroll
-        for (int qi = 0; qi < QB; qi++) {
-          s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < 4; d++) va[c][d] = vfrag(c, d);
+    }
+    if (partial) {  // uniform
+      // the wave's own row of relative positions: lane l's four score
+      // elements of block sb stand for slots sb*16 + 4*grp + j
+      Rl[wave][lane] = rel_l;
 #pragma unroll
-          for (int kc = 0; kc < 2; kc++)
-            s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                QB > 1 ? ka[sb][kc] : kfrag(sb, kc), qb[qi][kc], s[qi][sb], 0, 0, 0);
+      for (int sb = 0; sb < 4; sb++) {
+        if ((partial >> (16 * sb)) & 0xFFFFu) {  // uniform
+          const int4 pv = *(const int4*)&Rl[wave][sb * 16 + grp * 4];
+          const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
+#pragma unroll
+          for (int j = 0; j < 4; j++)
+#pragma unroll
+            for (int qi = 0; qi < QB; qi++)
+              if ((uint32_t)(crel[qi] - pj[j]) >= (uint32_t)W) s[qi][sb][j] = -INFINITY;
         }
-      // (with registers to spare, the V^T fragments are read now, so their
-      // LDS latency runs under the softmax)
-      bf16x8_t va[NC][4];
-      if constexpr (QB > 1) {
-#pragma unroll
-        for (int c = 0; c < NC; c++)
-#pragma unroll
-          for (int d = 0; d < 4; d++) va[c][d] = vfrag(c, d);
-      }
-      if (partial) {  // uniform
-        // the wave's own row of relative positions: lane l's four score
-        // elements of block sb stand for slots sb*16 + 4*grp + j
-        Rl[wave][lane] = rel_l;
-#pragma unroll
-        for (int sb = 0; sb < 2 * NC; sb++) {
-          if ((partial >> (16 * sb)) & 0xFFFFu) {  // uniform
-            const int4 pv = *(const int4*)&Rl[wave][sb * 16 + grp * 4];
-            const int32_t pj[4] = {pv.x, pv.y, pv.z, pv.w};
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-#pragma unroll
-              for (int qi = 0; qi < QB; qi++)
-                if ((uint32_t)(crel[qi] - pj[j]) >= (uint32_t)W) s[qi][sb][j] = -INFINITY;
-          }
-        }
-      }
-      // Online softmax in log2 units.  The running maximum m only moves when
-      // a tile's maximum exceeds it by more than 8 (the conditional rescaling
-      // of FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
-      // rescale of the accumulators, a wave-uniform branch taken for all
-      // query blocks at once, is rare after the first tiles (and skipped on
-      // the wave's first tile, where acc and the weight sum are still zero).
-      // The result is the same softmax: acc and the weight sum always share
-      // one m.
-      float mt[QB];
-      bool grow[QB], any = false;
-#pragma unroll
-      for (int qi = 0; qi < QB; qi++) {
-        float x = -INFINITY;
-#pragma unroll
-        for (int sb = 0; sb < 2 * NC; sb++)
-#pragma unroll
-          for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
-        mt[qi] = col_max_plain(x) * kScoreLog2;
-        grow[qi] = mt[qi] > m[qi] + 8.f;
-        any = any || grow[qi];
-      }
-      if (!started) {
-#pragma unroll
-        for (int qi = 0; qi < QB; qi++) m[qi] = grow[qi] ? mt[qi] : m[qi];
-        started = true;
-      } else if (__ballot(any)) {
-#pragma unroll
-        for (int qi = 0; qi < QB; qi++) {
-          const float mn = grow[qi] ? mt[qi] : m[qi];
-          const float scale = grow[qi] ? __builtin_amdgcn_exp2f(m[qi] - mn) : 1.f;
-          m[qi] = mn;
-#pragma unroll
-          for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
-          lsum[qi] *= scale;
-        }
-      }
-      bf16x8_t pb[QB][NC];
-#pragma unroll
-      for (int qi = 0; qi < QB; qi++) {
-        const float mu = m[qi] == -INFINITY ? 0.f : m[qi];
-#pragma unroll
-        for (int c = 0; c < NC; c++)
-#pragma unroll
-          for (int e = 0; e < 8; e++)
-            pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(
-                fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, -mu));
-      }
-      // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those
-      // slots][queries].  The weight sum is one more MFMA with an all-ones A,
-      // so it adds the same rounded weights the products use.
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-#pragma unroll
-        for (int d = 0; d < 4; d++) {
-          const bf16x8_t a = QB > 1 ? va[c][d] : vfrag(c, d);
-#pragma unroll
-          for (int qi = 0; qi < QB; qi++)
-            acc[qi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][c], acc[qi][d], 0, 0, 0);
-        }
-#pragma unroll
-        for (int qi = 0; qi < QB; qi++)
-          lsum[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qi][c], lsum[qi], 0, 0, 0);
       }
     }
+    // Online softmax in log2 units.  The running maximum m only moves when a
+    // tile's maximum exceeds it by more than 8 (the conditional rescaling of
+    // FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
+    // rescale of the accumulators, a wave-uniform branch taken for all query
+    // blocks at once, is rare after the first tiles.  The result is the same
+    // softmax: acc and the weight sum always share one m.
+    float xm[QB];       // column maximum of the raw scores
+    uint64_t grow = 0;  // lanes whose column maximum moves
+#pragma unroll
+    for (int qi = 0; qi < QB; qi++) {
+      float x = -INFINITY;
+#pragma unroll
+      for (int sb = 0; sb < 4; sb++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
+      xm[qi] = col_max_plain(x);
+      grow |= __ballot(xm[qi] > lim[qi]);
+    }
+    if (grow) {  // uniform
+#pragma unroll
+      for (int qi = 0; qi < QB; qi++) {
+        if (xm[qi] > lim[qi]) {
+          const float mt = xm[qi] * kScoreLog2;
+          if constexpr (!FIRST) {
+            const float scale = __builtin_amdgcn_exp2f(m[qi] - mt);
+#pragma unroll
+            for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
+            lsum[qi] *= scale;
+          }
+          m[qi] = mt;
+          lim[qi] = (mt + 8.f) * kInvScoreLog2;
+          mneg[qi] = -mt;
+        }
+      }
+    }
+    bf16x8_t pb[QB][2];
+#pragma unroll
+    for (int qi = 0; qi < QB; qi++)
+#pragma unroll
+      for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(
+              fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, mneg[qi]));
+    // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those
+    // slots][queries].  The weight sum is one more MFMA with an all-ones A,
+    // so it adds the same rounded weights the products use.
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        const bf16x8_t a = QB > 1 ? va[c][d] : vfrag(c, d);
+#pragma unroll
+        for (int qi = 0; qi < QB; qi++)
+          acc[qi][d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[qi][c], acc[qi][d], 0, 0, 0);
+      }
+#pragma unroll
+      for (int qi = 0; qi < QB; qi++)
+        lsum[qi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[qi][c], lsum[qi], 0, 0, 0);
+    }
+  };
+  // the first tile and q, then every later tile two tiles ahead of its use
+  // (kv_end >= 1: the workgroup has rows)
+  using std::integral_constant;
+  issue(0, 0);
+  MB_WAIT_VMCNT(0);
+  step(0, integral_constant<int, 0>{}, std::true_type{});
+  for (int t0 = KT; t0 < kv_end; t0 += NBUF * KT) {
+    static_assert(NBUF == 3, "the loop is unrolled by the buffer count");
+    step(t0, integral_constant<int, 1>{}, std::false_type{});
+    if (t0 + KT >= kv_end) break;
+    step(t0 + KT, integral_constant<int, 2>{}, std::false_type{});
+    if (t0 + 2 * KT >= kv_end) break;
+    step(t0 + 2 * KT, integral_constant<int, 0>{}, std::false_type{});
   }
-  // The output goes through LDS so that every store writes whole rows: each
-  // wave stages its WQ x 64 fp32 block (rows FPAD floats apart) in the K/V
-  // buffers, which the barrier frees, and reads it back 16 lanes per row.
-  // The stores are non-temporal: this kernel never reads the rows again, and
-  // rows kept out of the L2 leave nothing to write back when the kernel
-  // ends (16 sequences x 512 rows: 18.9 us with the former 64-byte pieces
-  // through the L2, 16.9 us whole rows non-temporal; non-temporal 64-byte
-  // pieces gain as much there but lose 4 us at 64 sequences).
-  static_assert((NW / 2) * WQ * FPAD * 4 <= (int)sizeof(Ks), "output stage");
-  __syncthreads();
-  float* stage = (wave < NW / 2 ? (float*)&Ks[0][0] : (float*)&Vs[0][0]) + (wave % (NW / 2)) * WQ * FPAD;
+  const int buf = ((kv_end + KT - 1) / KT) % NBUF;  // the buffer a next tile would fill
+  // The output goes through LDS so that every store writes whole rows.
+  // After the last tile's barrier no wave touches two of the three K/V
+  // buffers again (the one before the last tile, and the one the next tile
+  // would have filled: no load is in flight), so each wave stages its WQ x
+  // 64 fp32 block in a quarter of their 32 KB without waiting for the
+  // others, 16-byte chunks of row r XOR-swizzled by r mod 16 (conflict-free
+  // both ways), and reads it back 16 lanes per row.  The stores are
+  // non-temporal: this kernel never reads the rows again, and rows kept out
+  // of the L2 leave nothing to write back when the kernel ends (16
+  // sequences x 512 rows: 18.9 us with 64-byte pieces through the L2, 16.9
+  // us whole rows non-temporal; non-temporal 64-byte pieces gain as much
+  // there but lose 4 us at 64 sequences).
+  static_assert(BQ * HD * 4 == 4 * KT * HD * 2 && NW % 4 == 0, "output stage");
+  float* stage;
+  {
+    const int f = (wave / (NW / 4)) >> 1;            // which free buffer
+    const int fb = f == 0 ? buf : (buf == NBUF - 1 ? 0 : buf + 1);
+    uint16_t* region = (wave / (NW / 4)) & 1 ? &Vs[fb][0] : &Ks[fb][0];
+    stage = (float*)region + (wave % (NW / 4)) * WQ * HD;
+  }
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
     const float l = lsum[qi][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int d = 0; d < 4; d++)
-      *(f32x4_t*)&stage[(qi * 16 + qcol) * FPAD + d * 16 + grp * 4] = acc[qi][d] * inv;
+      *(f32x4_t*)&stage[(qi * 16 + qcol) * HD + (((4 * d + grp) ^ qcol) << 2)] = acc[qi][d] * inv;
   }
   const int64_t rs = out_rows.row_stride;
   float* ob = out + row_at(out_rows, b, rw) + h * HD + (lane >> 4) * rs + (lane & 15) * 4;
 #pragma unroll
   for (int i = 0; i < WQ / 4; i++) {
     const int row = i * 4 + (lane >> 4);
-    const f32x4_t v = *(const f32x4_t*)&stage[row * FPAD + (lane & 15) * 4];
+    const f32x4_t v = *(const f32x4_t*)&stage[row * HD + (((lane & 15) ^ (row & 15)) << 2)];
     if (rw + row < n) __builtin_nontemporal_store(v, (f32x4_t*)(ob + i * 4 * rs));
   }
 }
