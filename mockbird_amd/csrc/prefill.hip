@@ -102,16 +102,17 @@ __device__ __forceinline__ bool live_slot(int32_t p, int64_t cur, int C) {
 // for every query (no per-slot test), or mixed (the window rule per slot and
 // query, against relative positions the wave reads back from its own LDS row).
 //
-// Where the time goes (16 sequences x 512 rows, 12 heads, measured by taking
-// parts out of copies of the kernel): the q reads and fp32 output writes
-// alone take 8.8 us, streaming K/V through the buffers with no arithmetic
-// 12.5 us, the whole kernel ~21.5 us; replacing either product's MFMAs with
-// a few adds changes nothing, removing the softmax saves ~3 us.  A wave's
-// tile is a dependent chain (scores -> softmax -> P V) of about 2000 cycles,
-// against about 1100 cycles of issue; software-pipelining the next tile's
-// scores under this tile's softmax needs ~210 registers (2 waves per SIMD)
-// and was slower, as were 8 waves of 16 queries and an order that keeps a
-// sequence's query tiles on one XCD.
+// Where the time goes (16 sequences x 512 rows, 12 heads, ~16 us): the
+// workgroups start over ~1.4 us, every one loads its q rows and first tile
+// at once (~1.9 us with HBM near peak), and the longest query tiles then run
+// ~10 us of tile loop on SIMDs that issue ~60 % of the time.  A wave's tile
+// is a dependent chain (scores -> softmax -> P V); taken out of copies of an
+// earlier form of the kernel, neither product's MFMAs cost time, the softmax
+// did.  Software-pipelining the next tile's scores under this tile's softmax
+// needs ~210 registers (2 waves per SIMD) and was slower, as were 8 waves of
+// 16 queries, an order that keeps a sequence's query tiles on one XCD, and
+// skipping the all-future half of a diagonal tile (its branches cost more
+// than the work saved).
 constexpr int BQ = 128;  // query rows per workgroup of the bf16 kernel
 constexpr int kFlashWaves = 4;  // waves per workgroup of the bf16 kernel
 constexpr int NBUF = 3;  // K/V tile buffers
