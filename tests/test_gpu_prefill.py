@@ -83,7 +83,8 @@ def test_prefill_rows_are_independent():
 
 def test_c2_bf16_prefill_full_size():
     """B=16, S=512 (128 text + 384 code rows), bf16 q/k/v ~ N(0,1), RoPE at
-    pos = row, ring C=1024 written from slot 0, bf16 MFMA causal attention."""
+    pos = row, ring C=1024 written from slot 0, bf16 MFMA causal attention;
+    all 16 sequences' roped q and rings bit-exact, attention within 2e-2."""
     torch = pytest.importorskip("torch")
     say("C2 bf16 prefill full size")
     B, S, C = 16, 512, 1024
@@ -104,7 +105,7 @@ def test_c2_bf16_prefill_full_size():
         torch.cuda.synchronize()
         out_h = out.cpu().numpy()
         assert np.isfinite(out_h).all()
-        for b in (0, 11):
+        for b in range(B):  # every sequence against the oracle
             x = qkv[b:b + 1].float().cpu().numpy()
             ring = oracle.Ring(1, C, kv_bf16=True)
             qo = ring.write(x, [0], [S])
