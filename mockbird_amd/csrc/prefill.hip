@@ -212,9 +212,11 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   const int64_t kv_end64 = p0 + rlast + 1;
   const int kv_end = kv_end64 < C ? (int)kv_end64 : C;
 
-  // B operands of the score MFMA: Q[row][32*kc + 8*grp + 0..7] as stored; the
-  // 1/sqrt(64) scale is applied with log2(e) in the softmax (a power of two,
-  // so the scores are the same as from a pre-scaled Q)
+  // B operands of the score MFMA: Q[row][32*kc + 8*grp + 0..7] times
+  // 1/sqrt(64) * log2(e), rounded to bf16 once here, so the MFMA yields the
+  // scores in log2 units and the softmax needs no per-score scaling.  (The
+  // extra rounding of q is a relative 2^-9 per element; the probabilities
+  // are rounded to bf16 for P V anyway.)
   bf16x8_t qb[QB][2];
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
@@ -223,7 +225,9 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     for (int kc = 0; kc < 2; kc++) {
       uint4 raw = make_uint4(0, 0, 0, 0);
       if (r < n) raw = *(const uint4*)(q + row_at(q_rows, b, r) + h * HD + kc * 32 + grp * 8);
-      qb[qi][kc] = __builtin_bit_cast(bf16x8_t, raw);
+      const bf16x8_t v = __builtin_bit_cast(bf16x8_t, raw);
+#pragma unroll
+      for (int e = 0; e < 8; e++) qb[qi][kc][e] = (__bf16)((float)v[e] * kScoreLog2);
     }
   }
   // Window test in 32 bits.  Stored positions are at most INT32_MAX (the ring
@@ -285,17 +289,19 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
   };
 
   f32x4_t acc[QB][4], lsum[QB];
-  // running maximum m (log2 units) per query column, with the rescale
-  // threshold (m + 8 in raw score units) and the exponent's offset -m (0
-  // while m = -inf)
-  float m[QB], lim[QB], mneg[QB];
+  // Per query column: the running maximum m (log2 units) enters as the
+  // score MFMA's accumulator input moff = -m (0 while m = -inf), so the
+  // products come out as t = score - m, the exponent's argument.  lim is
+  // the rescale threshold on t: -inf while m = -inf, then 8.
+  f32x4_t moff[QB];
+  float lim[QB];
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
 #pragma unroll
     for (int d = 0; d < 4; d++) acc[qi][d] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     lsum[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    m[qi] = lim[qi] = -INFINITY;
-    mneg[qi] = 0.f;
+    moff[qi] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    lim[qi] = -INFINITY;
   }
   bf16x8_t ones;
 #pragma unroll
@@ -354,13 +360,14 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     const uint64_t partial =
         ~(__ballot(rel_l <= crel_lo) & __ballot((uint32_t)crel_hi - (uint32_t)rel_l < (uint32_t)W));
 
-    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol
+    // S^T blocks: rows = slots sb*16 + grp*4 + j, column = query qi*16 + qcol;
+    // t = score - m in log2 units (the accumulator starts at -m)
     f32x4_t s[QB][4];
 #pragma unroll
     for (int sb = 0; sb < 4; sb++)
 #pragma unroll
       for (int qi = 0; qi < QB; qi++) {
-        s[qi][sb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        s[qi][sb] = moff[qi];
 #pragma unroll
         for (int kc = 0; kc < 2; kc++)
           s[qi][sb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(QB > 1 ? ka[sb][kc] : kfrag(sb, kc),
@@ -403,12 +410,14 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
     }
     // Online softmax in log2 units.  The running maximum m only moves when a
     // tile's maximum exceeds it by more than 8 (the conditional rescaling of
-    // FlashAttention-3): the weights 2^(t - m) then stay <= 256, and the
-    // rescale of the accumulators, a wave-uniform branch taken for all query
-    // blocks at once, is rare after the first tiles.  The result is the same
+    // FlashAttention-3): the weights 2^t then stay <= 256, and the rescale of
+    // the accumulators, a wave-uniform branch taken for all query blocks at
+    // once, is rare after the first tiles.  The test needs only each lane's
+    // own maximum (a column moves iff one of its four lanes exceeds lim); the
+    // column maximum is formed on the rare branch.  The result is the same
     // softmax: acc and the weight sum always share one m.
-    float xm[QB];       // column maximum of the raw scores
-    uint64_t grow = 0;  // lanes whose column maximum moves
+    float xm[QB];       // this lane's maximum of t
+    uint64_t grow = 0;  // lanes whose maximum passes the threshold
 #pragma unroll
     for (int qi = 0; qi < QB; qi++) {
       float x = -INFINITY;
@@ -416,23 +425,25 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
       for (int sb = 0; sb < 4; sb++)
 #pragma unroll
         for (int j = 0; j < 4; j++) x = fmaxf(x, s[qi][sb][j]);
-      xm[qi] = col_max_plain(x);
-      grow |= __ballot(xm[qi] > lim[qi]);
+      xm[qi] = x;
+      grow |= __ballot(x > lim[qi]);
     }
     if (grow) {  // uniform
 #pragma unroll
       for (int qi = 0; qi < QB; qi++) {
-        if (xm[qi] > lim[qi]) {
-          const float mt = xm[qi] * kScoreLog2;
+        const float xt = col_max_plain(xm[qi]);  // column maximum of t
+        if (xt > lim[qi]) {  // uniform per column
           if constexpr (!FIRST) {
-            const float scale = __builtin_amdgcn_exp2f(m[qi] - mt);
+            // exp2(m_old - m_new); 0 while m_old = -inf (acc is still zero)
+            const float scale = lim[qi] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(-xt);
 #pragma unroll
             for (int d = 0; d < 4; d++) acc[qi][d] *= scale;
             lsum[qi] *= scale;
           }
-          m[qi] = mt;
-          lim[qi] = (mt + 8.f) * kInvScoreLog2;
-          mneg[qi] = -mt;
+#pragma unroll
+          for (int sb = 0; sb < 4; sb++) s[qi][sb] -= xt;
+          moff[qi] -= xt;
+          lim[qi] = 8.f;
         }
       }
     }
@@ -443,8 +454,7 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
       for (int c = 0; c < 2; c++)
 #pragma unroll
         for (int e = 0; e < 8; e++)
-          pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(
-              fmaf(s[qi][2 * c + (e >> 2)][e & 3], kScoreLog2, mneg[qi]));
+          pb[qi][c][e] = (__bf16)__builtin_amdgcn_exp2f(s[qi][2 * c + (e >> 2)][e & 3]);
     // O^T[d-block] += V^T[d-block rows][32 slots of chunk c] P^T[those
     // slots][queries].  The weight sum is one more MFMA with an all-ones A,
     // so it adds the same rounded weights the products use.
@@ -500,18 +510,29 @@ __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(
 #pragma unroll
   for (int qi = 0; qi < QB; qi++) {
     const float l = lsum[qi][0];
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const float inv = l > 0.f ? __builtin_amdgcn_rcpf(l) : 0.f;
 #pragma unroll
     for (int d = 0; d < 4; d++)
       *(f32x4_t*)&stage[(qi * 16 + qcol) * HD + (((4 * d + grp) ^ qcol) << 2)] = acc[qi][d] * inv;
   }
+  // Lane (grp, c = lane mod 16) stores chunk c of rows 4 i + grp.  The
+  // swizzle (4 i + grp) mod 16 repeats every 4 rows-of-four, so four LDS
+  // offsets serve all WQ / 4 reads.
   const int64_t rs = out_rows.row_stride;
-  float* ob = out + row_at(out_rows, b, rw) + h * HD + (lane >> 4) * rs + (lane & 15) * 4;
+  float* ob = out + row_at(out_rows, b, rw) + h * HD + grp * rs + qcol * 4;
+  int soff[4];
 #pragma unroll
-  for (int i = 0; i < WQ / 4; i++) {
-    const int row = i * 4 + (lane >> 4);
-    const f32x4_t v = *(const f32x4_t*)&stage[row * HD + (((lane & 15) ^ (row & 15)) << 2)];
-    if (rw + row < n) __builtin_nontemporal_store(v, (f32x4_t*)(ob + i * 4 * rs));
+  for (int i = 0; i < 4; i++) soff[i] = (i * 4 + grp) * HD + ((qcol ^ (i * 4 + grp)) << 2);
+  auto row_out = [&](int i) {
+    return *(const f32x4_t*)&stage[soff[i & 3] + (i >> 2) * 16 * HD];
+  };
+  if (rw + WQ <= n) {  // uniform: every row of the wave is a query row
+#pragma unroll
+    for (int i = 0; i < WQ / 4; i++) __builtin_nontemporal_store(row_out(i), (f32x4_t*)(ob + i * 4 * rs));
+  } else {
+#pragma unroll
+    for (int i = 0; i < WQ / 4; i++)
+      if (rw + i * 4 + grp < n) __builtin_nontemporal_store(row_out(i), (f32x4_t*)(ob + i * 4 * rs));
   }
 }
 #undef MB_WAIT_VMCNT
