@@ -46,19 +46,23 @@ constexpr int FPAD = 68;  // fp32 LDS row stride (272 B)
 // long tiles with short ones on each CU.  Work item g = nxcd * j + x stays
 // on XCD x, so a (sequence, head) pair's tiles share one L2 whenever the
 // pair count is a multiple of nxcd.  cpx = 0 hands out the work in order.
+// The launcher keeps the workgroup count below 2^31, so the numbering is
+// done in 32-bit unsigned arithmetic (a 64-bit division by a run-time value
+// is a long scalar and vector sequence, run by every wave before its first
+// load).
 __device__ __forceinline__ void work_item(int& b, int& h, int& qtile, int nxcd, int cpx) {
-  const int64_t L = blockIdx.x + (int64_t)gridDim.x * (blockIdx.y + (int64_t)gridDim.y * blockIdx.z);
-  const int64_t pairs = (int64_t)gridDim.y * gridDim.z;
-  int64_t g = L;
+  const uint32_t L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t pairs = gridDim.y * gridDim.z;
+  uint32_t g = L;
   if (cpx > 0) {
-    const int64_t total = pairs * gridDim.x;
-    const int64_t x = L % nxcd, i = L / nxcd, nx = (total - x + nxcd - 1) / nxcd;
-    const int64_t r = i / cpx, c = i % cpx;
-    const int64_t j = ((r & 1) && (r + 1) * cpx <= nx) ? r * cpx + (cpx - 1 - c) : i;
-    g = nxcd * j + x;
+    const uint32_t total = pairs * gridDim.x, ux = (uint32_t)nxcd, uc = (uint32_t)cpx;
+    const uint32_t x = L % ux, i = L / ux, nx = (total - x + ux - 1) / ux;
+    const uint32_t r = i / uc, c = i % uc;
+    const uint32_t j = ((r & 1) && (r + 1) * uc <= nx) ? r * uc + (uc - 1 - c) : i;
+    g = ux * j + x;
   }
-  qtile = gridDim.x - 1 - (int)(g / pairs);
-  const int64_t hb = g % pairs;
+  qtile = (int)(gridDim.x - 1 - g / pairs);
+  const uint32_t hb = g % pairs;
   h = (int)(hb % gridDim.y);
   b = (int)(hb / gridDim.y);
 }
@@ -117,7 +121,6 @@ constexpr int BQ = 128;  // query rows per workgroup of the bf16 kernel
 constexpr int kFlashWaves = 4;  // waves per workgroup of the bf16 kernel
 constexpr int NBUF = 3;  // K/V tile buffers
 constexpr float kScoreLog2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
-constexpr float kInvScoreLog2 = 8.f * 0.6931471805599453f;   // its inverse, sqrt(64) * ln(2)
 constexpr int32_t kRelEmpty = INT32_MAX;  // relative position of an empty slot
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -968,6 +971,8 @@ int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_
     return fail(ctx, MB_ERR_ARG, "bf16 queries need a bf16 ring (the bf16 MFMA path)");
   if (B > 65535) return fail(ctx, MB_ERR_ARG, "at most 65535 sequences per prefill call");
   if (B == 0 || rows_max == 0) return MB_OK;
+  if ((int64_t)((rows_max + QT - 1) / QT) * ring.heads * B >= INT32_MAX)
+    return fail(ctx, MB_ERR_ARG, "too many query tiles in one prefill call");
   const unsigned nh = (unsigned)ring.heads;
   dim3 grid((unsigned)((rows_max + QT - 1) / QT), nh, (unsigned)B);
   if (q_dtype == MB_DT_BF16)
