@@ -18,7 +18,9 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB = os.path.join(_HERE, "liboracle.so")
+#: MB_ORACLE_LIB names another build of the same source (the sanitized one,
+#: oracle/_asan/liboracle.so, for tests/test_oracle_sanitized.py)
+_LIB = os.environ.get("MB_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 #: the fp32-accumulating build of mb_oracle.c: the CPU throughput baseline
 #: only (bench.py's cpu_baseline leg), never a checker
 _LIB_FP32 = os.path.join(_HERE, "liboracle_fp32.so")
