@@ -341,6 +341,29 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   // wave's range read as empty, and their K/V loads are clamped to `base`.
   uint4 kr[U], vr[U];
   int32_t spl = -1;
+  // The first batch is issued in two halves from the prologue: its K rows
+  // and stored positions before the RoPE rotation waits for q, its V rows
+  // after it.  Those loads are unconditional, each slot clamped to the last
+  // one of the window (slot 0 for an empty window, which every ring has),
+  // so the compiler counts the same loads on every path and its wait for q
+  // leaves them in flight (loads retire in issue order).  Lanes past the
+  // window are masked in the liveness ballot.
+  const int last = s1 > 0 ? s1 - 1 : 0;
+  auto issue_k0 = [&]() {
+    spl = sp[min(s0 + lane, last)];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int slot = s0 + u * G + g;
+      kr[u] = load_stream(kbase + (int64_t)(slot < s1 ? slot : last) * ROWB);
+    }
+  };
+  auto issue_v0 = [&]() {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int slot = s0 + u * G + g;
+      vr[u] = load_stream(vbase + (int64_t)(slot < s1 ? slot : last) * ROWB);
+    }
+  };
   auto issue = [&](int base) {
     spl = (lane < GU && base + lane < s1) ? sp[base + lane] : -1;
 #pragma unroll
@@ -369,8 +392,20 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
       slot_new = wrap ? (int)(cur % C) : (int)cur;
       owner = slot_new < s1 && (slot_new / GU) % nw == wave;
     }
+    // table entries of pos, clamped (a position beyond the table is
+    // evaluated after the K rows are issued, as rope_cs does it)
+    const int32_t tpos = pos < kRopeTab ? pos : kRopeTab - 1;
 #pragma unroll
-    for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+    for (int j = 0; j < VD / 2; j++) {
+      const float2 t = rope_tab[(int64_t)tpos * 32 + (sub * VD >> 1) + j];
+      cs[j] = t.x;
+      sn[j] = t.y;
+    }
+    issue_k0();
+    if (pos >= kRopeTab) {  // uniform
+#pragma unroll
+      for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+    }
 #pragma unroll
     for (int j = 0; j < VD / 2; j++) rope_pair(qi[2 * j], qi[2 * j + 1], cs[j], sn[j], qo[2 * j], qo[2 * j + 1]);
     if (q_out && wave == 0 && g == 0) {
@@ -380,7 +415,7 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
     }
 #pragma unroll
     for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
-    if (s0 < s1) issue(s0);
+    issue_v0();
     if (owner) {  // wave-uniform
       float ki[VD], vi[VD], ko[VD];
       load_n<IN_BF16, VD>(q, roff + D, ki);
@@ -401,7 +436,8 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
     float4 qt[VD / 4];
 #pragma unroll
     for (int i = 0; i < VD / 4; i++) qt[i] = *(const float4*)(qp + 4 * i);
-    if (s0 < s1) issue(s0);
+    issue_k0();
+    issue_v0();
 #pragma unroll
     for (int i = 0; i < VD / 4; i++) {
       // 0.125 = 2^-3: pre-scaling q is exact
@@ -416,7 +452,7 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
 
   for (int base = s0; base < s1; base += step) {
     const int64_t dlt = cur - (int64_t)spl;
-    const uint64_t live = __ballot(spl >= 0 && dlt >= 0 && dlt < C);
+    const uint64_t live = __ballot(lane < GU && base + lane < s1 && spl >= 0 && dlt >= 0 && dlt < C);
     bool ok[U];
 #pragma unroll
     for (int u = 0; u < U; u++) ok[u] = (live >> (u * G + g)) & 1ull;
