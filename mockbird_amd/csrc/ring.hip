@@ -303,7 +303,14 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 // fewer, the local head's launches at 256 voices (3072 one-wave blocks) no
 // longer fit the chip in one round.  The bf16 forms get 4 from their
 // 1024-thread blocks already.
-template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16>
+//
+// EARLY (launches with few waves per CU, bf16 4-load batches only): each
+// batch issues the next batch's K rows and stored positions as soon as its
+// own scores are formed, and the next V rows after its P V, so a wave keeps
+// a K half-batch in flight under its softmax.  With 12 waves per CU (64
+// sequences, C = 2048) that extra depth cost 0.9 %; with 7.5 (32 sequences,
+// C = 4096) it gained 2.4 %.
+template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16, bool EARLY = false>
 __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn_unit(
     const void* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, int rows, void* __restrict__ ring_k,
@@ -372,6 +379,21 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
       const int sl = slot < s1 ? slot : base;
       kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
       vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
+    }
+  };
+  auto issue_kn = [&](int base) {
+    spl = (lane < GU && base + lane < s1) ? sp[base + lane] : -1;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int slot = base + u * G + g;
+      kr[u] = load_stream(kbase + (int64_t)(slot < s1 ? slot : base) * ROWB);
+    }
+  };
+  auto issue_vn = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int slot = base + u * G + g;
+      vr[u] = load_stream(vbase + (int64_t)(slot < s1 ? slot : base) * ROWB);
     }
   };
 
@@ -481,6 +503,8 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
       sc[u] = ok[u] ? dot : -INFINITY;
       mx = fmaxf(mx, sc[u]);
     }
+    const bool more = base + step < s1;
+    if (EARLY && more) issue_kn(base + step);  // this batch's K rows are consumed
     if (mx != -INFINITY) {  // else nothing live yet in this lane group
       const float scale = __expf(m - mx);
       l *= scale;
@@ -497,7 +521,11 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
       }
       m = mx;
     }
-    if (base + step < s1) issue(base + step);
+    if (EARLY) {
+      if (more) issue_vn(base + step);
+    } else if (more) {
+      issue(base + step);
+    }
   }
 
   // fold the G lane groups: lanes sub, sub+LR, sub+2LR, ... hold the same dims
@@ -712,11 +740,16 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
   };
   if (ring.bf16) {
     constexpr int MAXNW = 16;
+    const int64_t cus = ctx->cus_per_xcd > 0 ? (int64_t)ctx->xcds * ctx->cus_per_xcd : 256;
     const int nw = short_waves(unit_waves(max_valid, 180, MAXNW), max_valid <= kAttnShortWindow ? 64 : 32, MAXNW);
     // short windows take 8-load batches, longer ones 4-load batches
     if (max_valid <= kAttnShortWindow)
       hipLaunchKernelGGL((k_attn_unit<true, 8, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                          ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+    else if (nq * H * nw <= 8 * cus)  // at most 8 waves per CU: deeper loads
+      hipLaunchKernelGGL((k_attn_unit<true, 4, MAXNW, APPEND, IN_BF16, true>), grid, dim3(64 * nw),
+                         0, ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
                          ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
     else
       hipLaunchKernelGGL((k_attn_unit<true, 4, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
