@@ -535,12 +535,14 @@ def frame_prompts(B, seed=33):
                          vocab=32000) for b, l in enumerate(lens)]
 
 
-def run_frames(weights, B, frames, kv_name, warmup=3):
+def run_frames(weights, B, frames, kv_name, warmup=3, weights_name="f32"):
     """Greedy decode frames/s: prefill the prompts (untimed), then time
     `frames` frames, each the 17-step local head (text decision + 16 codes with
     the repetition penalty) followed by the 12-layer global decode step of the
     frame row it produced.  Everything stays on the device (mb_decode_frames_dev:
-    one graph launch per frame); positions advance one per frame."""
+    one graph launch per frame); positions advance one per frame.
+    `weights_name` "bf16": the projection weights in bf16 storage
+    (mb_set_weight_storage), the model's bf16 form."""
     import torch
 
     import mockbird_amd as mb
@@ -559,6 +561,8 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
     dev = torch.device("cuda")
     ctx = mb.Context(n_layers=12, capacity=C, max_seqs=B, max_rows=int(n.max()), kv_dtype=kv)
     ctx.upload_all(weights)
+    if weights_name == "bf16":
+        ctx.set_weight_storage(mb.MB_W_BF16)
     stream = torch.cuda.current_stream()
     ctx.set_stream(stream.cuda_stream)
     t_pf = time.perf_counter()
@@ -587,7 +591,8 @@ def run_frames(weights, B, frames, kv_name, warmup=3):
     ms = t0.elapsed_time(t1)
     ok = bool(cont.all().item()) and bool(torch.isfinite(h).all().item())
     ctx.close()
-    return {"B": B, "kv": kv_name, "frames": frames, "ms_per_frame": round(ms / frames, 4),
+    return {"B": B, "kv": kv_name, "weights": weights_name, "frames": frames,
+            "ms_per_frame": round(ms / frames, 4),
             "frames_per_sec": round(B * frames / (ms * 1e-3), 1),
             "prompt_rows": [int(n.min()), int(n.max())], "prefill_s": round(t_pf, 3),
             "all_continued": ok}
@@ -757,15 +762,19 @@ def main():
         # the text head equals the audio_end column, so no voice ever stops
         w = synth.model_weights(n_layers=12, vocab=32000, seed=0)
         w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]
+    frames_w16 = None
     if "frames" in legs:
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
         frames = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1])
                   for b in map(int, args.frames_b.split(","))]
+        frames_w16 = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1], weights_name="bf16")
+                      for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "hbm_read_ceiling": ceiling, "gemm": gemm,
                           "kv_attention_256_voices": voices,
                           "kv_attention_c4_wrapped": c4, "prefill_attention": c2,
-                          "codec": codec, "frames_detail": frames}), flush=True)
+                          "codec": codec, "frames_detail": frames,
+                          "frames_bf16_weights": frames_w16}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -820,6 +829,9 @@ def main():
         "codec": codec,
         "frames_per_sec": None if frames is None else {f"B{r['B']}": r["frames_per_sec"] for r in frames},
         "frames_detail": frames,
+        "frames_per_sec_bf16_weights": None if frames_w16 is None else {
+            f"B{r['B']}": r["frames_per_sec"] for r in frames_w16},
+        "frames_detail_bf16_weights": frames_w16,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -245,6 +245,23 @@ int mb_linear_noalloc_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int6
  * frame graph of mb_decode_frames_dev. */
 int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, double penalty);
 
+/* Weight storage of the decoder's projections (c_attn, c_proj, fc_in, fc_out
+ * of every layer, the local layer's, and the 16 audio heads): MB_W_F32 (the
+ * default, the reference's fp32 weights) or MB_W_BF16.  With MB_W_BF16 each
+ * of those weights is rounded to bf16 once (round to nearest even) when the
+ * model is resolved, and the decode-sized kernels read the bf16 copies --
+ * half the weight bytes; products and sums stay fp32, so the results are
+ * those of the fp32 path on the rounded weights.  Embeddings and the text
+ * head stay fp32.  The bf16 re-export of the model weights that
+ * docs/moss-tts-runtime-analysis.md:408-411 plans (the reference's own
+ * "f16 re-export", a separate, independent win) is what this stands for;
+ * the uploaded tensors are left as they are, and a later call switches back.
+ * Re-derives the weight copies on the next model call and invalidates the
+ * captured frame graph. */
+#define MB_W_F32 0
+#define MB_W_BF16 1
+int mb_set_weight_storage(mb_ctx* ctx, int32_t storage);
+
 /* Global prefill of sequences b < B: ids [B][rows_max][17], n_rows[b] rows at
  * positions 0 .. n_rows[b]-1 (n_rows[b] <= capacity).  Each sequence's rings
  * are emptied first (a new utterance), every layer's K/V is written from

@@ -551,12 +551,21 @@ __global__ __launch_bounds__(256) void k_gemm_stream(
 constexpr int kX3Block = 32;  // k per MFMA step
 constexpr int kX3BlockU4 = 512;  // uint4 per 64-column x 32-deep block (8 KB)
 
-template <int MT, int ST, int EPI, bool LNF>
+//
+// W1 (bf16 weight storage): W is bf16-exact, so it has no remainder half:
+// the copy holds only the high halves ([column block j][lane][8], 4 KB per
+// 64-column x 32-deep block, launch_split_w1) and each product is the two
+// bf16 products al w + ah w.  GAM: the LayerNorm's gamma multiplies A on the
+// fly (A's LayerNorm sums stay those of the raw rows), gamma[32 kb + 8 r ..
+// + 7] loaded with each block.
+template <int MT, int ST, int EPI, bool LNF, bool W1 = false, bool GAM = false>
 __global__ __launch_bounds__(256) void k_gemm_x3(
     const float* __restrict__ A, int64_t lda, const uint4* __restrict__ Wx, int N, int kw,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     float* __restrict__ part, const float* __restrict__ lnc, const float* __restrict__ lnd,
-    int32_t* __restrict__ cnt) {
+    int32_t* __restrict__ cnt, const float* __restrict__ gamma) {
+  constexpr int BU4 = W1 ? kX3BlockU4 / 2 : kX3BlockU4;  // uint4 per 64 x 32 weight block
+  constexpr int NH = W1 ? 1 : 2;                          // weight halves
   constexpr int MI = MT / 16, AL = MT / 8;  // row blocks; A loads per block (8 rows each)
   __shared__ f32x4_t Ablk[4][MT * 8];       // per wave: MT rows x 8 chunks of 4 floats
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -594,17 +603,22 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
     f32x4_t* const Aw = Ablk[wave] + crow * 8 + (cchunk ^ crow);
     const f32x4_t* const Ar0 = Ablk[wave] + l16 * 8 + ((2 * r) ^ (l16 & 7));
     const f32x4_t* const Ar1 = Ablk[wave] + l16 * 8 + ((2 * r + 1) ^ (l16 & 7));
-    const uint4* Wb = Wx + (int64_t)blockIdx.x * (K / kX3Block) * kX3BlockU4 + lane;
+    const uint4* Wb = Wx + (int64_t)blockIdx.x * (K / kX3Block) * BU4 + lane;
     f32x4_t a[ST][AL];
-    uint4 w[ST][4][2];
+    uint4 w[ST][4][NH];
+    f32x4_t g[ST][2];
     auto load = [&](auto st_, int kb) {
       constexpr int st = decltype(st_)::value;
 #pragma unroll
       for (int j = 0; j < 4; j++)
 #pragma unroll
-        for (int h = 0; h < 2; h++) w[st][j][h] = Wb[(int64_t)kb * kX3BlockU4 + (2 * j + h) * 64];
+        for (int h = 0; h < NH; h++) w[st][j][h] = Wb[(int64_t)kb * BU4 + (NH * j + h) * 64];
 #pragma unroll
       for (int p = 0; p < AL; p++) a[st][p] = *(const f32x4_t*)(A + kb * kX3Block + aoff[p]);
+      if (GAM) {
+        g[st][0] = *(const f32x4_t*)(gamma + kb * kX3Block + 8 * r);
+        g[st][1] = *(const f32x4_t*)(gamma + kb * kX3Block + 8 * r + 4);
+      }
     };
     auto mma = [&](auto st_) {
       constexpr int st = decltype(st_)::value;
@@ -614,7 +628,7 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
 #pragma unroll
       for (int i = 0; i < MI; i++) {
         const f32x4_t v0 = Ar0[i * 128], v1 = Ar1[i * 128];
-        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         if (LNF) {
           float s1 = 0.f, s2 = sxx[i];
 #pragma unroll
@@ -625,6 +639,13 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
           }
           sx[i] += s1;
           sxx[i] = s2;
+        }
+        if (GAM) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[e] = __fmul_rn(v[e], g[st][0][e]);
+            v[e + 4] = __fmul_rn(v[e + 4], g[st][1][e]);
+          }
         }
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -642,12 +663,14 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
         for (int i = 0; i < MI; i++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], wh, acc[i][j], 0, 0, 0);
       }
+      if constexpr (!W1) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const bf16x8_t wl = __builtin_bit_cast(bf16x8_t, w[st][j][1]);
+        for (int j = 0; j < 4; j++) {
+          const bf16x8_t wl = __builtin_bit_cast(bf16x8_t, w[st][j][NH - 1]);
 #pragma unroll
-        for (int i = 0; i < MI; i++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], wl, acc[i][j], 0, 0, 0);
+          for (int i = 0; i < MI; i++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[i], wl, acc[i][j], 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int j = 0; j < 4; j++) {
@@ -803,10 +826,10 @@ static int tile_counters(mb_ctx* ctx, int32_t*& cnt) {
   return fresh ? launch_fill_i32(ctx, cnt, kTileCounters, 0) : MB_OK;
 }
 
-template <int MT, int ST, bool LNF>
+template <int MT, int ST, bool LNF, bool W1 = false, bool GAM = false>
 static int x3_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint4* Wx, int N,
                      int K, const float* bias, float* Cm, int64_t ldc, int M, int S,
-                     const float* lnc, const float* lnd) {
+                     const float* lnc, const float* lnd, const float* gamma = nullptr) {
   const dim3 grid((unsigned)(N / 64), (unsigned)((M + MT - 1) / MT), (unsigned)S);
   float* part = nullptr;
   int32_t* cnt = nullptr;
@@ -825,32 +848,34 @@ static int x3_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const ui
     constexpr int E = decltype(e)::value;
     if constexpr (LNF) {
       if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
-        hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, true>), grid, dim3(256), 0, ctx->stream, A, lda,
-                           Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt);
-    } else {
-      hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, false>), grid, dim3(256), 0, ctx->stream, A, lda,
-                         Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt);
+        hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, true, W1, GAM>), grid, dim3(256), 0, ctx->stream,
+                           A, lda, Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt, gamma);
+    } else if constexpr (!GAM) {
+      hipLaunchKernelGGL((k_gemm_x3<MT, ST, E, false, W1, false>), grid, dim3(256), 0, ctx->stream,
+                         A, lda, Wx, N, kw, bias, Cm, ldc, M, part, lnc, lnd, cnt, gamma);
     }
   });
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
 
-int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
-                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
-                   const float* lnd) {
+template <bool W1>
+static int gemm_x3_any(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
+                       int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                       const float* lnd, const float* gamma) {
   if (M <= 0) return MB_OK;
   if (M <= kGemvMaxM || !gemm_streams(M, N))
     return fail(ctx, MB_ERR_STATE, "split-bf16 gemm takes the streaming shapes (M %d N %d)", M, N);
   if (N % 64 || K % (4 * kX3Block) || lda % 4 || ldc % 4 || (int64_t)M * lda >= INT32_MAX ||
       ((uintptr_t)A & 15) ||
       ((uintptr_t)Wx & 15) || ((uintptr_t)Cm & 15) || ((uintptr_t)bias & 15) ||
-      ((uintptr_t)lnc & 15) || ((uintptr_t)lnd & 15))
+      ((uintptr_t)lnc & 15) || ((uintptr_t)lnd & 15) || ((uintptr_t)gamma & 15))
     return fail(ctx, MB_ERR_ARG, "split-bf16 gemm shape/alignment unsupported (M %d N %d K %d)", M,
                 N, K);
   const bool lnf = lnc != nullptr;
   if (lnf && (!lnd || (epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)))
     return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  if (gamma && !lnf) return fail(ctx, MB_ERR_ARG, "gamma on A goes with a folded LayerNorm");
   int mt, S;
   stream_shape(M, N, K, lnf, mt, S);
   while (S > 1 && K % (4 * kX3Block * S)) S--;
@@ -864,20 +889,31 @@ int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void
   // against 11.7 with 3; deeper prologues spend longer issuing loads before
   // the first MFMA, and the per-CU load rate, not latency, bounds the rest).
   const uint4* W = (const uint4*)Wx;
-  if (lnf) {
-    switch (mt) {
-      case 16: return x3_launch<16, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
-      case 32: return x3_launch<32, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
-      case 48: return x3_launch<48, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
-      default: return x3_launch<64, 2, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
-    }
-  }
+  auto go = [&](auto mt_) {
+    constexpr int T = decltype(mt_)::value;
+    if (lnf && gamma)
+      return x3_launch<T, 2, true, W1, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd, gamma);
+    if (lnf) return x3_launch<T, 2, true, W1>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, lnc, lnd);
+    return x3_launch<T, 2, false, W1>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+  };
   switch (mt) {
-    case 16: return x3_launch<16, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-    case 32: return x3_launch<32, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-    case 48: return x3_launch<48, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
-    default: return x3_launch<64, 2, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, S, nullptr, nullptr);
+    case 16: return go(std::integral_constant<int, 16>{});
+    case 32: return go(std::integral_constant<int, 32>{});
+    case 48: return go(std::integral_constant<int, 48>{});
+    default: return go(std::integral_constant<int, 64>{});
   }
+}
+
+int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
+                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                   const float* lnd) {
+  return gemm_x3_any<false>(ctx, epi, A, lda, Wx, N, K, bias, Cm, ldc, M, lnc, lnd, nullptr);
+}
+
+int launch_gemm_x2(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx1, int N,
+                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                   const float* lnd, const float* gamma) {
+  return gemm_x3_any<true>(ctx, epi, A, lda, Wx1, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
 }
 
 // ---------------------------------------------------------------------------
@@ -1237,6 +1273,206 @@ int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float
   return MB_OK;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 weight storage (mb_set_weight_storage): the projection weights are
+// rounded to bf16 once (k_round_bf16) and the decode-sized kernels read them
+// as bf16 -- half the bytes -- with fp32 products and accumulation.  The
+// LayerNorm's gamma stays on the activation side (gamma[k] x[k] w[k][n] in
+// the kernel; c and d come from the rounded W, launch_fold_ln), so every
+// product is one of the rounded weights exactly as the model holds it.
+//
+// k_gemv_k16: k_gemv_k on a bf16 k-major copy Wk16[n][k] = W[k][n].  Lane l
+// reads 8 consecutive k per load (k = 8 l + 512 i: a wave reads 1 KB
+// contiguous per load), with the matching two float4 of every A row (and of
+// gamma with GAM), all issued before the first multiply-add.  The LayerNorm
+// sums of LNF are taken over the raw rows, as in k_gemv_k.
+template <int EPI, bool LNF, bool GAM, int MR>
+__global__ __launch_bounds__(256) void k_gemv_k16(
+    const float* __restrict__ A, int64_t lda, const uint16_t* __restrict__ Wk, int N, int K,
+    const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
+    const float* __restrict__ lnc, const float* __restrict__ lnd,
+    const float* __restrict__ gamma) {
+  constexpr int RI = MR <= 2 ? 6 : MR <= 4 ? 3 : 2;  // k steps (512 each) per round of loads
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + wave;
+  const uint16_t* wp = Wk + (int64_t)n * K + 8 * lane;
+  float ep_b = 0.f, ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
+  if (lane < M) {
+    if (bias) ep_b = bias[n];
+    if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)lane * ldc + n];
+    if (LNF) {
+      ep_cv = lnc[n];
+      ep_dv = lnd[n];
+    }
+  }
+  float acc[MR], s1[MR], s2[MR], x0[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    acc[m] = s1[m] = s2[m] = 0.f;
+    x0[m] = LNF && m < M ? A[(int64_t)m * lda] : 0.f;
+  }
+  const int steps = (K + 511) >> 9;
+  for (int i0 = 0; i0 < steps; i0 += RI) {
+    uint4 w[RI];
+    float4 a[RI][MR][2], g[RI][2];
+#pragma unroll
+    for (int i = 0; i < RI; i++) {
+      const int k = (i0 + i) * 512 + 8 * lane;
+      const bool in = i0 + i < steps && k < K;
+      w[i] = in ? *(const uint4*)(wp + (int64_t)(i0 + i) * 512) : make_uint4(0, 0, 0, 0);
+      if (GAM) {
+        g[i][0] = in ? *(const float4*)(gamma + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        g[i][1] = in ? *(const float4*)(gamma + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        const bool am = in && m < M;
+        a[i][m][0] = am ? *(const float4*)(A + (int64_t)m * lda + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        a[i][m][1] = am ? *(const float4*)(A + (int64_t)m * lda + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RI; i++) {
+      if (i0 + i >= steps || (i0 + i) * 512 + 8 * lane >= K) continue;
+      const uint32_t wb[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
+      float wf[8], gf[8];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        wf[2 * t] = __uint_as_float(wb[t] << 16);
+        wf[2 * t + 1] = __uint_as_float(wb[t] & 0xFFFF0000u);
+      }
+      if (GAM) {
+        gf[0] = g[i][0].x; gf[1] = g[i][0].y; gf[2] = g[i][0].z; gf[3] = g[i][0].w;
+        gf[4] = g[i][1].x; gf[5] = g[i][1].y; gf[6] = g[i][1].z; gf[7] = g[i][1].w;
+      }
+#pragma unroll
+      for (int m = 0; m < MR; m++) {
+        const float av[8] = {a[i][m][0].x, a[i][m][0].y, a[i][m][0].z, a[i][m][0].w,
+                             a[i][m][1].x, a[i][m][1].y, a[i][m][1].z, a[i][m][1].w};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          acc[m] = fmaf(GAM ? __fmul_rn(av[t], gf[t]) : av[t], wf[t], acc[m]);
+          if (LNF) {
+            const float e = av[t] - x0[m];
+            s1[m] += e;
+            s2[m] = fmaf(e, e, s2[m]);
+          }
+        }
+      }
+    }
+  }
+  auto fold = [](float v) {
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) v += __shfl_xor(v, sh);
+    return col_sum(v);
+  };
+  float mine = 0.f, m1 = 0.f, m2 = 0.f, mx0 = 0.f;
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m >= M) break;
+    const float t = fold(acc[m]);
+    if (lane == m) mine = t;
+    if (LNF) {
+      const float u1 = fold(s1[m]), u2 = fold(s2[m]);
+      if (lane == m) {
+        m1 = u1;
+        m2 = u2;
+        mx0 = x0[m];
+      }
+    }
+  }
+  if (lane >= M) return;
+  float o = mine;
+  if (LNF) {
+    const float inv_k = 1.f / (float)K;
+    const float ms = m1 * inv_k;  // mean of x - x0
+    const float var = fmaxf(m2 * inv_k - ms * ms, 0.f);
+    const float rstd = 1.f / sqrtf(var + 1e-5f);
+    o = rstd * (o - (mx0 + ms) * ep_cv) + ep_dv;
+  }
+  if (EPI == EPI_SCALE_ADD) {
+    o = ep_c + ep_b * o;
+  } else {
+    if (bias) o += ep_b;
+    if (EPI == EPI_GELU) o = gelu_tanh(o);
+    if (EPI == EPI_GELU_ERF) o = gelu_erf(o);
+    if (EPI == EPI_ADD) o = ep_c + o;
+  }
+  Cm[(int64_t)lane * ldc + n] = o;
+}
+
+int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint16_t* Wk,
+                    int N, int K, const float* bias, float* Cm, int64_t ldc, int M,
+                    const float* lnc, const float* lnd, const float* gamma) {
+  if (M <= 0) return MB_OK;
+  const bool lnf = lnc != nullptr;
+  if (M > kGemvMaxM || N % 4 || K % 8 || lda % 4 || ((uintptr_t)A & 15) || ((uintptr_t)Wk & 15) ||
+      ((uintptr_t)gamma & 15) || (lnf && !lnd))
+    return fail(ctx, MB_ERR_ARG, "bf16 k-major gemv shape/alignment unsupported (M %d N %d K %d)", M, N, K);
+  if (lnf && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
+    return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
+  const dim3 grid((unsigned)(N / 4));
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    auto go = [&](auto mr) {
+      constexpr int MRv = decltype(mr)::value;
+      if (lnf) {
+        if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF) {
+          if (gamma)
+            hipLaunchKernelGGL((k_gemv_k16<E, true, true, MRv>), grid, dim3(256), 0, ctx->stream, A,
+                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+          else
+            hipLaunchKernelGGL((k_gemv_k16<E, true, false, MRv>), grid, dim3(256), 0, ctx->stream, A,
+                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+        }
+      } else {
+        hipLaunchKernelGGL((k_gemv_k16<E, false, false, MRv>), grid, dim3(256), 0, ctx->stream, A,
+                           lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+      }
+    };
+    if (M <= 1) go(std::integral_constant<int, 1>{});
+    else if (M <= 2) go(std::integral_constant<int, 2>{});
+    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+  });
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// Wr = bf16(W) (round to nearest even), kept as fp32: the rounded weights
+// every later copy and the fp32 paths derive from.
+__global__ __launch_bounds__(256) void k_round_bf16(const float* __restrict__ W, int64_t n,
+                                                    float* __restrict__ Wr) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) Wr[i] = (float)(__bf16)W[i];
+}
+
+int launch_round_bf16(mb_ctx* ctx, const float* W, int64_t n, float* Wr) {
+  hipLaunchKernelGGL(k_round_bf16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, W,
+                     n, Wr);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
+// Wk16[n][k] = bf16(W[k][n]) (W [K][N] row-major, already bf16-exact where
+// it comes from k_round_bf16).
+__global__ __launch_bounds__(256) void k_kmajor_w16(const float* __restrict__ W, int K, int N,
+                                                    uint16_t* __restrict__ Wk) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)K * N) return;
+  const int k = (int)(i % K);
+  const int64_t n = i / K;
+  Wk[i] = __builtin_bit_cast(uint16_t, (__bf16)W[(int64_t)k * N + n]);
+}
+
+int launch_kmajor_w16(mb_ctx* ctx, const float* W, int K, int N, uint16_t* Wk) {
+  const int64_t n = (int64_t)K * N;
+  hipLaunchKernelGGL(k_kmajor_w16, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, W,
+                     K, N, Wk);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
 // Wk[n][k] = gamma[k] * W[k][n] (W [K][N] row-major; gamma null: 1), one
 // thread per output element, rounded as k_fold_ln rounds its product, so a
 // folded k-major copy holds the same values as the folded tiled one.
@@ -1306,6 +1542,35 @@ __global__ __launch_bounds__(256) void k_split_w(const float* __restrict__ Wt, i
     out[t] = h ? (__bf16)(v - (float)hi) : hi;
   }
   Wx[u] = __builtin_bit_cast(uint4, out);
+}
+
+// The W1 layout of k_gemm_x3 (bf16 weight storage): the high halves only,
+// per (strip, k block, column block j, lane) one 16-byte piece.
+__global__ __launch_bounds__(256) void k_split_w1(const float* __restrict__ Wt, int K, int N,
+                                                  bool tiled, uint4* __restrict__ Wx) {
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= (int64_t)(N / 64) * (K / kX3Block) * (kX3BlockU4 / 2)) return;
+  const int lane = (int)(u & 63), j = (int)((u >> 6) & 3);
+  const int64_t blk = u >> 8;  // strip * (K / 32) + k block
+  const int nkb = K / kX3Block;
+  const int64_t strip = blk / nkb;
+  const int kb = (int)(blk % nkb);
+  const int64_t k = kb * kX3Block + 8 * (lane >> 4), ld = tiled ? 64 : N;
+  const float* src = (tiled ? Wt + strip * K * 64 : Wt + strip * 64) + k * ld + 4 * (lane & 15) + j;
+  bf16x8_t out;
+#pragma unroll
+  for (int t = 0; t < 8; t++) out[t] = (__bf16)src[t * ld];
+  Wx[u] = __builtin_bit_cast(uint4, out);
+}
+
+int launch_split_w1(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled) {
+  if (N % 64 || K % kX3Block)
+    return fail(ctx, MB_ERR_ARG, "bf16 weights need N %% 64 == 0 and K %% 32 == 0 (K %d N %d)", K, N);
+  const int64_t n = (int64_t)(N / 64) * (K / kX3Block) * (kX3BlockU4 / 2);
+  hipLaunchKernelGGL(k_split_w1, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, ctx->stream, Wt,
+                     K, N, tiled, (uint4*)Wx);
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
 }
 
 int launch_split_w(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled) {

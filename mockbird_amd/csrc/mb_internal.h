@@ -80,7 +80,9 @@ struct LayerW {
   const float *ln2_w, *ln2_b, *fc_in_w, *fc_in_b, *fc_out_w, *fc_out_b;
   const float *attn_wg, *attn_c, *attn_d, *fc_in_wg, *fc_in_c, *fc_in_d;
   const float *proj_wt, *fc_out_wt;
-  const float *attn_wk, *fc_in_wk, *proj_wk, *fc_out_wk;
+  // k-major copies: fp32 with the LayerNorm gamma folded in, or, with bf16
+  // weight storage, bf16 and unscaled (the kernels apply gamma to the rows)
+  const void *attn_wk, *fc_in_wk, *proj_wk, *fc_out_wk;
   const void *attn_wx, *fc_in_wx, *proj_wx, *fc_out_wx;  // null in fp32-KV contexts
 };
 
@@ -94,7 +96,8 @@ struct ModelW {
   AudioTables audio_heads;
   // the audio heads with the local ln_f folded in (column-block-major and k-major;
   // split-bf16 in bf16-KV contexts, else null)
-  AudioTables head_wg, head_c, head_d, head_wk;
+  AudioTables head_wg, head_c, head_d;
+  const void* head_wk[NVQ];  // as LayerW's k-major copies
   const void* head_wx[NVQ];
 };
 
@@ -110,6 +113,9 @@ struct mb_ctx {
   // MultiprocessorCount / that); cus_per_xcd stays 0 when unknown
   int xcds = 8;
   int cus_per_xcd = 0;
+  // mb_set_weight_storage: the decoder's projection weights rounded to bf16
+  // and read as bf16 by the decode-sized kernels
+  bool w_bf16 = false;
   hipStream_t own_stream = nullptr;
   hipStream_t stream = nullptr;
   std::string err;
@@ -335,6 +341,25 @@ int launch_split_w(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool ti
 int launch_gemm_x3(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx, int N,
                    int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
                    const float* lnd);
+
+// bf16 weight storage (mb_set_weight_storage).  launch_round_bf16: Wr =
+// bf16(W) kept as fp32 (round to nearest even), the weights every other copy
+// derives from.  launch_kmajor_w16: Wk16[n][k] = bf16(W[k][n]).
+// launch_gemv_k16: launch_gemv_k on that copy; with lnc the LayerNorm is
+// folded in with gamma applied to the rows on the fly (c, d from
+// launch_fold_ln over Wr with gamma, W itself unscaled).  launch_split_w1:
+// the high halves of launch_split_w's layout (Wr is bf16-exact: no
+// remainder), which launch_gemm_x2 reads, two bf16 products per product;
+// gamma as for launch_gemv_k16 (only with lnc).
+int launch_round_bf16(mb_ctx* ctx, const float* W, int64_t n, float* Wr);
+int launch_kmajor_w16(mb_ctx* ctx, const float* W, int K, int N, uint16_t* Wk);
+int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint16_t* Wk,
+                    int N, int K, const float* bias, float* Cm, int64_t ldc, int M,
+                    const float* lnc, const float* lnd, const float* gamma);
+int launch_split_w1(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled = true);
+int launch_gemm_x2(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx1, int N,
+                   int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
+                   const float* lnd, const float* gamma);
 
 // layers.hip
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,

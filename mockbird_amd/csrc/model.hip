@@ -54,31 +54,57 @@ int tile(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, con
   return launch_tile_w(ctx, W, K, N, p);
 }
 
-// A k-major copy Wk[n][k] = gamma[k] W[k][n] of the [K][N] projection W
-// (launch_kmajor_w; gamma null: the plain transpose).
+// The k-major copy the GEMV kernels read of the [K][N] projection W:
+// Wk[n][k] = gamma[k] W[k][n] in fp32 (launch_kmajor_w; gamma null: the
+// plain transpose), or with bf16 weight storage bf16(W[k][n]) with no gamma
+// (the kernel applies it to the rows).
 int kmajor(mb_ctx* ctx, const std::string& name, const float* W, int K, int N, const float* gamma,
-           const float*& wk) {
-  float* p = internal_tensor(ctx, name, (int64_t)K * N);
+           const void*& wk) {
+  const int64_t n = (int64_t)K * N;
+  float* p = internal_tensor(ctx, name, ctx->w_bf16 ? (n + 1) / 2 : n);
   if (!p) return fail(ctx, MB_ERR_NOMEM, "k-major weight allocation failed (%s)", name.c_str());
   wk = p;
+  if (ctx->w_bf16) return launch_kmajor_w16(ctx, W, K, N, (uint16_t*)p);
   return launch_kmajor_w(ctx, W, K, N, gamma, p);
 }
 
-// The split-bf16 copy (launch_split_w) of a column-block-major [K][N]
-// projection Wt, for bf16-KV contexts; null in fp32-KV contexts.
-int split(mb_ctx* ctx, const std::string& name, const float* Wt, int K, int N, const void*& wx) {
+// The split-bf16 copy of a [K][N] projection for bf16-KV contexts (null in
+// fp32-KV contexts): of the column-block-major Wt (launch_split_w, gamma
+// already folded in where the LayerNorm is), or with bf16 weight storage
+// the high halves alone (launch_split_w1) of the row-major, unscaled W.
+int split(mb_ctx* ctx, const std::string& name, const float* Wt, const float* W, int K, int N,
+          const void*& wx) {
   wx = nullptr;
   if (ctx->cfg.kv_dtype != MB_KV_BF16) return MB_OK;
-  float* p = internal_tensor(ctx, name, (int64_t)K * N);  // 2 K N bf16
+  const int64_t n = (int64_t)K * N;  // 2 K N bf16, or K N with bf16 storage
+  float* p = internal_tensor(ctx, name, ctx->w_bf16 ? (n + 1) / 2 : n);
   if (!p) return fail(ctx, MB_ERR_NOMEM, "split weight allocation failed (%s)", name.c_str());
   wx = p;
+  if (ctx->w_bf16) return launch_split_w1(ctx, W, K, N, p, false);
   return launch_split_w(ctx, Wt, K, N, p);
 }
 
+// With bf16 weight storage: W <- bf16(W) in a copy of its own (the uploaded
+// tensor is left as it is), from which every other copy derives.
+int round_w(mb_ctx* ctx, const std::string& name, const float*& W, int64_t n) {
+  if (!ctx->w_bf16) return MB_OK;
+  float* p = internal_tensor(ctx, name, n);
+  if (!p) return fail(ctx, MB_ERR_NOMEM, "rounded weight allocation failed (%s)", name.c_str());
+  const int rc = launch_round_bf16(ctx, W, n, p);
+  W = p;
+  return rc;
+}
+
 int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
-  int rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
-                w.attn_d);
-  if (rc) return rc;
+  int rc;
+  if ((rc = round_w(ctx, key + ".attn.r", w.attn_w, (int64_t)D * QKV)) ||
+      (rc = round_w(ctx, key + ".proj.r", w.proj_w, (int64_t)D * D)) ||
+      (rc = round_w(ctx, key + ".fc_in.r", w.fc_in_w, (int64_t)D * FFN)) ||
+      (rc = round_w(ctx, key + ".fc_out.r", w.fc_out_w, (int64_t)FFN * D)))
+    return rc;
+  if ((rc = fold(ctx, key + ".attn", w.attn_w, D, QKV, w.ln1_w, w.ln1_b, w.attn_wg, w.attn_c,
+                 w.attn_d)))
+    return rc;
   if ((rc = tile(ctx, key + ".proj.t", w.proj_w, D, D, w.proj_wt))) return rc;
   if ((rc = tile(ctx, key + ".fc_out.t", w.fc_out_w, FFN, D, w.fc_out_wt))) return rc;
   if ((rc = kmajor(ctx, key + ".attn.k", w.attn_w, D, QKV, w.ln1_w, w.attn_wk))) return rc;
@@ -88,11 +114,31 @@ int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
   if ((rc = fold(ctx, key + ".fc_in", w.fc_in_w, D, FFN, w.ln2_w, w.ln2_b, w.fc_in_wg, w.fc_in_c,
                  w.fc_in_d)))
     return rc;
-  if ((rc = split(ctx, key + ".attn.x", w.attn_wg, D, QKV, w.attn_wx)) ||
-      (rc = split(ctx, key + ".fc_in.x", w.fc_in_wg, D, FFN, w.fc_in_wx)) ||
-      (rc = split(ctx, key + ".proj.x", w.proj_wt, D, D, w.proj_wx)))
+  if ((rc = split(ctx, key + ".attn.x", w.attn_wg, w.attn_w, D, QKV, w.attn_wx)) ||
+      (rc = split(ctx, key + ".fc_in.x", w.fc_in_wg, w.fc_in_w, D, FFN, w.fc_in_wx)) ||
+      (rc = split(ctx, key + ".proj.x", w.proj_wt, w.proj_w, D, D, w.proj_wx)))
     return rc;
-  return split(ctx, key + ".fc_out.x", w.fc_out_wt, FFN, D, w.fc_out_wx);
+  return split(ctx, key + ".fc_out.x", w.fc_out_wt, w.fc_out_w, FFN, D, w.fc_out_wx);
+}
+
+// The decode-sized projections: the GEMV kernel (k-major copy) and the
+// split-bf16 kernel, in the form the context's weight storage calls for.
+// `gamma` is the folded LayerNorm's (used with lnc under bf16 storage).
+int proj_gemv(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* wk, int N, int K,
+              const float* bias, float* C, int64_t ldc, int M, const float* lnc, const float* lnd,
+              const float* gamma) {
+  if (ctx->w_bf16)
+    return launch_gemv_k16(ctx, epi, A, lda, (const uint16_t*)wk, N, K, bias, C, ldc, M, lnc, lnd,
+                           lnc ? gamma : nullptr);
+  return launch_gemv_k(ctx, epi, A, lda, (const float*)wk, N, K, bias, C, ldc, M, lnc, lnd);
+}
+int proj_split(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* wx, int N, int K,
+               const float* bias, float* C, int64_t ldc, int M, const float* lnc, const float* lnd,
+               const float* gamma) {
+  if (ctx->w_bf16)
+    return launch_gemm_x2(ctx, epi, A, lda, wx, N, K, bias, C, ldc, M, lnc, lnd,
+                          lnc ? gamma : nullptr);
+  return launch_gemm_x3(ctx, epi, A, lda, wx, N, K, bias, C, ldc, M, lnc, lnd);
 }
 
 // Resolve every weight once per upload (gpu.ts:339-343 throws "weight not
@@ -133,10 +179,11 @@ int resolve(mb_ctx* ctx, bool global, bool local) {
     if ((rc = fold_layer(ctx, "#fold/local", m.local))) return rc;
     for (int k = 0; k < NVQ; k++) {
       const std::string p = "#fold/head" + std::to_string(k);
-      if ((rc = fold(ctx, p, m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.local_lnf_b,
+      if ((rc = round_w(ctx, p + ".r", m.audio_heads.t[k], (int64_t)D * CODES)) ||
+          (rc = fold(ctx, p, m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.local_lnf_b,
                      m.head_wg.t[k], m.head_c.t[k], m.head_d.t[k])) ||
-          (rc = kmajor(ctx, p + ".k", m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.head_wk.t[k])) ||
-          (rc = split(ctx, p + ".x", m.head_wg.t[k], D, CODES, m.head_wx[k])))
+          (rc = kmajor(ctx, p + ".k", m.audio_heads.t[k], D, CODES, m.local_lnf_w, m.head_wk[k])) ||
+          (rc = split(ctx, p + ".x", m.head_wg.t[k], m.audio_heads.t[k], D, CODES, m.head_wx[k])))
         return rc;
     }
     ctx->model_ok = true;
@@ -185,12 +232,12 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   // bf16-KV contexts: decode-sized projections as split-bf16 products
   const bool x3 = !gemv && folded && w.attn_wx && gemm_streams((int)M, D);
   if (gemv) {
-    if ((rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
-                            (int)M, w.attn_c, w.attn_d)))
+    if ((rc = proj_gemv(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
+                        (int)M, w.attn_c, w.attn_d, w.ln1_w)))
       return rc;
   } else if (x3) {
-    if ((rc = launch_gemm_x3(ctx, EPI_STORE, a.x, D, w.attn_wx, QKV, D, w.attn_b, a.qkv, QKV,
-                             (int)M, w.attn_c, w.attn_d)))
+    if ((rc = proj_split(ctx, EPI_STORE, a.x, D, w.attn_wx, QKV, D, w.attn_b, a.qkv, QKV,
+                         (int)M, w.attn_c, w.attn_d, w.ln1_w)))
       return rc;
   } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, w.attn_wg, QKV, D, w.attn_c, w.attn_d,
@@ -225,20 +272,20 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   if (rc) return rc;
   // decode sizes read the column-block-major copies of O and fc_out
   const bool tiled = gemm_streams((int)M, D);
-  if ((rc = gemv ? launch_gemv_k(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
-                                 nullptr, nullptr)
-           : x3 ? launch_gemm_x3(ctx, EPI_ADD, a.att, D, w.proj_wx, D, D, w.proj_b, a.x, D, (int)M,
-                                 nullptr, nullptr)
+  if ((rc = gemv ? proj_gemv(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
+                             nullptr, nullptr, nullptr)
+           : x3 ? proj_split(ctx, EPI_ADD, a.att, D, w.proj_wx, D, D, w.proj_b, a.x, D, (int)M,
+                             nullptr, nullptr, nullptr)
                 : launch_gemm(ctx, EPI_ADD, a.att, D, tiled ? w.proj_wt : w.proj_w, D, D, w.proj_b,
                               a.x, D, (int)M, tiled)))
     return rc;
   if (gemv) {
-    if ((rc = launch_gemv_k(ctx, EPI_GELU, a.x, D, w.fc_in_wk, FFN, D, w.fc_in_b, a.ffn, FFN,
-                            (int)M, w.fc_in_c, w.fc_in_d)))
+    if ((rc = proj_gemv(ctx, EPI_GELU, a.x, D, w.fc_in_wk, FFN, D, w.fc_in_b, a.ffn, FFN,
+                        (int)M, w.fc_in_c, w.fc_in_d, w.ln2_w)))
       return rc;
   } else if (x3) {
-    if ((rc = launch_gemm_x3(ctx, EPI_GELU, a.x, D, w.fc_in_wx, FFN, D, w.fc_in_b, a.ffn, FFN,
-                             (int)M, w.fc_in_c, w.fc_in_d)))
+    if ((rc = proj_split(ctx, EPI_GELU, a.x, D, w.fc_in_wx, FFN, D, w.fc_in_b, a.ffn, FFN,
+                         (int)M, w.fc_in_c, w.fc_in_d, w.ln2_w)))
       return rc;
   } else if (folded) {
     if ((rc = launch_gemm_ln(ctx, EPI_GELU, a.x, D, w.fc_in_wg, FFN, D, w.fc_in_c, w.fc_in_d,
@@ -250,11 +297,11 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
       return rc;
   }
   if (gemv)
-    return launch_gemv_k(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wk, D, FFN, w.fc_out_b, a.x, D, (int)M,
-                         nullptr, nullptr);
+    return proj_gemv(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wk, D, FFN, w.fc_out_b, a.x, D, (int)M,
+                     nullptr, nullptr, nullptr);
   if (x3)
-    return launch_gemm_x3(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wx, D, FFN, w.fc_out_b, a.x, D, (int)M,
-                          nullptr, nullptr);
+    return proj_split(ctx, EPI_ADD, a.ffn, FFN, w.fc_out_wx, D, FFN, w.fc_out_b, a.x, D, (int)M,
+                      nullptr, nullptr, nullptr);
   return launch_gemm(ctx, EPI_ADD, a.ffn, FFN, tiled ? w.fc_out_wt : w.fc_out_w, D, FFN, w.fc_out_b,
                      a.x, D, (int)M, tiled);
 }
@@ -387,11 +434,11 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
       float* lg = pick ? a.logits : probe->logits + (int64_t)ch * CODES;
       const int64_t ldl = pick ? CODES : (int64_t)NVQ * CODES;
       if (folded_head && B <= kGemvMaxM)
-        rc = launch_gemv_k(ctx, EPI_STORE, a.x, D, m.head_wk.t[ch], CODES, D, nullptr, lg, ldl, B,
-                           m.head_c.t[ch], m.head_d.t[ch]);
+        rc = proj_gemv(ctx, EPI_STORE, a.x, D, m.head_wk[ch], CODES, D, nullptr, lg, ldl, B,
+                       m.head_c.t[ch], m.head_d.t[ch], m.local_lnf_w);
       else if (folded_head && m.head_wx[ch] && gemm_streams(B, CODES))
-        rc = launch_gemm_x3(ctx, EPI_STORE, a.x, D, m.head_wx[ch], CODES, D, nullptr, lg, ldl, B,
-                            m.head_c.t[ch], m.head_d.t[ch]);
+        rc = proj_split(ctx, EPI_STORE, a.x, D, m.head_wx[ch], CODES, D, nullptr, lg, ldl, B,
+                        m.head_c.t[ch], m.head_d.t[ch], m.local_lnf_w);
       else if (folded_head)
         rc = launch_gemm_ln(ctx, EPI_STORE, a.x, D, m.head_wg.t[ch], CODES, D, m.head_c.t[ch],
                             m.head_d.t[ch], nullptr, lg, ldl, B);
@@ -450,6 +497,19 @@ int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, d
   ctx->end_id = audio_end_id;
   ctx->assistant_id = assistant_id;
   ctx->penalty = penalty;
+  return MB_OK;
+}
+
+int mb_set_weight_storage(mb_ctx* ctx, int32_t storage) {
+  if (!ctx) return MB_ERR_ARG;
+  if (storage != MB_W_F32 && storage != MB_W_BF16)
+    return fail(ctx, MB_ERR_ARG, "weight storage must be MB_W_F32 or MB_W_BF16");
+  const bool bf16 = storage == MB_W_BF16;
+  if (bf16 != ctx->w_bf16) {
+    ctx->w_bf16 = bf16;
+    ctx->model_ok = false;  // the copies are derived again, from the uploads
+    ctx->graph_gen++;
+  }
   return MB_OK;
 }
 

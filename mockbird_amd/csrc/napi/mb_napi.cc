@@ -477,6 +477,27 @@ napi_value SetLocalHead(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// setWeightStorage(h, "f32" | "bf16")
+napi_value SetWeightStorage(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  char buf[8] = {0};
+  size_t len = 0;
+  if (napi_get_value_string_utf8(env, a.at(1), buf, sizeof buf, &len) != napi_ok) {
+    napi_throw_type_error(env, nullptr, "weight storage must be \"f32\" or \"bf16\"");
+    return nullptr;
+  }
+  const std::string v(buf, len);
+  if (v != "f32" && v != "bf16") {
+    napi_throw_range_error(env, nullptr, "weight storage must be \"f32\" or \"bf16\"");
+    return nullptr;
+  }
+  int rc = mb_set_weight_storage(ctx, v == "bf16" ? MB_W_BF16 : MB_W_F32);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
 // ringReset(h, Int32Array seqIds | null) / clearSeen(h, Int32Array seqIds | null)
 template <int (*F)(mb_ctx*, int, const int32_t*)>
 napi_value SeqListCall(napi_env env, napi_callback_info info) {
@@ -828,6 +849,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"uploadTensor", UploadTensor},
       {"cancel", Cancel},
       {"setLocalHead", SetLocalHead},
+      {"setWeightStorage", SetWeightStorage},
       {"ringReset", SeqListCall<mb_ring_reset>},
       {"clearSeen", SeqListCall<mb_clear_seen>},
       {"ringPoison", RingPoison},

@@ -35,6 +35,8 @@ export type EngineOptions = {
   /** transformer layers the weights must resolve to (12) */
   layers?: number;
   kvDtype?: "f32" | "bf16";
+  /** projection weights rounded to and read as bf16 (mb_set_weight_storage) */
+  weightDtype?: "f32" | "bf16";
   /** false (default): the reference's non-wrapping global ring */
   wrap?: boolean;
   device?: number;

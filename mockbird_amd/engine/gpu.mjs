@@ -184,6 +184,8 @@ class HipTtsEngineImpl {
  * (createGpuEngineFor, gpu.ts:316-388).  `tables` = {global, local[, codec]}
  * WeightTables; options: {localHead, maxSlots (570), maxRows (= maxSlots),
  * layers (12: the count the model must resolve to), kvDtype ("f32" | "bf16"),
+ * weightDtype ("f32" | "bf16": projection weights rounded to and read as
+ * bf16, mb_set_weight_storage),
  * wrap (false: the reference's non-wrapping ring), device (0), codecShape
  * ({layersPerStage, contextPerStage}, the real shape by default),
  * codecKvDtype ("f32")}.  With a codec table the codec decoder is set up
@@ -209,6 +211,7 @@ export async function createGpuEngineFor(tables, log, options) {
     device: orDefault(options.device, 0),
   });
   try {
+    if (options.weightDtype) native.setWeightStorage(handle, options.weightDtype);
     let bytes = 0;
     for (const t of tensors) {
       native.uploadTensor(handle, t.name, t.data, t.dims);

@@ -20,6 +20,8 @@ export type MultiVoiceOptions = {
   capacity?: number;
   maxRows?: number;
   kvDtype?: "f32" | "bf16";
+  /** projection weights rounded to and read as bf16 (mb_set_weight_storage) */
+  weightDtype?: "f32" | "bf16";
   wrap?: boolean;
   device?: number;
   codecShape?: CodecShape;

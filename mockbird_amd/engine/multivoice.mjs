@@ -130,7 +130,7 @@ export class MultiVoiceEngine {
 
 /**
  * A context for `maxVoices` voices: options {localHead, maxVoices, capacity
- * (1024), maxRows (capacity), kvDtype ("bf16"), wrap (true), device (0),
+ * (1024), maxRows (capacity), kvDtype ("bf16"), weightDtype ("f32" | "bf16"), wrap (true), device (0),
  * codecShape, codecKvDtype ("bf16")}; a `codec` table sets up the codec for
  * every voice (decodeAudio).
  */
@@ -152,6 +152,7 @@ export async function createMultiVoiceEngine(tables, log, options) {
   try {
     for (const t of tensors) native.uploadTensor(handle, t.name, t.data, t.dims);
     const s = options.localHead;
+    if (options.weightDtype) native.setWeightStorage(handle, options.weightDtype);
     native.setLocalHead(handle, s.audioEndTokenId, s.audioAssistantSlotTokenId, s.repetitionPenalty);
     let hasCodec = false;
     if (tables.codec) {

@@ -27,6 +27,7 @@ export interface Native {
   uploadTensor(h: NativeHandle, name: string, data: Float32Array, dims: number[]): void;
   cancel(h: NativeHandle, on?: boolean): void;
   setLocalHead(h: NativeHandle, audioEnd: number, assistant: number, penalty: number): void;
+  setWeightStorage(h: NativeHandle, storage: "f32" | "bf16"): void;
   ringReset(h: NativeHandle, seqIds: Int32Array | null): void;
   clearSeen(h: NativeHandle, seqIds: Int32Array | null): void;
   ringPoison(h: NativeHandle, layer: number, seq: number, nSlots: number, sentinel: number): void;

@@ -1,0 +1,113 @@
+"""GPU parity of bf16 weight storage (mb_set_weight_storage(MB_W_BF16)).
+
+With bf16 storage the decoder's projection weights -- c_attn, c_proj,
+fc_in, fc_out of every layer and of the local layer, and the 16 audio heads
+-- are rounded to bf16 once and read as bf16; products and sums stay fp32.
+The oracle is therefore run on the same model with exactly those tensors
+rounded to bf16 (round to nearest even, oracle.bf16_round) and everything
+else unchanged, and the GPU must match it to the bars of the fp32-storage
+tests: hidden states and logits within 1e-4 (fp32 K/V) or 2e-2 (bf16 K/V),
+codes exact up to counted near ties.  The model has non-trivial LayerNorm
+scales and biases, so the LayerNorm scale that bf16 storage applies to the
+rows instead of folding into the weights is exercised.
+
+Voice counts pick the kernels: 3 voices run the GEMV kernel on the bf16
+k-major copies, 12 voices the two-product split-bf16 kernel (bf16 K/V) or
+the folded fp32 streaming kernel on the rounded weights (fp32 K/V).
+"""
+import numpy as np
+import pytest
+
+import mockbird_amd as mb
+from mockbird_amd import synth
+from oracle import oracle
+from conftest import say
+from frame_check import FrameCheck
+
+pytestmark = pytest.mark.gpu
+
+TOL = {mb.MB_KV_F32: 1e-4, mb.MB_KV_BF16: 2e-2}
+ROUNDED = ("attn.c_attn.weight", "attn.c_proj.weight", "mlp.fc_in.weight", "mlp.fc_out.weight")
+
+
+def rounded_weights(w):
+    """The model as bf16 storage holds it: the projection matrices and the
+    audio heads rounded to bf16, everything else as uploaded."""
+    out = dict(w)
+    for name, a in w.items():
+        if name.endswith(ROUNDED) or name.startswith("model.audio_lm_heads."):
+            out[name] = oracle.bf16_round(a)
+    return out
+
+
+def _prompts(B, V):
+    prompts = [synth.prompt(20 + b, n_frames=3 + 4 * b, n_text=4 + b % 5, vocab=V) for b in range(B)]
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    ids[:, :, 0] = 0
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    return ids, n
+
+
+@pytest.mark.parametrize("kv,B", [(mb.MB_KV_F32, 3), (mb.MB_KV_F32, 12), (mb.MB_KV_BF16, 3),
+                                  (mb.MB_KV_BF16, 12)])
+def test_bf16_weights_prefill_decode_frames(kv, B):
+    say(f"bf16 weights: kv={kv} voices={B}")
+    L, V, C = 2, 64, 128
+    w = synth.model_weights(n_layers=L, vocab=V, seed=11, bias_std=0.02, ln_std=0.1)
+    m = oracle.Model(rounded_weights(w), n_layers=L, vocab=V)
+    m_f32 = oracle.Model(w, n_layers=L, vocab=V)
+    ids, n = _prompts(B, V)
+    st = oracle.ModelState(m, B, C, kv_bf16=(kv == mb.MB_KV_BF16))
+    chk = FrameCheck(B)
+    with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=96, kv_dtype=kv, vocab=V) as ctx:
+        ctx.upload_all(w)
+        ctx.set_weight_storage(mb.MB_W_BF16)
+        h = ctx.prefill(ids, n)
+        h_or = st.prefill(ids, n)
+        assert np.abs(h - h_or).max() < TOL[kv]
+        if kv == mb.MB_KV_F32:
+            # the storage took effect: the unrounded model is much further away
+            st32 = oracle.ModelState(m_f32, B, C)
+            far = float(np.abs(h - st32.prefill(ids, n)).max())
+            assert far > 10 * float(np.abs(h - h_or).max()), far
+        pos = n.copy()
+        for f in range(5):
+            codes, cont = ctx.local_frame(h)
+            g_text, g_logits = ctx.local_logits(h, codes)
+            for b in range(B):
+                o_text, o_logits = m.local_logits(h_or[b], codes[b])
+                chk.frame(b, f"frame {f} voice {b}", codes[b], cont[b], o_text, o_logits, TOL[kv],
+                          g_text[b], g_logits[b])
+            rows = np.stack([synth.frame_row(codes[b]) for b in range(B)])
+            h = ctx.decode_step(rows, pos)
+            h_or = st.decode_step(rows, pos)
+            assert np.abs(h - h_or).max() < TOL[kv], f
+            pos = pos + 1
+    chk.summary(f"bf16 weights kv={kv} voices={B}")
+    assert chk.codes_equal + chk.codes_tied >= 16 * 5  # at least one voice went on every frame
+
+
+def test_weight_storage_switches_back():
+    """MB_W_BF16, then MB_W_F32 again on the same context: the copies are
+    derived again and the fp32 model's results come back."""
+    say("bf16 weights: switch back to fp32")
+    L, V, B, C = 1, 32, 2, 64
+    w = synth.model_weights(n_layers=L, vocab=V, seed=5, bias_std=0.02, ln_std=0.1)
+    ids, n = _prompts(B, V)
+    want32 = oracle.ModelState(oracle.Model(w, n_layers=L, vocab=V), B, C).prefill(ids, n)
+    want16 = oracle.ModelState(oracle.Model(rounded_weights(w), n_layers=L, vocab=V), B,
+                               C).prefill(ids, n)
+    with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=64, vocab=V) as ctx:
+        ctx.upload_all(w)
+        assert np.abs(ctx.prefill(ids, n) - want32).max() < 1e-4
+        ctx.set_weight_storage(mb.MB_W_BF16)
+        ctx.ring_reset()
+        assert np.abs(ctx.prefill(ids, n) - want16).max() < 1e-4
+        ctx.set_weight_storage(mb.MB_W_F32)
+        ctx.ring_reset()
+        assert np.abs(ctx.prefill(ids, n) - want32).max() < 1e-4
+        with pytest.raises(mb.MbError) as e:
+            ctx.set_weight_storage(7)
+        assert e.value.code == mb.MB_ERR_ARG
