@@ -1138,66 +1138,92 @@ static int gemv_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const 
 // sums x - x0 and (x - x0)^2 over the rows it loads (x0 = x[m][0]) and
 // applies the folded LayerNorm itself.  The grid is N / 4 workgroups (192
 // for 768 outputs, 768 for 3072), and every output is a fixed-order sum.
-template <int EPI, bool LNF, int MR>
-__global__ __launch_bounds__(256) void k_gemv_k(
+// KC > 0: K == KC known at compile time, so every round of loads is a fixed
+// set of unconditional loads (no branch around a load: the compiler then
+// leaves them in flight across the epilogue operands' waits); KC = 0: any K,
+// in a run-time loop.
+// (At most 4 waves per SIMD are asked for: a grid is N / 4 workgroups, one
+// column per wave, so at 768 and 3072 columns there are 0.75 and 3 waves per
+// SIMD, and the registers go to keeping every load of a round in flight.)
+template <int EPI, bool LNF, int MR, int KC = 0>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_gemv_k(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ Wk, int N, int K,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     const float* __restrict__ lnc, const float* __restrict__ lnd) {
   constexpr int RI = MR <= 2 ? 12 : MR <= 4 ? 6 : 3;  // k steps (256 rows each) per round of loads
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + wave;
-  const float* wp = Wk + (int64_t)n * K + 4 * lane;
-  // lane m < M finishes row m: its epilogue operands, loaded under the main loop
-  float ep_b = 0.f, ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
-  if (lane < M) {
-    if (bias) ep_b = bias[n];
-    if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)lane * ldc + n];
-    if (LNF) {
-      ep_cv = lnc[n];
-      ep_dv = lnd[n];
-    }
+  const float* wp = Wk + (int64_t)n * K;
+  // Every load is unconditional (addresses clamped into the operands, the
+  // values of rows >= M and of k >= K never used), so the compiler counts the
+  // same loads on every path: the weight loads issue right behind the
+  // epilogue operands instead of after a wait for them.
+  const int le = min(lane, M - 1);  // lane m < M finishes row m
+  const float* bp = bias ? bias : A;
+  float ep_b = bp[bias ? n : 0], ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
+  if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)le * ldc + n];
+  if (LNF) {
+    ep_cv = lnc[n];
+    ep_dv = lnd[n];
   }
   float acc[MR], s1[MR], s2[MR], x0[MR];
 #pragma unroll
   for (int m = 0; m < MR; m++) {
     acc[m] = s1[m] = s2[m] = 0.f;
-    x0[m] = LNF && m < M ? A[(int64_t)m * lda] : 0.f;
+    x0[m] = LNF ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
   }
-  const int steps = (K + 255) >> 8;
-  for (int i0 = 0; i0 < steps; i0 += RI) {
-    float4 w[RI], a[RI][MR];
+  const int Kx = KC > 0 ? KC : K;  // a constant where the launch fixed it
+  // one k step (256 k): lane l's float4 at k = 256 step + 4 l.  Lanes past K
+  // (only in a last, partial step) add zeros: no branch, so no load is sunk
+  // into one.
+  auto step_mac = [&](int st, float4 w, const float4* a) {
+    const bool in = st * 256 + 4 * lane < Kx;
+    if (!in) w = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < RI; i++) {
-      const int k = (i0 + i) * 256 + 4 * lane;
-      if (i0 + i < steps && k < K) w[i] = *(const float4*)(wp + (int64_t)(i0 + i) * 256);
-    }
+    for (int m = 0; m < MR; m++) {
+      acc[m] = fmaf(a[m].x, w.x, acc[m]);
+      acc[m] = fmaf(a[m].y, w.y, acc[m]);
+      acc[m] = fmaf(a[m].z, w.z, acc[m]);
+      acc[m] = fmaf(a[m].w, w.w, acc[m]);
+      if (LNF) {
+        const float x0m = in ? x0[m] : 0.f;
+        const float e[4] = {in ? a[m].x - x0m : 0.f, in ? a[m].y - x0m : 0.f,
+                            in ? a[m].z - x0m : 0.f, in ? a[m].w - x0m : 0.f};
 #pragma unroll
-    for (int i = 0; i < RI; i++) {
-      const int k = (i0 + i) * 256 + 4 * lane;
-#pragma unroll
-      for (int m = 0; m < MR; m++)
-        a[i][m] = i0 + i < steps && k < K && m < M ? *(const float4*)(A + (int64_t)m * lda + k)
-                                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int i = 0; i < RI; i++) {
-      if (i0 + i >= steps || (i0 + i) * 256 + 4 * lane >= K) continue;
-#pragma unroll
-      for (int m = 0; m < MR; m++) {
-        acc[m] = fmaf(a[i][m].x, w[i].x, acc[m]);
-        acc[m] = fmaf(a[i][m].y, w[i].y, acc[m]);
-        acc[m] = fmaf(a[i][m].z, w[i].z, acc[m]);
-        acc[m] = fmaf(a[i][m].w, w[i].w, acc[m]);
-        if (LNF) {
-          const float e[4] = {a[i][m].x - x0[m], a[i][m].y - x0[m], a[i][m].z - x0[m],
-                              a[i][m].w - x0[m]};
-#pragma unroll
-          for (int j = 0; j < 4; j++) {
-            s1[m] += e[j];
-            s2[m] = fmaf(e[j], e[j], s2[m]);
-          }
+        for (int j = 0; j < 4; j++) {
+          s1[m] += e[j];
+          s2[m] = fmaf(e[j], e[j], s2[m]);
         }
       }
+    }
+  };
+  auto step_load = [&](int st, float4& w, float4* a) {
+    const int k = min(st * 256 + 4 * lane, Kx - 4);
+    w = *(const float4*)(wp + k);
+#pragma unroll
+    for (int m = 0; m < MR; m++) a[m] = *(const float4*)(A + (int64_t)min(m, M - 1) * lda + k);
+  };
+  if constexpr (KC > 0) {
+    constexpr int SPR = (KC + 255) / 256;
+    constexpr int RK = SPR < RI ? SPR : RI;
+    static_for<(SPR + RK - 1) / RK>([&](auto r_) {
+      constexpr int r = decltype(r_)::value;
+      constexpr int NI = (r + 1) * RK <= SPR ? RK : SPR - r * RK;
+      float4 w[NI], a[NI][MR];
+#pragma unroll
+      for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], a[i]);
+      asm volatile("" ::: "memory");  // the round's loads stay in front, none sunk into a branch
+#pragma unroll
+      for (int i = 0; i < NI; i++) step_mac(r * RK + i, w[i], a[i]);
+    });
+  } else {
+    const int steps = (K + 255) >> 8;
+    for (int i0 = 0; i0 < steps; i0 += RI) {
+      float4 w[RI], a[RI][MR];
+#pragma unroll
+      for (int i = 0; i < RI; i++) step_load(i0 + i, w[i], a[i]);
+#pragma unroll
+      for (int i = 0; i < RI; i++) step_mac(i0 + i, w[i], a[i]);
     }
   }
   auto fold = [](float v) {
@@ -1221,6 +1247,7 @@ __global__ __launch_bounds__(256) void k_gemv_k(
     }
   }
   if (lane >= M) return;
+  if (!bias) ep_b = 0.f;
   float o = mine;
   if (LNF) {
     const float inv_k = 1.f / (float)K;
@@ -1251,18 +1278,28 @@ int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float
   if (lnf && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
     return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
   const dim3 grid((unsigned)(N / 4));
+  // one row at the model's two widths: k loops fixed at compile time
+  const int kc = M == 1 && (K == D || K == FFN) ? K : 0;
   with_epi(epi, [&](auto e) {
     constexpr int E = decltype(e)::value;
     auto go = [&](auto mr) {
       constexpr int MRv = decltype(mr)::value;
-      if (lnf) {
-        if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
-          hipLaunchKernelGGL((k_gemv_k<E, true, MRv>), grid, dim3(256), 0, ctx->stream, A, lda, Wk,
-                             N, K, bias, Cm, ldc, M, lnc, lnd);
-      } else {
-        hipLaunchKernelGGL((k_gemv_k<E, false, MRv>), grid, dim3(256), 0, ctx->stream, A, lda, Wk,
-                           N, K, bias, Cm, ldc, M, lnc, lnd);
+      auto launch = [&](auto kc_) {
+        constexpr int KCv = decltype(kc_)::value;
+        if (lnf) {
+          if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
+            hipLaunchKernelGGL((k_gemv_k<E, true, MRv, KCv>), grid, dim3(256), 0, ctx->stream, A,
+                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd);
+        } else {
+          hipLaunchKernelGGL((k_gemv_k<E, false, MRv, KCv>), grid, dim3(256), 0, ctx->stream, A,
+                             lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd);
+        }
+      };
+      if constexpr (MRv == 1) {
+        if (kc == D) return launch(std::integral_constant<int, D>{});
+        if (kc == FFN) return launch(std::integral_constant<int, FFN>{});
       }
+      launch(std::integral_constant<int, 0>{});
     };
     if (M <= 1) go(std::integral_constant<int, 1>{});
     else if (M <= 2) go(std::integral_constant<int, 2>{});
@@ -1286,8 +1323,8 @@ int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float
 // contiguous per load), with the matching two float4 of every A row (and of
 // gamma with GAM), all issued before the first multiply-add.  The LayerNorm
 // sums of LNF are taken over the raw rows, as in k_gemv_k.
-template <int EPI, bool LNF, bool GAM, int MR>
-__global__ __launch_bounds__(256) void k_gemv_k16(
+template <int EPI, bool LNF, bool GAM, int MR, int KC = 0>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_gemv_k16(
     const float* __restrict__ A, int64_t lda, const uint16_t* __restrict__ Wk, int N, int K,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     const float* __restrict__ lnc, const float* __restrict__ lnd,
@@ -1295,70 +1332,89 @@ __global__ __launch_bounds__(256) void k_gemv_k16(
   constexpr int RI = MR <= 2 ? 6 : MR <= 4 ? 3 : 2;  // k steps (512 each) per round of loads
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + wave;
-  const uint16_t* wp = Wk + (int64_t)n * K + 8 * lane;
-  float ep_b = 0.f, ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
-  if (lane < M) {
-    if (bias) ep_b = bias[n];
-    if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)lane * ldc + n];
-    if (LNF) {
-      ep_cv = lnc[n];
-      ep_dv = lnd[n];
-    }
+  const uint16_t* wp = Wk + (int64_t)n * K;
+  // unconditional, clamped loads, as in k_gemv_k
+  const int le = min(lane, M - 1);
+  const float* bp = bias ? bias : A;
+  float ep_b = bp[bias ? n : 0], ep_c = 0.f, ep_cv = 0.f, ep_dv = 0.f;
+  if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ep_c = Cm[(int64_t)le * ldc + n];
+  if (LNF) {
+    ep_cv = lnc[n];
+    ep_dv = lnd[n];
   }
   float acc[MR], s1[MR], s2[MR], x0[MR];
 #pragma unroll
   for (int m = 0; m < MR; m++) {
     acc[m] = s1[m] = s2[m] = 0.f;
-    x0[m] = LNF && m < M ? A[(int64_t)m * lda] : 0.f;
+    x0[m] = LNF ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
   }
-  const int steps = (K + 511) >> 9;
-  for (int i0 = 0; i0 < steps; i0 += RI) {
-    uint4 w[RI];
-    float4 a[RI][MR][2], g[RI][2];
-#pragma unroll
-    for (int i = 0; i < RI; i++) {
-      const int k = (i0 + i) * 512 + 8 * lane;
-      const bool in = i0 + i < steps && k < K;
-      w[i] = in ? *(const uint4*)(wp + (int64_t)(i0 + i) * 512) : make_uint4(0, 0, 0, 0);
-      if (GAM) {
-        g[i][0] = in ? *(const float4*)(gamma + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-        g[i][1] = in ? *(const float4*)(gamma + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int m = 0; m < MR; m++) {
-        const bool am = in && m < M;
-        a[i][m][0] = am ? *(const float4*)(A + (int64_t)m * lda + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-        a[i][m][1] = am ? *(const float4*)(A + (int64_t)m * lda + k + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+  const int Kx = KC > 0 ? KC : K;  // a constant where the launch fixed it
+  auto step_load = [&](int st, uint4& w, float4* g, float4 (*a)[2]) {
+    const int k = min(st * 512 + 8 * lane, Kx - 8);
+    w = *(const uint4*)(wp + k);
+    if (GAM) {
+      g[0] = *(const float4*)(gamma + k);
+      g[1] = *(const float4*)(gamma + k + 4);
     }
 #pragma unroll
-    for (int i = 0; i < RI; i++) {
-      if (i0 + i >= steps || (i0 + i) * 512 + 8 * lane >= K) continue;
-      const uint32_t wb[4] = {w[i].x, w[i].y, w[i].z, w[i].w};
-      float wf[8], gf[8];
+    for (int m = 0; m < MR; m++) {
+      const float* ar = A + (int64_t)min(m, M - 1) * lda + k;
+      a[m][0] = *(const float4*)ar;
+      a[m][1] = *(const float4*)(ar + 4);
+    }
+  };
+  // lanes past K (only in a last, partial step) add zeros, with no branch
+  auto step_mac = [&](int st, const uint4& w, const float4* g, const float4 (*a)[2]) {
+    const bool in = st * 512 + 8 * lane < Kx;
+    const uint32_t wb[4] = {in ? w.x : 0u, in ? w.y : 0u, in ? w.z : 0u, in ? w.w : 0u};
+    float wf[8], gf[8];
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        wf[2 * t] = __uint_as_float(wb[t] << 16);
-        wf[2 * t + 1] = __uint_as_float(wb[t] & 0xFFFF0000u);
-      }
-      if (GAM) {
-        gf[0] = g[i][0].x; gf[1] = g[i][0].y; gf[2] = g[i][0].z; gf[3] = g[i][0].w;
-        gf[4] = g[i][1].x; gf[5] = g[i][1].y; gf[6] = g[i][1].z; gf[7] = g[i][1].w;
-      }
+    for (int t = 0; t < 4; t++) {
+      wf[2 * t] = __uint_as_float(wb[t] << 16);
+      wf[2 * t + 1] = __uint_as_float(wb[t] & 0xFFFF0000u);
+    }
+    if (GAM) {
+      gf[0] = g[0].x; gf[1] = g[0].y; gf[2] = g[0].z; gf[3] = g[0].w;
+      gf[4] = g[1].x; gf[5] = g[1].y; gf[6] = g[1].z; gf[7] = g[1].w;
+    }
 #pragma unroll
-      for (int m = 0; m < MR; m++) {
-        const float av[8] = {a[i][m][0].x, a[i][m][0].y, a[i][m][0].z, a[i][m][0].w,
-                             a[i][m][1].x, a[i][m][1].y, a[i][m][1].z, a[i][m][1].w};
+    for (int m = 0; m < MR; m++) {
+      const float av[8] = {a[m][0].x, a[m][0].y, a[m][0].z, a[m][0].w,
+                           a[m][1].x, a[m][1].y, a[m][1].z, a[m][1].w};
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
-          acc[m] = fmaf(GAM ? __fmul_rn(av[t], gf[t]) : av[t], wf[t], acc[m]);
-          if (LNF) {
-            const float e = av[t] - x0[m];
-            s1[m] += e;
-            s2[m] = fmaf(e, e, s2[m]);
-          }
+      for (int t = 0; t < 8; t++) {
+        acc[m] = fmaf(GAM ? __fmul_rn(av[t], gf[t]) : av[t], wf[t], acc[m]);
+        if (LNF) {
+          const float e = in ? av[t] - x0[m] : 0.f;
+          s1[m] += e;
+          s2[m] = fmaf(e, e, s2[m]);
         }
       }
+    }
+  };
+  if constexpr (KC > 0) {
+    constexpr int SPR = (KC + 511) / 512;
+    constexpr int RK = SPR < RI ? SPR : RI;
+    static_for<(SPR + RK - 1) / RK>([&](auto r_) {
+      constexpr int r = decltype(r_)::value;
+      constexpr int NI = (r + 1) * RK <= SPR ? RK : SPR - r * RK;
+      uint4 w[NI];
+      float4 g[NI][2], a[NI][MR][2];
+#pragma unroll
+      for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], g[i], a[i]);
+      asm volatile("" ::: "memory");  // the round's loads stay in front, none sunk into a branch
+#pragma unroll
+      for (int i = 0; i < NI; i++) step_mac(r * RK + i, w[i], g[i], a[i]);
+    });
+  } else {
+    const int steps = (K + 511) >> 9;
+    for (int i0 = 0; i0 < steps; i0 += RI) {
+      uint4 w[RI];
+      float4 g[RI][2], a[RI][MR][2];
+#pragma unroll
+      for (int i = 0; i < RI; i++) step_load(i0 + i, w[i], g[i], a[i]);
+#pragma unroll
+      for (int i = 0; i < RI; i++) step_mac(i0 + i, w[i], g[i], a[i]);
     }
   }
   auto fold = [](float v) {
@@ -1382,6 +1438,7 @@ __global__ __launch_bounds__(256) void k_gemv_k16(
     }
   }
   if (lane >= M) return;
+  if (!bias) ep_b = 0.f;
   float o = mine;
   if (LNF) {
     const float inv_k = 1.f / (float)K;
@@ -1412,23 +1469,32 @@ int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uin
   if (lnf && epi != EPI_STORE && epi != EPI_GELU && epi != EPI_GELU_ERF)
     return fail(ctx, MB_ERR_ARG, "folded LayerNorm gemm has no epilogue %d", epi);
   const dim3 grid((unsigned)(N / 4));
+  const int kc = M == 1 && (K == D || K == FFN) ? K : 0;  // as launch_gemv_k
   with_epi(epi, [&](auto e) {
     constexpr int E = decltype(e)::value;
     auto go = [&](auto mr) {
       constexpr int MRv = decltype(mr)::value;
-      if (lnf) {
-        if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF) {
-          if (gamma)
-            hipLaunchKernelGGL((k_gemv_k16<E, true, true, MRv>), grid, dim3(256), 0, ctx->stream, A,
-                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
-          else
-            hipLaunchKernelGGL((k_gemv_k16<E, true, false, MRv>), grid, dim3(256), 0, ctx->stream, A,
-                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+      auto launch = [&](auto kc_) {
+        constexpr int KCv = decltype(kc_)::value;
+        if (lnf) {
+          if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF) {
+            if (gamma)
+              hipLaunchKernelGGL((k_gemv_k16<E, true, true, MRv, KCv>), grid, dim3(256), 0,
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+            else
+              hipLaunchKernelGGL((k_gemv_k16<E, true, false, MRv, KCv>), grid, dim3(256), 0,
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+          }
+        } else {
+          hipLaunchKernelGGL((k_gemv_k16<E, false, false, MRv, KCv>), grid, dim3(256), 0,
+                             ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
         }
-      } else {
-        hipLaunchKernelGGL((k_gemv_k16<E, false, false, MRv>), grid, dim3(256), 0, ctx->stream, A,
-                           lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+      };
+      if constexpr (MRv == 1) {
+        if (kc == D) return launch(std::integral_constant<int, D>{});
+        if (kc == FFN) return launch(std::integral_constant<int, FFN>{});
       }
+      launch(std::integral_constant<int, 0>{});
     };
     if (M <= 1) go(std::integral_constant<int, 1>{});
     else if (M <= 2) go(std::integral_constant<int, 2>{});
