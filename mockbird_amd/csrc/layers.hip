@@ -231,6 +231,7 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
     v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
   }
   const uint32_t word = sm[lane >> 1];
+  const bool go_on = !cont || cont[b];  // loaded with the logits, not after the choice
   const uint32_t bits = (word >> (16 * (lane & 1))) & 0xffffu;
   // the penalty applies once the channel has emitted anything (policy.ts:282)
   const bool any = __ballot(word != 0u) != 0ull;
@@ -255,11 +256,14 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
       idx = oi;
     }
   }
-  // the butterfly leaves every lane with the same winner
+  // the butterfly leaves every lane with the same winner; the seen word it
+  // updates is already in a register (lanes 2w and 2w + 1 hold word w), so
+  // the update is a store with no load in front of it
   const int tok = idx == 0x7fffffff ? 0 : idx;
+  const uint32_t wtok = __shfl(word, (tok >> 5) * 2);
   if (lane == 0) {
     tokens[b * NVQ + ch] = tok;
-    if (!cont || cont[b]) sm[tok >> 5] |= 1u << (tok & 31);
+    if (go_on) sm[tok >> 5] = wtok | (1u << (tok & 31));
   }
   if (x) copy_row(next_emb, tok, x, b, lane);
 }

@@ -594,25 +594,41 @@ __global__ __launch_bounds__(256) void k_attn_short(
   const char* vbase = (const char*)(ring_v + kv_off);
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
-  // the window's K and V rows and stored positions, issued before the append
+  // Every load is issued up front and unconditionally: the ring's K and V
+  // rows and stored positions (slots clamped into the ring, so they do not
+  // wait for the position; slots past the window are masked below), the
+  // q | k | v row, and the RoPE table entries of the position (clamped; a
+  // position beyond the table is evaluated after them, as rope_cs does).
+  // With no branch around a load the compiler waits once, for all of them.
   uint4 kr[U], vr[U];
-  const int32_t spl = (lane < GU && lane < nvalid) ? sp[lane] : -1;
+  const int32_t spl = sp[min(lane, C - 1)];
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int slot = u * G + g;
-    const int sl = slot < nvalid ? slot : 0;
+    const int sl = slot < C ? slot : 0;
     kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
     vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
   }
 
   const int64_t roff = row_at(q_rows, b, 0) + head * HD + sub * VD;
-  float qi[VD], qo[VD], cs[VD / 2], sn[VD / 2], qv[VD];
+  float qi[VD], qo[VD], cs[VD / 2], sn[VD / 2], qv[VD], ki[VD], vi[VD];
   load_n<IN_BF16, VD>(qkv, roff, qi);
+  load_n<IN_BF16, VD>(qkv, roff + D, ki);
+  load_n<IN_BF16, VD>(qkv, roff + 2 * D, vi);
   const bool have = cur >= 0 && cur < C;
   const int32_t pos = (int32_t)(have ? cur : 0);
   const int slot_new = have ? (int)cur : -1;
+  const int32_t tpos = pos < kRopeTab ? pos : kRopeTab - 1;
 #pragma unroll
-  for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+  for (int j = 0; j < VD / 2; j++) {
+    const float2 t = rope_tab[(int64_t)tpos * 32 + (sub * VD >> 1) + j];
+    cs[j] = t.x;
+    sn[j] = t.y;
+  }
+  if (pos >= kRopeTab) {  // uniform
+#pragma unroll
+    for (int j = 0; j < VD / 2; j++) rope_cs(rope_tab, pos, (sub * VD >> 1) + j, cs[j], sn[j]);
+  }
 #pragma unroll
   for (int j = 0; j < VD / 2; j++) rope_pair(qi[2 * j], qi[2 * j + 1], cs[j], sn[j], qo[2 * j], qo[2 * j + 1]);
   if (q_out && g == 0) {
@@ -623,9 +639,7 @@ __global__ __launch_bounds__(256) void k_attn_short(
   for (int i = 0; i < VD; i++) qv[i] = qo[i] * 0.125f;
   uint4 knew = make_uint4(0, 0, 0, 0), vnew = make_uint4(0, 0, 0, 0);
   if (slot_new >= 0) {  // wave-uniform
-    float ki[VD], vi[VD], ko[VD];
-    load_n<IN_BF16, VD>(qkv, roff + D, ki);
-    load_n<IN_BF16, VD>(qkv, roff + 2 * D, vi);
+    float ko[VD];
 #pragma unroll
     for (int j = 0; j < VD / 2; j++)
       rope_pair(ki[2 * j], ki[2 * j + 1], cs[j], sn[j], ko[2 * j], ko[2 * j + 1]);
@@ -639,7 +653,7 @@ __global__ __launch_bounds__(256) void k_attn_short(
   }
 
   const int64_t dlt = cur - (int64_t)spl;
-  const uint64_t live = __ballot(spl >= 0 && dlt >= 0 && dlt < C);
+  const uint64_t live = __ballot(lane < GU && lane < nvalid && spl >= 0 && dlt >= 0 && dlt < C);
   float sc[U], mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < U; u++) {
