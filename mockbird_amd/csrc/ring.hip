@@ -594,18 +594,19 @@ __global__ __launch_bounds__(256) void k_attn_short(
   const char* vbase = (const char*)(ring_v + kv_off);
   const int32_t* sp = slot_pos + (int64_t)b * C;
 
-  // Every load is issued up front and unconditionally: the ring's K and V
-  // rows and stored positions (slots clamped into the ring, so they do not
-  // wait for the position; slots past the window are masked below), the
-  // q | k | v row, and the RoPE table entries of the position (clamped; a
-  // position beyond the table is evaluated after them, as rope_cs does).
-  // With no branch around a load the compiler waits once, for all of them.
+  // Every load is issued up front and unconditionally: the window's K and V
+  // rows and stored positions (slots past the window clamped to slot 0, so
+  // a short window -- the local head's ring fills one slot per step -- reads
+  // no more lines than it holds; they are masked below), the q | k | v row,
+  // and the RoPE table entries of the position (clamped; a position beyond
+  // the table is evaluated after them, as rope_cs does).  With no branch
+  // around a load the compiler waits once, for all of them.
   uint4 kr[U], vr[U];
-  const int32_t spl = sp[min(lane, C - 1)];
+  const int32_t spl = sp[lane < nvalid ? lane : 0];
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int slot = u * G + g;
-    const int sl = slot < C ? slot : 0;
+    const int sl = slot < nvalid ? slot : 0;
     kr[u] = load_stream(kbase + (int64_t)sl * ROWB);
     vr[u] = load_stream(vbase + (int64_t)sl * ROWB);
   }
