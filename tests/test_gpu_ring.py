@@ -342,6 +342,42 @@ def test_append_attend_equals_append_then_attention(name, kv):
         assert np.array_equal(out_a, twin.decode_attention(0, q_t, pos))
 
 
+@pytest.mark.parametrize("name,kv", KV)
+def test_few_units_long_windows(name, kv):
+    """Launches of few (query, head) units take more waves per block (enough
+    to read the window in one batch each, up to the cap): 2 sequences (24
+    units) with windows of 700 to 2048 slots, one of them wrapped, through
+    the fused append + attention and the two-launch path, against the oracle
+    at every step and bit-exact between the two paths."""
+    say(f"long windows (few units) kv={name}")
+    B, C = 2, 2048
+    rng = np.random.default_rng(33)
+    pos = np.array([700, 2300], np.int32)
+    with mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=128, kv_dtype=kv) as fused, \
+            mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=128, kv_dtype=kv) as twin:
+        ring = _oracle_ring(B, C, kv)
+        start = np.maximum(0, pos - C + 1).astype(np.int32)
+        n = (pos - start).astype(np.int32)
+        for c0 in range(0, int(n.max()), 128):
+            fill = rng.standard_normal((B, 128, 2304), dtype=np.float32)
+            nn = np.clip(n - c0, 0, 128).astype(np.int32)
+            for ctx in (fused, twin):
+                ctx.ring_write_rows(0, fill, (start + c0).astype(np.int32), nn)
+            ring.write(fill, (start + c0).astype(np.int32), nn)
+        for step in range(4):
+            qkv = rng.standard_normal((B, 2304), dtype=np.float32)
+            q_f, out_f = fused.append_attend(0, qkv, pos)
+            q_t = twin.ring_append(0, qkv, pos)
+            out_t = twin.decode_attention(0, q_t, pos)
+            assert np.array_equal(q_f, q_t), step
+            assert np.array_equal(out_f, out_t), step
+            q_or = ring.append(qkv, pos)
+            err = np.abs(out_f - ring.attend(q_or, pos)).max()
+            assert err < 1e-4, (step, err)
+            pos = pos + 1
+        _check_ring(fused, ring, 0, range(B))
+
+
 def test_append_attend_range_error_on_a_non_wrapping_ring():
     say("fused append+attention range error")
     import torch
