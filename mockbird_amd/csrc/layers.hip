@@ -84,16 +84,32 @@ __global__ __launch_bounds__(256) void k_embed_rows(const int32_t* __restrict__ 
   const int row = blockIdx.x;
   if (row >= M) return;
   const int32_t* id = ids + (int64_t)row * ROW;
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float acc = 0.f;
-    const int t = id[0];
-    if (t >= 0 && t < vocab) acc = wte[(int64_t)t * D + d];
-    for (int k = 0; k < NVQ; k++) {
-      const int a = id[1 + k];
-      if (a == PAD || a < 0 || a >= CODES) continue;
-      acc = acc + audio.t[k][(int64_t)a * D + d];
-    }
-    x[(int64_t)row * D + d] = acc;
+  // Every table read is issued before the first add (ids clamped into their
+  // tables, the skipped ones then left out of the sum), so a row costs one
+  // memory round trip, not one per channel; the sum keeps channel order.
+  static_assert(D % 256 == 0, "whole rows per block");
+  constexpr int DI = D / 256;
+  const int t = id[0];
+  const bool tv = t >= 0 && t < vocab;
+  const int tc = tv ? t : 0;
+  float tw[DI], av[NVQ][DI];
+#pragma unroll
+  for (int i = 0; i < DI; i++) tw[i] = wte[(int64_t)tc * D + threadIdx.x + 256 * i];
+  bool ok[NVQ];
+#pragma unroll
+  for (int k = 0; k < NVQ; k++) {
+    const int a = id[1 + k];
+    ok[k] = a != PAD && a >= 0 && a < CODES;
+    const int ac = ok[k] ? a : 0;
+#pragma unroll
+    for (int i = 0; i < DI; i++) av[k][i] = audio.t[k][(int64_t)ac * D + threadIdx.x + 256 * i];
+  }
+#pragma unroll
+  for (int i = 0; i < DI; i++) {
+    float acc = tv ? tw[i] : 0.f;
+#pragma unroll
+    for (int k = 0; k < NVQ; k++) acc = ok[k] ? acc + av[k][i] : acc;
+    x[(int64_t)row * D + threadIdx.x + 256 * i] = acc;
   }
 }
 
