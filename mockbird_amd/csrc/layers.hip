@@ -182,12 +182,25 @@ __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
+  // every read issued before the first product (one round trip): the
+  // alive flag, the row of h and the two head columns (strided, one line each)
+  const bool was_alive = !alive || alive[b];
+  constexpr int DI = D / 64;
+  float hv[DI], he[DI], ha[DI];
+#pragma unroll
+  for (int i = 0; i < DI; i++) {
+    const int d = lane + 64 * i;
+    hv[i] = h[(int64_t)b * D + d];
+    he[i] = head[(int64_t)d * vocab + end_id];
+    ha[i] = head[(int64_t)d * vocab + assistant_id];
+  }
   if (x) copy_row(wte, assistant_id, x, b, lane);
   double e = 0.0, a = 0.0;
-  for (int d = lane; d < D; d += 64) {
-    const double x = h[(int64_t)b * D + d];
-    e += x * (double)head[(int64_t)d * vocab + end_id];
-    a += x * (double)head[(int64_t)d * vocab + assistant_id];
+#pragma unroll
+  for (int i = 0; i < DI; i++) {
+    const double xv = hv[i];
+    e += xv * (double)he[i];
+    a += xv * (double)ha[i];
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -195,7 +208,7 @@ __global__ __launch_bounds__(256) void k_text_decide(const float* __restrict__ h
     a += __shfl_xor(a, off);
   }
   if (lane == 0) {
-    cont[b] = a >= e && (!alive || alive[b]) ? 1 : 0;
+    cont[b] = a >= e && was_alive ? 1 : 0;
     if (te) {
       te[2 * b] = e;
       te[2 * b + 1] = a;
