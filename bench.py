@@ -732,6 +732,8 @@ def main():
                          "(prefill attention), codec (codec decoder frames/s at 64 and 256 "
                          "voices), frames (model decode frames/s); the JSON line needs c1")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
+    ap.add_argument("--frames-weights", default="f32,bf16",
+                    help="weight storage of the frames leg's runs (f32, bf16 or both)")
     ap.add_argument("--frames-n", type=int, default=0,
                     help="frames per voice count (default: 60 at B=1, 300 otherwise)")
     args = ap.parse_args()
@@ -765,10 +767,14 @@ def main():
     frames_w16 = None
     if "frames" in legs:
         plan = {1: (60, "f32"), 64: (300, "bf16"), 256: (300, "bf16")}
-        frames = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1])
-                  for b in map(int, args.frames_b.split(","))]
-        frames_w16 = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1], weights_name="bf16")
+        fw = args.frames_weights.split(",")
+        if "f32" in fw:
+            frames = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1])
                       for b in map(int, args.frames_b.split(","))]
+        if "bf16" in fw:
+            frames_w16 = [run_frames(w, b, args.frames_n or plan[b][0], plan[b][1],
+                                     weights_name="bf16")
+                          for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "hbm_read_ceiling": ceiling, "gemm": gemm,
                           "kv_attention_256_voices": voices,

@@ -271,9 +271,11 @@ int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float*
                 float* out, const Rows& out_rows);
 // Ring append fused into the decode attention: one row per sequence, qkv
 // [B] fused rows at pos[b]; q_out (roped q) may be null.
+// pos_const >= 0: every row sits at that position (pos is then not read
+// where the kernel can skip it: the short-window fp32 ring of the local head).
 int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv, int qkv_dtype,
                        const Rows& qkv_rows, const int32_t* pos, int64_t max_valid, float* q_out,
-                       const Rows& qo_rows, float* out, const Rows& out_rows);
+                       const Rows& qo_rows, float* out, const Rows& out_rows, int pos_const = -1);
 int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
                              const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
                              const int32_t* n_rows, float* out, const Rows& out_rows);

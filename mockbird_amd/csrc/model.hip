@@ -223,7 +223,7 @@ int cancelled(mb_ctx* ctx) {
 // set, else one row per sequence).
 int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int rows_max, int64_t M,
               const int32_t* pos0, const int32_t* n_rows, const int32_t* row_off, bool prefill,
-              int64_t max_valid, Act& a) {
+              int64_t max_valid, Act& a, int pos_const = -1) {
   int rc;
   // decode-sized M: each LayerNorm is folded into the projection after it;
   // up to kGemvMaxM rows the projections read the k-major copies
@@ -267,7 +267,7 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   } else {
     // one launch appends this row's K/V and attends the ring including it
     rc = launch_append_attn(ctx, ring, B, a.qkv, MB_DT_F32, qkv_rows, pos0, max_valid, nullptr,
-                            Rows{}, a.att, q_rows);
+                            Rows{}, a.att, q_rows, pos_const);
   }
   if (rc) return rc;
   // decode sizes read the column-block-major copies of O and fc_out
@@ -413,8 +413,9 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
                                                m.audio_emb, probe ? probe->forced : ctx->tokens,
                                                a.x)))
       return rc;
+    // (every voice's local step sits at position `step`)
     if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
-                        nullptr, false, step + 1, a)))
+                        nullptr, false, step + 1, a, step)))
       return rc;
     // the audio heads take ln_f folded in (decode-sized B); the text decision
     // and the step probe read ln_f itself

@@ -579,7 +579,8 @@ __global__ __launch_bounds__(256) void k_attn_short(
     const void* __restrict__ qkv, Rows q_rows, const int32_t* __restrict__ pos0, int nunits,
     float* __restrict__ ring_k, float* __restrict__ ring_v, int32_t* __restrict__ slot_pos,
     int64_t ring_seq_stride, int C, const float2* __restrict__ rope_tab,
-    float* __restrict__ q_out, Rows qo_rows, float* __restrict__ out, Rows out_rows) {
+    float* __restrict__ q_out, Rows qo_rows, float* __restrict__ out, Rows out_rows,
+    int pos_const) {
   constexpr int VD = 4, LR = 16, G = 4, U = kShortWindow / G, GU = G * U;
   constexpr int ROWB = HD * 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -587,7 +588,9 @@ __global__ __launch_bounds__(256) void k_attn_short(
   if (unit >= nunits) return;  // per wave: no barrier below
   const int b = unit / H, head = unit % H;
   const int g = lane / LR, sub = lane % LR;
-  const int64_t cur = pos0[b];
+  // pos_const >= 0: every query sits at that position (the local head's
+  // step), known without a load, so the window's loads issue at once
+  const int64_t cur = pos_const >= 0 ? (int64_t)pos_const : (int64_t)pos0[b];
   const int nvalid = cur < 0 ? 0 : (int)(cur + 1 < C ? cur + 1 : C);
   const int64_t kv_off = (int64_t)b * ring_seq_stride + (int64_t)head * C * HD + sub * VD;
   const char* kbase = (const char*)(ring_k + kv_off);
@@ -728,7 +731,7 @@ template <bool APPEND, bool IN_BF16>
 static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const void* q,
                        const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
                        int64_t max_valid, float* q_out, const Rows& qo_rows, float* out,
-                       const Rows& out_rows) {
+                       const Rows& out_rows, int pos_const = -1) {
   if (ring.heads != H || ring.window != ring.C)
     return fail(ctx, MB_ERR_ARG, "single-query decode attention runs on the model's 12-head rings");
   const int C = ring.C;
@@ -741,7 +744,8 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
     const int nunits = (int)(nq * H);
     hipLaunchKernelGGL(k_attn_short<IN_BF16>, dim3((unsigned)((nunits + 3) / 4)), dim3(256), 0,
                        ctx->stream, q, q_rows, pos0, nunits, (float*)ring.k, (float*)ring.v,
-                       ring.sp, ring.seq_stride, C, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+                       ring.sp, ring.seq_stride, C, ctx->rope_tab, q_out, qo_rows, out, out_rows,
+                       pos_const);
     MB_HIP(ctx, hipGetLastError());
     return MB_OK;
   }
@@ -790,12 +794,12 @@ int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float*
 
 int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv, int qkv_dtype,
                        const Rows& qkv_rows, const int32_t* pos, int64_t max_valid, float* q_out,
-                       const Rows& qo_rows, float* out, const Rows& out_rows) {
+                       const Rows& qo_rows, float* out, const Rows& out_rows, int pos_const) {
   if (qkv_dtype == MB_DT_BF16)
     return launch_unit<true, true>(ctx, ring, B, 1, qkv, qkv_rows, pos, nullptr, max_valid, q_out,
-                                   qo_rows, out, out_rows);
+                                   qo_rows, out, out_rows, pos_const);
   return launch_unit<true, false>(ctx, ring, B, 1, qkv, qkv_rows, pos, nullptr, max_valid, q_out,
-                                  qo_rows, out, out_rows);
+                                  qo_rows, out, out_rows, pos_const);
 }
 
 }  // namespace mb
