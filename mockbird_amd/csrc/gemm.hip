@@ -295,7 +295,38 @@ __device__ __forceinline__ float4 load_coherent(const float* p) {
 // move with device-coherent accesses: agent-scope relaxed atomic stores and
 // loads (global_store / global_load with sc1), the stores waited for
 // (vmcnt(0)) before the counter's atomic add.
+// The epilogue operands of a lane's stores, loaded before the k loop so the
+// tile's end waits on no memory round trip of its own: the bias (or scale),
+// the folded LayerNorm's c and d at columns n .. n+3, and for the residual
+// epilogues the old output values of the rows 16i + 4r + wave it stores.
+template <int MI>
+struct EpiRegs {
+  float4 b, cv, dv, c[MI];
+};
+
 template <int MI, int EPI, bool LNF>
+__device__ __forceinline__ void epi_prefetch(EpiRegs<MI>& pre, const float* __restrict__ bias,
+                                             const float* __restrict__ Cm, int64_t ldc, int M,
+                                             const float* __restrict__ lnc,
+                                             const float* __restrict__ lnd) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + 4 * (lane & 15), r = lane >> 4;
+  const int m0 = blockIdx.y * (16 * MI);
+  // no bias: any in-bounds address, the value is never used
+  pre.b = *(const float4*)(bias ? bias + n : Cm);
+  pre.cv = pre.dv = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (LNF) {
+    pre.cv = *(const float4*)(lnc + n);
+    pre.dv = *(const float4*)(lnd + n);
+  }
+  if (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) {
+#pragma unroll
+    for (int i = 0; i < MI; i++)
+      pre.c[i] = *(const float4*)(Cm + (int64_t)min(m0 + 16 * i + 4 * r + wave, M - 1) * ldc + n);
+  }
+}
+
+template <int MI, int EPI, bool LNF, bool PRE = false>
 __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)[MI],
                                               float (&sxx)[MI], const float (&x0)[MI], int K,
                                               const float* __restrict__ bias,
@@ -303,7 +334,8 @@ __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)
                                               int N, float* __restrict__ part,
                                               const float* __restrict__ lnc,
                                               const float* __restrict__ lnd,
-                                              int32_t* __restrict__ cnt = nullptr) {
+                                              int32_t* __restrict__ cnt = nullptr,
+                                              const EpiRegs<MI>* pre = nullptr) {
   __shared__ float red[4][2][4][4][64];  // [wave][block][column block][element][lane]
   __shared__ float4 stat[LNF ? 4 : 1][MI][16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -330,7 +362,10 @@ __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)
   // n .. n+3 -- summing the waves in wave order (the same order on every run).
   const float inv_k = 1.f / (float)K;
   float4 cv = make_float4(0.f, 0.f, 0.f, 0.f), dv = cv;
-  if (LNF) {
+  if (PRE) {
+    cv = pre->cv;
+    dv = pre->dv;
+  } else if (LNF) {
     cv = *(const float4*)(lnc + n);
     dv = *(const float4*)(lnd + n);
   }
@@ -386,7 +421,11 @@ __device__ __forceinline__ void stream_finish(f32x4_t (&acc)[MI][4], float (&sx)
         continue;
       }
       float* cp = Cm + (int64_t)row * ldc + n;
-      *(float4*)cp = epilogue4<EPI>(make_float4(o[0], o[1], o[2], o[3]), bias, n, cp);
+      const float4 ov = make_float4(o[0], o[1], o[2], o[3]);
+      if (PRE)
+        *(float4*)cp = epilogue_regs<EPI>(ov, pre->b, bias != nullptr, pre->c[i]);
+      else
+        *(float4*)cp = epilogue4<EPI>(ov, bias, n, cp);
     }
   }
   if (S == 1 || !cnt) return;
@@ -574,6 +613,8 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
   const int S = gridDim.z, split = blockIdx.z;
   const int K = 4 * S * kw;
 
+  EpiRegs<MI> pre;
+  epi_prefetch<MI, EPI, LNF>(pre, bias, Cm, ldc, M, lnc, lnd);
   f32x4_t acc[MI][4];
 #pragma unroll
   for (int i = 0; i < MI; i++)
@@ -701,7 +742,8 @@ __global__ __launch_bounds__(256) void k_gemm_x3(
     });
   }
 
-  stream_finish<MI, EPI, LNF>(acc, sx, sxx, x0, K, bias, Cm, ldc, M, N, part, lnc, lnd, cnt);
+  stream_finish<MI, EPI, LNF, true>(acc, sx, sxx, x0, K, bias, Cm, ldc, M, N, part, lnc, lnd, cnt,
+                                    &pre);
 }
 
 // C = epi(sum over splits of part, in split order, + bias); one float4 per thread.
