@@ -245,6 +245,25 @@ int mb_linear_noalloc_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int6
  * frame graph of mb_decode_frames_dev. */
 int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, double penalty);
 
+/* Arithmetic of the repetition penalty in the greedy choice.  The reference
+ * has two: its CPU path (the frame loop of mossTtsRuntime.js:1965-2141 over
+ * local_cached_step, the app's greedy path since the published model ships
+ * no local_greedy_frame graph) penalises and compares JS numbers, doubles
+ * (argmaxWithRepetitionPenalty, mossTtsRuntime.js:506-521; policy.ts:273-290);
+ * its WGSL engine passes the penalty as float bits (decode.ts:908) and
+ * multiplies or divides and compares in f32 (ARGMAX_PENALTY,
+ * kernels-decode.ts:454-461).  A penalised score can fall between s / 1.2
+ * and s / 1.2f, so the two can pick different codes.
+ *   MB_PENALTY_F64 (the default): the CPU path's doubles.
+ *   MB_PENALTY_F32: the WGSL engine's f32 arithmetic (the penalty rounded to
+ *   f32, a correctly rounded f32 multiply or divide; WGSL only bounds its f32
+ *   division to 2.5 ulp, so bit parity with a given WebGPU driver is not
+ *   claimed).
+ * A change invalidates the captured frame graph of mb_decode_frames_dev. */
+#define MB_PENALTY_F64 0
+#define MB_PENALTY_F32 1
+int mb_set_penalty_precision(mb_ctx* ctx, int32_t precision);
+
 /* Weight storage of the decoder's projections (c_attn, c_proj, fc_in, fc_out
  * of every layer, the local layer's, and the 16 audio heads): MB_W_F32 (the
  * default, the reference's fp32 weights) or MB_W_BF16.  With MB_W_BF16 each
@@ -255,9 +274,9 @@ int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, d
  * head stay fp32.  The bf16 re-export of the model weights that
  * docs/moss-tts-runtime-analysis.md:408-411 plans (the reference's own
  * "f16 re-export", a separate, independent win) is what this stands for;
- * the uploaded tensors are left as they are, and a later call switches back.
- * Re-derives the weight copies on the next model call and invalidates the
- * captured frame graph. */
+ * the uploaded tensors are left as they are, and a later call switches back
+ * (the rounded copies are then freed).  Re-derives the weight copies on the
+ * next model call and invalidates the captured frame graph. */
 #define MB_W_F32 0
 #define MB_W_BF16 1
 int mb_set_weight_storage(mb_ctx* ctx, int32_t storage);

@@ -20,6 +20,7 @@ MB_OK, MB_ERR_ARG, MB_ERR_RANGE, MB_ERR_HIP, MB_ERR_STATE, MB_ERR_CANCELLED, MB_
 MB_KV_F32, MB_KV_BF16 = 0, 1
 MB_DT_F32, MB_DT_BF16 = 0, 1
 MB_W_F32, MB_W_BF16 = 0, 1
+MB_PENALTY_F64, MB_PENALTY_F32 = 0, 1
 MB_EPI_STORE, MB_EPI_GELU, MB_EPI_ADD, MB_EPI_SCALE_ADD, MB_EPI_GELU_ERF = 0, 1, 2, 3, 4
 #: the codec decoder's shape (codec.ts:1-30)
 CODEC_LAYERS, CODEC_CONTEXT, CODEC_SAMPLES = (4, 2, 2, 4), (500, 1696, 2480, 3248), 3840
@@ -32,7 +33,7 @@ EXPORTS = (
     "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_ring_append", "mb_ring_write_rows",
     "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
-    "mb_set_local_head", "mb_set_weight_storage", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
+    "mb_set_local_head", "mb_set_penalty_precision", "mb_set_weight_storage", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
     "mb_local_steps", "mb_local_logits", "mb_clear_seen", "mb_decode_step_dev", "mb_local_frame_dev",
     "mb_linear_dev", "mb_split_weights_dev", "mb_linear_split_dev", "mb_linear_noalloc_dev", "mb_decode_frames_dev", "mb_decode_frames", "mb_append_attend",
     "mb_append_attend_dev", "mb_codec_init", "mb_codec_reset", "mb_codec_decode",
@@ -109,6 +110,7 @@ def load():
                                      C.c_int),
         "mb_set_local_head": ([_vp, _i32, _i32, C.c_double], C.c_int),
         "mb_set_weight_storage": ([_vp, _i32], C.c_int),
+        "mb_set_penalty_precision": ([_vp, _i32], C.c_int),
         "mb_prefill": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_prefill_rows": ([_vp, C.c_int, C.c_int, _vp, _vp, C.c_int, _vp], C.c_int),
         "mb_local_steps": ([_vp, C.c_int, _vp, C.c_int, _vp], C.c_int),
@@ -376,6 +378,11 @@ class Context:
     # -- model
     def set_local_head(self, audio_end_id: int = 7, assistant_id: int = 9, penalty: float = 1.2):
         self.check(self.lib.mb_set_local_head(self.h, audio_end_id, assistant_id, penalty))
+
+    def set_penalty_precision(self, precision: int = MB_PENALTY_F64):
+        """MB_PENALTY_F64 (default: the reference CPU path's JS doubles) or
+        MB_PENALTY_F32 (the WGSL engine's f32 penalty arithmetic)."""
+        self.check(self.lib.mb_set_penalty_precision(self.h, precision))
 
     def set_weight_storage(self, storage: int = MB_W_F32):
         """MB_W_F32 (default) or MB_W_BF16: the decoder's projection weights

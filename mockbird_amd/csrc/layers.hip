@@ -227,10 +227,15 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
 
 // Greedy argmax over 1024 logits with the HuggingFace repetition penalty on
 // this channel's seen set: a seen id's score is multiplied by the penalty
-// when negative and divided when not; penalty and score are doubles, as the
-// JS numbers of the reference are (audio_repetition_penalty is the double
-// 1.2, mossTtsRuntime.js:506-521) (argmaxWithRepetitionPenalty, policy.ts:273-290; ARGMAX_PENALTY,
-// kernels-decode.ts:428-478).  Strict '>' keeps the lowest id on ties and a
+// when negative and divided when not (argmaxWithRepetitionPenalty,
+// policy.ts:273-290; ARGMAX_PENALTY, kernels-decode.ts:428-478).  Penalty
+// and score are doubles, as the JS numbers of the reference's CPU path are
+// (audio_repetition_penalty is the double 1.2, mossTtsRuntime.js:506-521);
+// with `f32` (wave-uniform) they are f32, as in the WGSL engine: the penalty
+// rounded to f32 and a correctly rounded f32 multiply or divide (taken in
+// double and rounded once to f32, which for a product or quotient of two
+// floats is the correctly rounded f32 result, since 53 >= 2 * 24 + 2), whose
+// result the double compare then orders exactly as an f32 compare would.  Strict '>' keeps the lowest id on ties and a
 // NaN never wins.  The winner goes to tokens[b][ch]; the seen bit is set only
 // for sequences that continue (the reference stops before drawing codes).
 // One wave per sequence.  Lane l takes ids 16l .. 16l+15: four 16-byte logit
@@ -241,7 +246,7 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
 // `x`, the wave also writes the next step's input row, next_emb[winner]
 // (EMBED_ROW_LOCAL mode 2: the next step embeds this channel's code).
 __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
-                                                        int ch, double penalty,
+                                                        int ch, double penalty, int f32,
                                                         uint32_t* __restrict__ seen,
                                                         const int32_t* __restrict__ cont,
                                                         int32_t* __restrict__ tokens,
@@ -267,10 +272,16 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
   const bool apply = any && penalty != 1.0;
   double best = -INFINITY;
   int idx = 0x7fffffff;
+  const float pf = (float)penalty;
 #pragma unroll
   for (int j = 0; j < 16; j++) {
     double s = v[j];
-    if (apply && ((bits >> j) & 1u)) s = s < 0 ? s * penalty : s / penalty;
+    if (apply && ((bits >> j) & 1u)) {
+      if (f32)  // f32 result: the double product / quotient of two floats rounded once
+        s = (double)(float)(v[j] < 0.f ? (double)v[j] * (double)pf : (double)v[j] / (double)pf);
+      else
+        s = s < 0 ? s * penalty : s / penalty;
+    }
     if (s > best) {
       best = s;
       idx = 16 * lane + j;
@@ -298,10 +309,10 @@ __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict_
 }
 
 int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
-                          uint32_t* seen, const int32_t* cont, int32_t* tokens,
+                          bool penalty_f32, uint32_t* seen, const int32_t* cont, int32_t* tokens,
                           const float* next_emb, float* x) {
   hipLaunchKernelGGL(k_argmax_penalty, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream,
-                     logits, B, ch, penalty, seen, cont, tokens, next_emb, x);
+                     logits, B, ch, penalty, (int)penalty_f32, seen, cont, tokens, next_emb, x);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

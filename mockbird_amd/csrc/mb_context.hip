@@ -47,6 +47,18 @@ float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel) {
   return t.ptr;
 }
 
+void drop_internal(mb_ctx* ctx, const std::string& name) {
+  auto it = ctx->weights.find(name);
+  if (it == ctx->weights.end()) return;
+  if (it->second.ptr) {
+    (void)hipStreamSynchronize(ctx->stream);  // no launch in flight still reads it
+    (void)hipFree(it->second.ptr);
+    ctx->device_bytes -= it->second.numel * 4;
+    ctx->graph_gen++;
+  }
+  ctx->weights.erase(it);
+}
+
 
 int fail(mb_ctx* ctx, int code, const char* fmt, ...) {
   if (ctx) {

@@ -140,6 +140,7 @@ struct mb_ctx {
   int32_t end_id = 7;          // audio_end_token_id
   int32_t assistant_id = 9;    // audio_assistant_slot_token_id
   double penalty = 1.2;        // audio_repetition_penalty (a JS number in the reference)
+  bool penalty_f32 = false;    // MB_PENALTY_F32: the penalty applied in f32
 
   // Local head state: a 17-slot fp32 cache per sequence, the per-channel
   // repetition history, the last frame's codes and continue flags.
@@ -212,6 +213,8 @@ const DeviceTensor* find(mb_ctx* ctx, const std::string& name, std::initializer_
 // A device tensor owned by the context under an internal ('#') name, freed
 // with the uploaded weights; reallocated only when its size changes.
 float* internal_tensor(mb_ctx* ctx, const std::string& name, int64_t numel);
+// Frees the internal tensor `name` (after the context's stream drains), if any.
+void drop_internal(mb_ctx* ctx, const std::string& name);
 
 inline size_t kv_elem_bytes(const mb_ctx* ctx) { return ctx->cfg.kv_dtype == MB_KV_BF16 ? 2 : 4; }
 
@@ -378,7 +381,7 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
                        int assistant_id, const int32_t* alive, int32_t* cont,
                        const float* wte = nullptr, float* x = nullptr, double* te = nullptr);
 int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
-                          uint32_t* seen, const int32_t* cont, int32_t* tokens,
+                          bool penalty_f32, uint32_t* seen, const int32_t* cont, int32_t* tokens,
                           const float* next_emb = nullptr, float* x = nullptr);
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);
 int launch_frame_emit(mb_ctx* ctx, const int32_t* tokens, const int32_t* cont, int B,

@@ -85,9 +85,13 @@ int split(mb_ctx* ctx, const std::string& name, const float* Wt, const float* W,
 }
 
 // With bf16 weight storage: W <- bf16(W) in a copy of its own (the uploaded
-// tensor is left as it is), from which every other copy derives.
+// tensor is left as it is), from which every other copy derives.  With fp32
+// storage the copy a bf16 period left behind is freed.
 int round_w(mb_ctx* ctx, const std::string& name, const float*& W, int64_t n) {
-  if (!ctx->w_bf16) return MB_OK;
+  if (!ctx->w_bf16) {
+    drop_internal(ctx, name);
+    return MB_OK;
+  }
   float* p = internal_tensor(ctx, name, n);
   if (!p) return fail(ctx, MB_ERR_NOMEM, "rounded weight allocation failed (%s)", name.c_str());
   const int rc = launch_round_bf16(ctx, W, n, p);
@@ -448,7 +452,8 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
                          B);
       if (rc) return rc;
       if (pick)
-        rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->seen, ctx->cont,
+        rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->penalty_f32, ctx->seen,
+                                   ctx->cont,
                                    ctx->tokens, embed_next ? m.audio_emb.t[ch] : nullptr,
                                    embed_next ? a.x : nullptr);
     }
@@ -498,6 +503,16 @@ int mb_set_local_head(mb_ctx* ctx, int32_t audio_end_id, int32_t assistant_id, d
   ctx->end_id = audio_end_id;
   ctx->assistant_id = assistant_id;
   ctx->penalty = penalty;
+  return MB_OK;
+}
+
+int mb_set_penalty_precision(mb_ctx* ctx, int32_t precision) {
+  if (!ctx) return MB_ERR_ARG;
+  if (precision != MB_PENALTY_F64 && precision != MB_PENALTY_F32)
+    return fail(ctx, MB_ERR_ARG, "penalty precision must be MB_PENALTY_F64 or MB_PENALTY_F32");
+  const bool f32 = precision == MB_PENALTY_F32;
+  if (f32 != ctx->penalty_f32) ctx->graph_gen++;  // a kernel argument of the frame graph
+  ctx->penalty_f32 = f32;
   return MB_OK;
 }
 

@@ -477,23 +477,47 @@ napi_value SetLocalHead(napi_env env, napi_callback_info info) {
   return undef(env);
 }
 
+// A two-way string option: sets *second to whether `v` names the second
+// choice; throws (and returns false) unless it names one of the two.
+bool get_choice(napi_env env, napi_value v, const char* first, const char* second, bool* is_second,
+                const char* what) {
+  char buf[8] = {0};
+  size_t len = 0;
+  const std::string msg = std::string(what) + " must be \"" + first + "\" or \"" + second + "\"";
+  if (napi_get_value_string_utf8(env, v, buf, sizeof buf, &len) != napi_ok) {
+    napi_throw_type_error(env, nullptr, msg.c_str());
+    return false;
+  }
+  const std::string s(buf, len);
+  if (s != first && s != second) {
+    napi_throw_range_error(env, nullptr, msg.c_str());
+    return false;
+  }
+  *is_second = s == second;
+  return true;
+}
+
 // setWeightStorage(h, "f32" | "bf16")
 napi_value SetWeightStorage(napi_env env, napi_callback_info info) {
   Args a(env, info);
   mb_ctx* ctx = get_ctx(env, a.at(0));
   if (!ctx) return nullptr;
-  char buf[8] = {0};
-  size_t len = 0;
-  if (napi_get_value_string_utf8(env, a.at(1), buf, sizeof buf, &len) != napi_ok) {
-    napi_throw_type_error(env, nullptr, "weight storage must be \"f32\" or \"bf16\"");
-    return nullptr;
-  }
-  const std::string v(buf, len);
-  if (v != "f32" && v != "bf16") {
-    napi_throw_range_error(env, nullptr, "weight storage must be \"f32\" or \"bf16\"");
-    return nullptr;
-  }
-  int rc = mb_set_weight_storage(ctx, v == "bf16" ? MB_W_BF16 : MB_W_F32);
+  bool bf16;
+  if (!get_choice(env, a.at(1), "f32", "bf16", &bf16, "weight storage")) return nullptr;
+  int rc = mb_set_weight_storage(ctx, bf16 ? MB_W_BF16 : MB_W_F32);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
+// setPenaltyPrecision(h, "f64" | "f32"): the CPU path's doubles or the WGSL
+// engine's f32 repetition-penalty arithmetic
+napi_value SetPenaltyPrecision(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  bool f32;
+  if (!get_choice(env, a.at(1), "f64", "f32", &f32, "penalty precision")) return nullptr;
+  int rc = mb_set_penalty_precision(ctx, f32 ? MB_PENALTY_F32 : MB_PENALTY_F64);
   if (rc) return throw_status(env, ctx, rc);
   return undef(env);
 }
@@ -850,6 +874,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"cancel", Cancel},
       {"setLocalHead", SetLocalHead},
       {"setWeightStorage", SetWeightStorage},
+      {"setPenaltyPrecision", SetPenaltyPrecision},
       {"ringReset", SeqListCall<mb_ring_reset>},
       {"clearSeen", SeqListCall<mb_clear_seen>},
       {"ringPoison", RingPoison},

@@ -34,6 +34,20 @@ export function frameRowFrom(assistantSlot, frame) {
   return row;
 }
 
+/**
+ * The largest decode-vs-prefill gap warm-up accepts.  With fp32 K/V both
+ * paths multiply in fp32 (1e-3).  With bf16 K/V the prefill path's causal
+ * attention rounds q and the softmax weights to bf16 for its matrix products
+ * while the decode step keeps them in fp32, so the two agree to the bf16
+ * bar (2e-2).  Either bar is taken relative to the hidden state's largest
+ * magnitude once that exceeds 1, as real weights give hidden states of tens.
+ */
+function warmupTolerance(kvBf16, hidden) {
+  let scale = 1;
+  for (let i = 0; i < hidden.length; i += 1) scale = Math.max(scale, Math.abs(hidden[i]));
+  return (kvBf16 ? 2e-2 : 1e-3) * scale;
+}
+
 /** max |a - b| over two equally long arrays */
 function maxAbsDiff(a, b) {
   let m = 0;
@@ -57,6 +71,7 @@ class HipTtsEngineImpl {
     this.decoder = new DecodeRunner(native, handle, maxSlots, settings);
     this.utterance = null;
     this.hasCodec = false;
+    this.kvBf16 = false;
     this.disposed = false;
   }
 
@@ -134,7 +149,7 @@ class HipTtsEngineImpl {
     await this.prefill({ inputIds: prompt.slice(0, 1), attentionMask: [[1]] });
     const stepped = await this.decodeStep({ row, position: 1 });
     const gap = maxAbsDiff(stepped, both);
-    if (!(gap < 1e-3)) {
+    if (!(gap < warmupTolerance(this.kvBf16, both))) {
       throw new Error(`warmup: the decode step disagrees with the prefill of the same rows (max |diff| ${gap})`);
     }
     this.reset();
@@ -170,12 +185,17 @@ class HipTtsEngineImpl {
     throw new EngineNotImplemented("clone encoder (codec encode convs)");
   }
 
+  /**
+   * Frees the context.  While an *Async call is in flight destroy throws
+   * MB_ERR_BUSY and the engine stays usable: await the call, then dispose
+   * again.
+   */
   dispose() {
     if (this.disposed) return;
+    this.native.destroy(this.handle);
     this.disposed = true;
     this.utterance = null;
     this.prefillRunner.dispose();
-    this.native.destroy(this.handle);
   }
 }
 
@@ -185,7 +205,9 @@ class HipTtsEngineImpl {
  * WeightTables; options: {localHead, maxSlots (570), maxRows (= maxSlots),
  * layers (12: the count the model must resolve to), kvDtype ("f32" | "bf16"),
  * weightDtype ("f32" | "bf16": projection weights rounded to and read as
- * bf16, mb_set_weight_storage),
+ * bf16, mb_set_weight_storage), penaltyPrecision ("f64": the reference CPU
+ * path's doubles, the default | "f32": its WGSL engine's arithmetic,
+ * mb_set_penalty_precision),
  * wrap (false: the reference's non-wrapping ring), device (0), codecShape
  * ({layersPerStage, contextPerStage}, the real shape by default),
  * codecKvDtype ("f32")}.  With a codec table the codec decoder is set up
@@ -212,6 +234,7 @@ export async function createGpuEngineFor(tables, log, options) {
   });
   try {
     if (options.weightDtype) native.setWeightStorage(handle, options.weightDtype);
+    if (options.penaltyPrecision) native.setPenaltyPrecision(handle, options.penaltyPrecision);
     let bytes = 0;
     for (const t of tensors) {
       native.uploadTensor(handle, t.name, t.data, t.dims);
@@ -235,6 +258,7 @@ export async function createGpuEngineFor(tables, log, options) {
     const engine = new HipTtsEngineImpl(native, handle, info, options.localHead, maxSlots, maxRows,
       layers);
     engine.hasCodec = codecShape !== null;
+    engine.kvBf16 = options.kvDtype === "bf16";
     log(`engine ready: ${layers} layers, KV ring ${maxSlots} slots, vocab ${vocab}`);
     const warm = await engine.warmup();
     log(`warmup: 1 prefill over ${warm.rows} rows in ${warm.prefillMs} ms`);

@@ -22,6 +22,8 @@ export type MultiVoiceOptions = {
   kvDtype?: "f32" | "bf16";
   /** projection weights rounded to and read as bf16 (mb_set_weight_storage) */
   weightDtype?: "f32" | "bf16";
+  /** Repetition-penalty arithmetic: "f64" (default, the reference CPU path) or "f32" (its WGSL engine). */
+  penaltyPrecision?: "f64" | "f32";
   wrap?: boolean;
   device?: number;
   codecShape?: CodecShape;

@@ -121,16 +121,18 @@ export class MultiVoiceEngine {
     if (this.hasCodec) this.native.codecReset(this.handle, ids);
   }
 
+  /** Frees the context; throws MB_ERR_BUSY (and stays usable) while an *Async call is in flight. */
   dispose() {
     if (this.disposed) return;
-    this.disposed = true;
     this.native.destroy(this.handle);
+    this.disposed = true;
   }
 }
 
 /**
  * A context for `maxVoices` voices: options {localHead, maxVoices, capacity
- * (1024), maxRows (capacity), kvDtype ("bf16"), weightDtype ("f32" | "bf16"), wrap (true), device (0),
+ * (1024), maxRows (capacity), kvDtype ("bf16"), weightDtype ("f32" | "bf16"),
+ * penaltyPrecision ("f64" | "f32"), wrap (true), device (0),
  * codecShape, codecKvDtype ("bf16")}; a `codec` table sets up the codec for
  * every voice (decodeAudio).
  */
@@ -153,6 +155,7 @@ export async function createMultiVoiceEngine(tables, log, options) {
     for (const t of tensors) native.uploadTensor(handle, t.name, t.data, t.dims);
     const s = options.localHead;
     if (options.weightDtype) native.setWeightStorage(handle, options.weightDtype);
+    if (options.penaltyPrecision) native.setPenaltyPrecision(handle, options.penaltyPrecision);
     native.setLocalHead(handle, s.audioEndTokenId, s.audioAssistantSlotTokenId, s.repetitionPenalty);
     let hasCodec = false;
     if (tables.codec) {

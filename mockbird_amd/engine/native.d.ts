@@ -28,6 +28,8 @@ export interface Native {
   cancel(h: NativeHandle, on?: boolean): void;
   setLocalHead(h: NativeHandle, audioEnd: number, assistant: number, penalty: number): void;
   setWeightStorage(h: NativeHandle, storage: "f32" | "bf16"): void;
+  /** The repetition penalty's arithmetic: "f64" (the reference CPU path) or "f32" (its WGSL engine). */
+  setPenaltyPrecision(h: NativeHandle, precision: "f64" | "f32"): void;
   ringReset(h: NativeHandle, seqIds: Int32Array | null): void;
   clearSeen(h: NativeHandle, seqIds: Int32Array | null): void;
   ringPoison(h: NativeHandle, layer: number, seq: number, nSlots: number, sentinel: number): void;

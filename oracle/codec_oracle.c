@@ -124,34 +124,61 @@ void or_codec_rvq(const or_codec* W, const int32_t* codes, float* stage0) {
   }
 }
 
-/* One query at `cur` against one layer's ring of `C` slots, 4 heads. */
+/* One query at `cur` against one layer's ring of `C` slots, 4 heads.
+ * `live` is scratch for C slot indices. */
 static void attend(const float* q, int64_t cur, int C, const float* K, const float* V,
-                   const int32_t* sp, float* out, double* scores) {
+                   const int32_t* sp, float* out, double* scores, int* live) {
+  int nl = 0;
+  for (int j = 0; j < C; j++) {
+    const int64_t d = cur - (int64_t)sp[j];
+    if (sp[j] >= 0 && d >= 0 && d < C) live[nl++] = j;
+  }
   for (int h = 0; h < CO_H; h++) {
-    double mx = -INFINITY;
-    for (int j = 0; j < C; j++) {
-      const int64_t d = cur - (int64_t)sp[j];
-      if (sp[j] < 0 || d < 0 || d >= C) {
-        scores[j] = -INFINITY;
-        continue;
+    double qd[CO_HD];
+    for (int i = 0; i < CO_HD; i++) qd[i] = q[h * CO_HD + i];
+    /* each score is its own sum over i in ascending order; four slots' sums
+     * run side by side so their dependency chains overlap */
+    int t = 0;
+    for (; t + 4 <= nl; t += 4) {
+      const float* k0 = K + (int64_t)live[t] * CO_D + h * CO_HD;
+      const float* k1 = K + (int64_t)live[t + 1] * CO_D + h * CO_HD;
+      const float* k2 = K + (int64_t)live[t + 2] * CO_D + h * CO_HD;
+      const float* k3 = K + (int64_t)live[t + 3] * CO_D + h * CO_HD;
+      double s0 = 0.0, s1 = 0.0, s2 = 0.0, s3 = 0.0;
+      for (int i = 0; i < CO_HD; i++) {
+        s0 += qd[i] * (double)k0[i];
+        s1 += qd[i] * (double)k1[i];
+        s2 += qd[i] * (double)k2[i];
+        s3 += qd[i] * (double)k3[i];
       }
+      scores[t] = s0 * 0.125;
+      scores[t + 1] = s1 * 0.125;
+      scores[t + 2] = s2 * 0.125;
+      scores[t + 3] = s3 * 0.125;
+    }
+    for (; t < nl; t++) {
+      const float* kr = K + (int64_t)live[t] * CO_D + h * CO_HD;
       double s = 0.0;
-      for (int i = 0; i < CO_HD; i++)
-        s += (double)q[h * CO_HD + i] * (double)K[(int64_t)j * CO_D + h * CO_HD + i];
-      scores[j] = s * 0.125;
-      if (scores[j] > mx) mx = scores[j];
+      for (int i = 0; i < CO_HD; i++) s += qd[i] * (double)kr[i];
+      scores[t] = s * 0.125;
     }
+    double mx = -INFINITY;
+    for (t = 0; t < nl; t++)
+      if (scores[t] > mx) mx = scores[t];
+    /* the softmax and P V over the live slots in ascending slot order */
     double sum = 0.0;
-    for (int j = 0; j < C; j++) {
-      scores[j] = scores[j] == -INFINITY ? 0.0 : exp(scores[j] - mx);
-      sum += scores[j];
+    for (t = 0; t < nl; t++) {
+      scores[t] = exp(scores[t] - mx);
+      sum += scores[t];
     }
-    for (int i = 0; i < CO_HD; i++) {
-      double acc = 0.0;
-      for (int j = 0; j < C; j++)
-        if (scores[j] != 0.0) acc += scores[j] * (double)V[(int64_t)j * CO_D + h * CO_HD + i];
-      out[h * CO_HD + i] = sum > 0.0 ? (float)(acc / sum) : 0.0f;
+    double acc[CO_HD];
+    for (int i = 0; i < CO_HD; i++) acc[i] = 0.0;
+    for (t = 0; t < nl; t++) {
+      if (scores[t] == 0.0) continue;
+      const float* vr = V + (int64_t)live[t] * CO_D + h * CO_HD;
+      for (int i = 0; i < CO_HD; i++) acc[i] += scores[t] * (double)vr[i];
     }
+    for (int i = 0; i < CO_HD; i++) out[h * CO_HD + i] = sum > 0.0 ? (float)(acc[i] / sum) : 0.0f;
   }
 }
 
@@ -171,8 +198,9 @@ int or_codec_decode(const or_codec* W, float* ringK, float* ringV, int32_t* slot
   float* x = (float*)malloc(sizeof(float) * 32 * CO_D);
   float* out = (float*)malloc(sizeof(float) * 32 * CO_RVQ_OUT);
   double* scores = (double*)malloc(sizeof(double) * (size_t)maxC);
-  if (!in || !x || !out || !scores) {
-    free(in); free(x); free(out); free(scores);
+  int* live = (int*)malloc(sizeof(int) * (size_t)maxC);
+  if (!in || !x || !out || !scores || !live) {
+    free(in); free(x); free(out); free(scores); free(live);
     return -1;
   }
   float h[CO_D], qkv[3 * CO_D], q[CO_D], ctx[CO_D], proj[CO_D], ffn[CO_FFN];
@@ -204,7 +232,7 @@ int or_codec_decode(const or_codec* W, float* ringK, float* ringV, int32_t* slot
               V[(int64_t)slot * CO_D + d] = or_bf16_round(V[(int64_t)slot * CO_D + d]);
             }
           sp[slot] = (int32_t)p;
-          attend(q, p, C, K, V, sp, ctx, scores);
+          attend(q, p, C, K, V, sp, ctx, scores, live);
           gemv(ctx, L->o, CO_D, CO_D, proj);
           for (int d = 0; d < CO_D; d++) xi[d] = xi[d] + L->s1[d] * proj[d];
           or_layernorm(xi, L->ln2_w, L->ln2_b, CO_D, h);
@@ -236,6 +264,7 @@ int or_codec_decode(const or_codec* W, float* ringK, float* ringV, int32_t* slot
   free(x);
   free(out);
   free(scores);
+  free(live);
   return 0;
 }
 

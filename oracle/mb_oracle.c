@@ -362,6 +362,7 @@ typedef struct {
   const float* audio_heads[OR_NVQ];   /* [768][1024] each */
   int audio_end_id, assistant_id;     /* 7, 9 */
   double penalty;                     /* 1.2, a JS number in the reference */
+  int penalty_f32;                    /* 1: the WGSL engine's f32 penalty arithmetic */
 } or_model;
 
 /* Embed one 17-wide row: wte[row[0]] + sum_k audio_k[row[1+k]], pads skipped,
@@ -452,16 +453,24 @@ int or_model_decode_step(const or_model* M, int C, int wrap, int kv_bf16, const 
  * as in the JS reference (GEN.audio_repetition_penalty is the JS number 1.2,
  * mossTtsRuntime.js:506-521).  Returns the winning id; *best_out / *second_out get the
  * winning and runner-up penalised scores (for margin reports). */
-int or_argmax_penalty(const float* logits, int n, const uint32_t* seen, double penalty,
-                      double* best_out, double* second_out) {
+int or_argmax_penalty_prec(const float* logits, int n, const uint32_t* seen, double penalty,
+                           int f32, double* best_out, double* second_out) {
   int any = 0;
   for (int w = 0; w < (n + 31) / 32; w++) any |= seen[w] != 0;
   const int apply = any && penalty != 1.0;
+  const float pf = (float)penalty;
   int best = 0;
   double bv = -INFINITY, sv = -INFINITY;
   for (int i = 0; i < n; i++) {
     double s = logits[i];
-    if (apply && ((seen[i >> 5] >> (i & 31)) & 1u)) s = s < 0 ? s * penalty : s / penalty;
+    if (apply && ((seen[i >> 5] >> (i & 31)) & 1u)) {
+      if (f32) { /* ARGMAX_PENALTY, kernels-decode.ts:454-461: f32 penalty and arithmetic */
+        const float x = logits[i];
+        s = x < 0.0f ? (double)(x * pf) : (double)(x / pf);
+      } else {
+        s = s < 0 ? s * penalty : s / penalty;
+      }
+    }
     if (s > bv) {
       sv = bv;
       bv = s;
@@ -473,6 +482,11 @@ int or_argmax_penalty(const float* logits, int n, const uint32_t* seen, double p
   if (best_out) *best_out = bv;
   if (second_out) *second_out = sv;
   return best;
+}
+
+int or_argmax_penalty(const float* logits, int n, const uint32_t* seen, double penalty,
+                      double* best_out, double* second_out) {
+  return or_argmax_penalty_prec(logits, n, seen, penalty, 0, best_out, second_out);
 }
 
 /* Continue/stop decision (policy.ts:297-302, kernels-decode.ts:487-518): two
@@ -528,7 +542,8 @@ int or_local_frame(const or_model* M, const float* hidden, uint32_t* seen, int32
       local_step(M, x, ch + 1, K, V, sp, h);
       or_gemm(1, OR_D, OR_CODES, h, M->audio_heads[ch], NULL, logits);
       double bv, sv;
-      const int tok = or_argmax_penalty(logits, OR_CODES, seen + ch * 32, M->penalty, &bv, &sv);
+      const int tok = or_argmax_penalty_prec(logits, OR_CODES, seen + ch * 32, M->penalty,
+                                             M->penalty_f32, &bv, &sv);
       if (margins) margins[ch + 1] = bv - sv;
       codes[ch] = tok;
       seen[ch * 32 + (tok >> 5)] |= 1u << (tok & 31);

@@ -76,6 +76,8 @@ def _load(path, codec=True):
     L.or_gelu_tanh.argtypes = [C.c_float]
     L.or_gelu_tanh.restype = C.c_float
     L.or_argmax_penalty.argtypes = [_f32p, C.c_int, _u32p, C.c_double, C.c_void_p, C.c_void_p]
+    L.or_argmax_penalty_prec.argtypes = [_f32p, C.c_int, _u32p, C.c_double, C.c_int, C.c_void_p,
+                                         C.c_void_p]
     L.or_build_rows.argtypes = [C.c_int, _i32p, C.c_int, _i32p, _i32p]
     L.or_embed_row.argtypes = [C.c_void_p, _i32p, _f32p]
     L.or_text_decide.argtypes = [C.c_void_p, _f32p, C.c_void_p, C.c_void_p]
@@ -212,14 +214,15 @@ def gelu(x) -> np.ndarray:
     return f(np.asarray(x, np.float32))
 
 
-def argmax_penalty(logits, seen_ids=(), penalty: float = 1.2):
+def argmax_penalty(logits, seen_ids=(), penalty: float = 1.2, f32: bool = False):
+    """Penalised argmax; f32 selects the WGSL engine's f32 penalty arithmetic."""
     logits = _c(logits, np.float32)
     seen = np.zeros((logits.size + 31) // 32, np.uint32)
     for i in seen_ids:
         seen[i >> 5] |= np.uint32(1 << (i & 31))
     bv, sv = C.c_double(), C.c_double()
-    tok = lib().or_argmax_penalty(logits, logits.size, seen, C.c_double(penalty), C.byref(bv),
-                                  C.byref(sv))
+    tok = lib().or_argmax_penalty_prec(logits, logits.size, seen, C.c_double(penalty), int(f32),
+                                       C.byref(bv), C.byref(sv))
     return tok, bv.value, sv.value
 
 
@@ -253,6 +256,7 @@ class _Model(C.Structure):
         ("audio_heads", C.c_void_p * NVQ),
         ("audio_end_id", C.c_int), ("assistant_id", C.c_int),
         ("penalty", C.c_double),
+        ("penalty_f32", C.c_int),
     ]
 
 
@@ -266,7 +270,8 @@ class Model:
     reference's ONNX tensor names, ref-decode.mjs:40-80)."""
 
     def __init__(self, weights: dict, n_layers: int, vocab: int, penalty: float = 1.2,
-                 audio_end_id: int = 7, assistant_id: int = 9, fp32: bool = False):
+                 audio_end_id: int = 7, assistant_id: int = 9, fp32: bool = False,
+                 penalty_f32: bool = False):
         # fp32 selects the fp32-accumulating baseline build (timing only)
         self._lib = lib_fp32() if fp32 else lib()
         self._keep = {k: _c(v, np.float32) for k, v in weights.items()}
@@ -290,6 +295,7 @@ class Model:
         m.local_lnf_b = w["model.local_transformer.ln_f.bias"].ctypes.data
         m.text_head = w["model.text_lm_head.weight"].ctypes.data
         m.audio_end_id, m.assistant_id, m.penalty = audio_end_id, assistant_id, penalty
+        m.penalty_f32 = int(penalty_f32)
         self._m = m
         self.n_layers, self.vocab = n_layers, vocab
 
@@ -367,6 +373,17 @@ class ModelState:
                                               _c(pos, np.int32), self.K, self.V, self.slot_pos, out)
         if rc != 0:
             raise ValueError("decode position exceeds the KV ring")
+        return out
+
+    def select(self, voices) -> "ModelState":
+        """A new state holding copies of the given voices' rings and
+        repetition history, in that order."""
+        idx = list(voices)
+        out = ModelState(self.m, len(idx), self.C, kv_bf16=self.kv_bf16, wrap=self.wrap)
+        out.K[:] = self.K[idx]
+        out.V[:] = self.V[idx]
+        out.slot_pos[:] = self.slot_pos[idx]
+        out.seen[:] = self.seen[idx]
         return out
 
     def local_frame(self, hidden: np.ndarray):

@@ -39,3 +39,19 @@ def write_sidecar(manifest_path: str, tensors) -> None:
             off += a.nbytes
     with open(manifest_path, "w") as f:
         json.dump({"data": os.path.basename(data_path), "tensors": entries}, f)
+
+
+BF16_ROUNDED = ("attn.c_attn.weight", "attn.c_proj.weight", "mlp.fc_in.weight", "mlp.fc_out.weight")
+
+
+def rounded_weights(w):
+    """The model as bf16 weight storage holds it: every layer's projection
+    matrices and the audio heads rounded to bf16 (round to nearest even),
+    everything else as uploaded."""
+    from oracle import oracle
+
+    out = dict(w)
+    for name, a in w.items():
+        if name.endswith(BF16_ROUNDED) or name.startswith("model.audio_lm_heads."):
+            out[name] = oracle.bf16_round(a)
+    return out

@@ -67,9 +67,16 @@ async function single() {
   } catch (e) {
     busy = e.code;
   }
+  // dispose while the prefill is in flight is refused and leaves the engine usable
+  let disposeBusy = null;
+  try {
+    engine.dispose();
+  } catch (e) {
+    disposeBusy = e.code;
+  }
   await pending;
   running = false;
-  res.async = { ticks, busy };
+  res.async = { ticks, busy, disposeBusy, disposedEarly: engine.disposed };
   // the codec: the voice's code frames over two calls (the rings carry over)
   const codes = spec.codec.single;
   const a = await engine.decodeFrames(codes.slice(0, 2));
@@ -114,10 +121,34 @@ async function multi() {
   };
 }
 
+// Engines with bf16 K/V rings, fp32 and bf16 weights: creation runs the
+// warm-up (its decode-vs-prefill check then compares fp32 decode attention
+// with the bf16 prefill path), then the prompt's prefill and one frame.
+async function bf16Variants() {
+  const res = [];
+  for (const weightDtype of ["f32", "bf16"]) {
+    const engine = await createGpuEngineFor({ global: tables.global, local: tables.local }, log, {
+      localHead,
+      maxSlots: spec.maxSlots,
+      layers: spec.layers,
+      kvDtype: "bf16",
+      weightDtype,
+      penaltyPrecision: weightDtype === "bf16" ? "f32" : "f64",
+    });
+    const prompt = spec.prompts[0];
+    const hidden = await engine.prefill({ inputIds: prompt, attentionMask: [prompt.map(() => 1)] });
+    const frame = await engine.nextFrame(hidden);
+    engine.dispose();
+    res.push({ weightDtype, prefillHidden: Array.from(hidden), frame });
+  }
+  return res;
+}
+
 // Node 12 has no top-level await
 (async () => {
   out.single = await single();
   out.multi = await multi();
+  out.bf16 = await bf16Variants();
   console.log(JSON.stringify(out));
 })().catch((error) => {
   console.error(error && error.stack ? error.stack : error);

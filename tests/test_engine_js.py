@@ -15,7 +15,7 @@ BINDINGS = {
     "KV", "abiVersion", "cancel", "clearSeen", "create", "decodeAttention", "decodeFrames",
     "decodeStep", "destroy", "deviceBytes", "lastError", "localFrame", "localSteps", "prefill",
     "prefillAttention", "readRing", "ringAppend", "ringPoison", "ringReset", "ringWriteRows",
-    "setLocalHead", "setWeightStorage", "uploadTensor", "codecInit", "codecReset", "codecDecode",
+    "setLocalHead", "setWeightStorage", "setPenaltyPrecision", "uploadTensor", "codecInit", "codecReset", "codecDecode",
     "prefillAsync", "decodeStepAsync", "localFrameAsync", "decodeFramesAsync", "codecDecodeAsync",
 }
 

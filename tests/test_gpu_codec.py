@@ -13,8 +13,9 @@ visible window of every query is the same, so the PCM must agree:
   step; measured 1e-5).
 
 Small windows (6, 12, 20, 40 positions) make every ring wrap within a few
-frames; the full-size case runs the real stage shapes (4, 2, 2, 4 layers,
-windows 500 / 1696 / 2480 / 3248).
+frames; the full-size cases run the real stage shapes (4, 2, 2, 4 layers,
+windows 500 / 1696 / 2480 / 3248), for 3 frames and for long runs at the
+benchmark's voice counts in which the rings fill and wrap.
 """
 import numpy as np
 import pytest
@@ -128,6 +129,35 @@ def test_codec_full_size_shapes():
     for b in range(B):
         r = _close(got[b], want[b], 2e-5, f"voice {b}")
         say(f"  voice {b}: max error / scale {r:.2e}")
+
+
+@pytest.mark.parametrize("B,kv,frames", [(256, mb.MB_KV_BF16, 216), (64, mb.MB_KV_F32, 110)])
+def test_codec_full_size_long_run(B, kv, frames):
+    """The real stage shapes at the benchmark's voice counts and ring types
+    (256 voices with bf16 rings, 64 with fp32 rings), so the projections run
+    the row-tiled forms the benchmark times, decoded in calls of 24 frames.
+    Over 216 frames every stage's ring fills and wraps (stage 2, the last to
+    fill, holds 1696 + 8 slots: 213 frames); over 110 frames stages 1 and 4
+    wrap.  The oracle follows three voices in different row tiles; their PCM
+    must agree within the bar of the ring type on every call."""
+    say(f"codec full size, {B} voices, kv={kv}, {frames} frames")
+    watch = [0, B // 2 + 3, B - 1]
+    w = synth.codec_weights(mb.CODEC_LAYERS, seed=19)
+    codes = synth.codec_codes(20, frames, B)
+    ora = oracle.CodecOracle(w, len(watch), kv_bf16=(kv == mb.MB_KV_BF16))
+    rel = 2e-5 if kv == mb.MB_KV_F32 else 1e-3
+    worst = 0.0
+    with _ctx() as ctx:
+        ctx.upload_all(w)
+        ctx.codec_init(B, kv_dtype=kv)
+        for f0 in range(0, frames, 24):
+            f1 = min(frames, f0 + 24)
+            got = ctx.codec_decode(codes[f0:f1])
+            want = ora.decode(np.ascontiguousarray(codes[f0:f1][:, watch]))
+            for i, b in enumerate(watch):
+                worst = max(worst, _close(got[b], want[i], rel, f"voice {b} frames {f0}-{f1}"))
+            assert np.isfinite(got).all()
+    say(f"  max error / scale over {len(watch)} voices: {worst:.2e}")
 
 
 def test_codec_argument_errors():

@@ -22,7 +22,7 @@ import pytest
 
 from mockbird_amd import synth
 from oracle import oracle
-from conftest import say, write_sidecar
+from conftest import rounded_weights, say, write_sidecar
 from frame_check import FrameCheck
 
 pytestmark = pytest.mark.gpu
@@ -117,6 +117,7 @@ def test_engine_runtime_loop_and_multivoice_match_oracle(tmp_path):
     a = s["async"]
     say(f"  event-loop turns during one prefill: {a['ticks']}; overlapping call: {a['busy']}")
     assert a["ticks"] >= 1 and a["busy"] == "MB_ERR_BUSY"
+    assert a["disposeBusy"] == "MB_ERR_BUSY" and a["disposedEarly"] is False
 
     mv = out["multi"]
     for b, p in enumerate(prompts):
@@ -139,3 +140,15 @@ def test_engine_runtime_loop_and_multivoice_match_oracle(tmp_path):
     assert got3.shape == want3.shape
     assert np.abs(got3 - want3).max() <= 2e-5 * np.abs(want3).max()
     say("  codec: decodeFrames and decodeAudio match the oracle")
+
+    # bf16 K/V engines passed their warm-up (creation returned) with fp32 and
+    # bf16 weights; their prefill is the oracle's within the bf16 bar, on
+    # the bf16-rounded weights for weightDtype "bf16"
+    assert [v["weightDtype"] for v in out["bf16"]] == ["f32", "bf16"]
+    for v in out["bf16"]:
+        wv = w if v["weightDtype"] == "f32" else rounded_weights(w)
+        st = oracle.ModelState(oracle.Model(wv, n_layers=L, vocab=V), 1, C, kv_bf16=True)
+        h0 = st.prefill_all(0, prompts[0])[-1]
+        err = float(np.abs(np.array(v["prefillHidden"], np.float32) - h0).max())
+        say(f"  bf16 K/V engine, {v['weightDtype']} weights: prefill within {err:.2e}")
+        assert err < 2e-2 and v["frame"] is not None and len(v["frame"]) == 16

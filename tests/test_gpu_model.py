@@ -219,13 +219,16 @@ def _c3_prompts(B):
 
 
 def test_c3_many_voices():
-    """256 voices with prompt lengths U[64, 400), bf16 KV, ring 1024.  The GPU
-    runs every voice; the oracle follows 8 of them (shortest, longest and six
-    others), teacher-forced: 40 frames driven call by call with every
-    watched voice's logits, codes and hidden states compared, then 20 more
-    through mb_decode_frames (graph replay) with the codes compared and the
-    hidden state checked at the end."""
-    say("C3: B=256 prefill + 40 per-call frames + 20 graph frames, 8 voices checked")
+    """256 voices with prompt lengths U[64, 400), bf16 KV, ring 1024, the
+    configuration's 300 frames.  The GPU runs every voice; the oracle follows
+    8 of them (shortest, longest and six others), teacher-forced: 40 frames
+    driven call by call with every watched voice's logits, codes and hidden
+    states compared, then 260 through mb_decode_frames (graph replay) with
+    the codes compared -- all 8 voices for the first 20 of them (hidden
+    states checked there), the shortest and the longest voice through all
+    260, so the longest reaches position 698 -- and the hidden state checked
+    at the end."""
+    say("C3: B=256 prefill + 40 per-call frames + 260 graph frames, 8 voices checked")
     B, C = 256, 1024
     w = _c0_weights()
     prompts, n, ids = _c3_prompts(B)
@@ -262,8 +265,10 @@ def test_c3_many_voices():
             max_h = max(max_h, d)
             assert d < tol, f
             pos = pos + 1
-        codes, cont, h_end, p_end = ctx.decode_frames(h, pos, 20)
-        assert cont.all() and (p_end == pos + 20).all()
+        G = 260
+        codes, cont, h_end, p_end = ctx.decode_frames(h, pos, G)
+        assert cont.all() and (p_end == pos + G).all()
+        assert int(p_end.max()) == int(n.max()) + 300 <= C
         for f in range(20):
             for i, b in enumerate(watch):
                 o_text, o_logits = m.local_logits(h_or[i], codes[f, b])
@@ -271,21 +276,38 @@ def test_c3_many_voices():
                           o_logits, tol, bar=2.4 * tol)
             h_or = st.decode_step(np.stack([synth.frame_row(codes[f, b]) for b in watch]),
                                   pos[watch] + f)
-        d = float(np.abs(h_end[watch] - h_or).max())
+        # the shortest and the longest voice on to the 300th frame
+        ends = [watch.index(int(np.argmin(n))), watch.index(int(np.argmax(n)))]
+        st2 = st.select(ends)
+        h2 = h_or[ends]
+        far = [watch[i] for i in ends]
+        for f in range(20, G):
+            for j, b in enumerate(far):
+                o_text, o_logits = m.local_logits(h2[j], codes[f, b])
+                chk.frame(ends[j], f"graph frame {f} voice {b}", codes[f, b], cont[f, b], o_text,
+                          o_logits, tol, bar=2.4 * tol)
+            h2 = st2.decode_step(np.stack([synth.frame_row(codes[f, b]) for b in far]),
+                                 pos[far] + f)
+        d = float(np.abs(h_end[far] - h2).max())
         assert d < tol
+        for l in (0, 11):
+            for j, b in enumerate(far):
+                k, v, sp = ctx.read_ring(l, b)
+                assert np.array_equal(sp, st2.slot_pos[j, l]), (l, b)
     chk.summary("C3")
     say(f"  C3: max |hidden diff| {max(max_h, d):.2e}")
-    assert chk.codes_equal + chk.codes_tied == 8 * 60 * 16
-    assert chk.codes_equal >= 0.99 * 8 * 60 * 16
+    total = 8 * 60 * 16 + 2 * (G - 20) * 16
+    assert chk.codes_equal + chk.codes_tied == total
+    assert chk.codes_equal >= 0.99 * total
 
 
-def _crafted_head_weights():
+def _crafted_head_weights(hi=3, lo=5):
     """A 2-layer model whose local ln_f has scale 0 and shift e_0, so every
     local step's output is exactly e_0: each audio head's logits are then its
     row 0 exactly (also through the LayerNorm-folded head), and the text
     decision is text_head[0][9] = 1 against text_head[0][7] = 0 (always go
-    on).  Row 0 of every head holds 1.0 at id 3, fp32(0.8333333) at id 5,
-    0.81 at id 11 and -1 elsewhere."""
+    on).  Row 0 of every head holds 1.0 at id `hi`, fp32(0.8333333) at id
+    `lo`, 0.81 at id 11 and -1 elsewhere."""
     w = synth.model_weights(n_layers=2, vocab=64, seed=5)
     w["model.local_transformer.ln_f.weight"] = np.zeros(768, np.float32)
     e0 = np.zeros(768, np.float32)
@@ -294,16 +316,16 @@ def _crafted_head_weights():
     th = w["model.text_lm_head.weight"]
     th[0, 7], th[0, 9] = 0.0, 1.0
     row = np.full(1024, -1.0, np.float32)
-    row[3], row[5], row[11] = 1.0, np.float32(0.8333333), 0.81
+    row[hi], row[lo], row[11] = 1.0, np.float32(0.8333333), 0.81
     for k in range(16):
         w[f"model.audio_lm_heads.{k}.weight"][0] = row
     return w, row
 
 
-def _expected_codes(row, n_frames, penalty, seen):
+def _expected_codes(row, n_frames, penalty, seen, f32=False):
     out = []
     for _ in range(n_frames):
-        tok = oracle.argmax_penalty(row, sorted(seen), penalty)[0]
+        tok = oracle.argmax_penalty(row, sorted(seen), penalty, f32=f32)[0]
         out.append(tok)
         seen.add(tok)
     return out
@@ -346,6 +368,47 @@ def test_penalty_is_the_double_and_settings_reach_the_frame_graph():
                 ref.set_local_head(7, 9, 1.25)
             codes, cont = ref.local_frame(h)
             assert (codes == (want1 + want2)[f]).all(), (f, codes)
+            h = ref.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
+            pos = pos + 1
+
+
+def test_penalty_precision_f32_is_the_wgsl_arithmetic():
+    """MB_PENALTY_F32, the WGSL engine's arithmetic (kernels-decode.ts:454-461):
+    id 5 holds 1.0 and id 3 fp32(0.8333333).  Once 5 has been drawn, its f32
+    penalised score 1.0 / 1.2f rounds to exactly fp32(0.8333333), a tie that
+    the lower id 3 wins, while the double 1.0 / 1.2 = 0.83333333 keeps 5.
+    Per call and through the frame graph (the precision switched between two
+    mb_decode_frames calls on the same buffers, so the graph must be taken
+    again), every channel of both voices follows the oracle's f32 or double
+    choice, and the oracle's f32 path (plain fp32 division) agrees with the
+    kernel's (a double quotient rounded once to f32)."""
+    say("penalty precision: f32 (WGSL engine) against f64 (CPU path)")
+    w, row = _crafted_head_weights(hi=5, lo=3)
+    want64 = _expected_codes(row, 3, 1.2, set())
+    want32 = _expected_codes(row, 3, 1.2, set(), f32=True)
+    assert want64[:2] == [5, 5] and want32[:2] == [5, 3]  # the case discriminates
+    B = 2
+    ids, n = _prompt_batch(B, 64, 90)
+    with _ctx(w, 2, 64, B, 64) as ctx:
+        h = ctx.prefill(ids, n)
+        c1, f1, h1, p1 = ctx.decode_frames(h, n, 3)
+        ctx.clear_seen()
+        ctx.set_penalty_precision(mb.MB_PENALTY_F32)
+        c2, f2, _, _ = ctx.decode_frames(h1, p1, 3)
+        with pytest.raises(mb.MbError) as e:
+            ctx.set_penalty_precision(2)
+        assert e.value.code == mb.MB_ERR_ARG
+    assert f1.all() and f2.all()
+    for f in range(3):
+        assert (c1[f] == want64[f]).all(), (f, c1[f])
+        assert (c2[f] == want32[f]).all(), (f, c2[f])
+    with _ctx(w, 2, 64, B, 64) as ref:  # the f32 frames call by call
+        ref.set_penalty_precision(mb.MB_PENALTY_F32)
+        h = ref.prefill(ids, n)
+        pos = n.copy()
+        for f in range(3):
+            codes, cont = ref.local_frame(h)
+            assert (codes == want32[f]).all(), (f, codes)
             h = ref.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
             pos = pos + 1
 

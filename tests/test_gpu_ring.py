@@ -257,51 +257,62 @@ def test_c4_eviction_stress():
 
 
 def test_c4_bf16_wrapped_full_size():
-    """B=32, C=4096, bf16 KV: rows 0..4999 written through the row writer
-    (every ring wraps and evicts 904 slots), then one fused append + attention
-    step at position 5000, as the wrapped decode workload runs it; every
-    sequence's slot positions by the closed-form window, 8 sequences' rings
-    bit-exact and their attention within 1e-4 of the oracle."""
+    """B=32, C=4096, bf16 KV, as the wrapped decode workload runs it: rows
+    written through the row writer and fused append + attention steps at the
+    checkpoints 4095 (the ring just full, nothing evicted), 4096 (slot 0 now
+    holds 4096, position 0 evicted), 4097 and 5000 (window 905..5000; rows
+    4098..4999 written by the row writer in between).  At every checkpoint
+    every sequence's slot positions follow the closed-form window, and 8
+    sequences' rings are bit-exact and their attention within 1e-4 of the
+    oracle's on the same stored values."""
     torch = pytest.importorskip("torch")
     say("C4 bf16 wrapped full size")
     B, C, P = 32, 4096, 5000
+    steps = (4095, 4096, 4097, P)
     watch = [0, 5, 11, 16, 21, 26, 30, 31]
     dev = torch.device("cuda")
     chunk = 256
-    host_rows = {b: [] for b in watch}
+    rings = {b: _oracle_ring(1, C, mb.MB_KV_BF16) for b in watch}
     with mb.Context(n_layers=1, capacity=C, max_seqs=B, max_rows=chunk, kv_dtype=mb.MB_KV_BF16) as ctx:
         ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-        for c0 in range(0, P, chunk):
-            rows = np.random.default_rng([45, c0]).standard_normal((B, chunk, 2304), dtype=np.float32)
-            nrow = min(chunk, P - c0)
-            qkv = torch.from_numpy(rows).to(dev)
-            n = torch.full((B,), nrow, dtype=torch.int32, device=dev)
-            p0 = torch.full((B,), c0, dtype=torch.int32, device=dev)
-            ctx.ring_write_rows_dev(0, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+
+        def write_rows(lo, hi):
+            for c0 in range(lo, hi, chunk):
+                nrow = min(chunk, hi - c0)
+                rows = np.random.default_rng([45, c0]).standard_normal((B, chunk, 2304),
+                                                                        dtype=np.float32)
+                qkv = torch.from_numpy(rows).to(dev)
+                n = torch.full((B,), nrow, dtype=torch.int32, device=dev)
+                p0 = torch.full((B,), c0, dtype=torch.int32, device=dev)
+                ctx.ring_write_rows_dev(0, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
+                for b in watch:
+                    rings[b].write(rows[b:b + 1, :nrow], [c0], [nrow])
+
+        written = 0
+        for p in steps:
+            write_rows(written, p)
+            say(f"  checkpoint {p}")
+            step = np.random.default_rng([46, p]).standard_normal((B, 2304), dtype=np.float32)
+            step_d = torch.from_numpy(step).to(dev)
+            pos_d = torch.full((B,), p, dtype=torch.int32, device=dev)
+            out = torch.empty((B, 768), device=dev)
+            ctx.append_attend_dev(0, B, step_d.data_ptr(), pos_d.data_ptr(), p, out.data_ptr())
+            torch.cuda.synchronize()
+            written = p + 1
+            out_h = out.cpu().numpy()
+            assert np.isfinite(out_h).all()
+            want_sp = np.full(C, -1, np.int32)
+            for pp in range(max(0, p - C + 1), p + 1):
+                want_sp[pp % C] = pp
+            for b in range(B):
+                assert np.array_equal(ctx.read_ring(0, b)[2], want_sp), (p, b)
             for b in watch:
-                host_rows[b].append(rows[b, :nrow])
-        step = np.random.default_rng(46).standard_normal((B, 2304), dtype=np.float32)
-        step_d = torch.from_numpy(step).to(dev)
-        pos_d = torch.full((B,), P, dtype=torch.int32, device=dev)
-        out = torch.empty((B, 768), device=dev)
-        ctx.append_attend_dev(0, B, step_d.data_ptr(), pos_d.data_ptr(), P, out.data_ptr())
-        torch.cuda.synchronize()
-        out_h = out.cpu().numpy()
-        assert np.isfinite(out_h).all()
-        want_sp = np.full(C, -1, np.int32)
-        for pp in range(P - C + 1, P + 1):
-            want_sp[pp % C] = pp
-        for b in range(B):
-            assert np.array_equal(ctx.read_ring(0, b)[2], want_sp), b
-        for b in watch:
-            ring = _oracle_ring(1, C, mb.MB_KV_BF16)
-            allrows = np.concatenate(host_rows[b] + [step[b][None]])[None]
-            qo = ring.write(allrows, [0], [P + 1])[0, -1]
-            k, v, sp = ctx.read_ring(0, b)
-            assert np.array_equal(sp, ring.slot_pos[0])
-            assert np.array_equal(k, ring.K[0]) and np.array_equal(v, ring.V[0]), b
-            want = ring.attend(qo[None], [P])[0]
-            assert np.abs(out_h[b] - want).max() < 1e-4, b
+                qo = rings[b].append(step[b][None], [p])[0]
+                k, v, sp = ctx.read_ring(0, b)
+                assert np.array_equal(sp, rings[b].slot_pos[0])
+                assert np.array_equal(k, rings[b].K[0]) and np.array_equal(v, rings[b].V[0]), (p, b)
+                want = rings[b].attend(qo[None], [p])[0]
+                assert np.abs(out_h[b] - want).max() < 1e-4, (p, b)
 
 
 @pytest.mark.parametrize("name,kv", KV)

@@ -13,7 +13,9 @@ rows instead of folding into the weights is exercised.
 
 Voice counts pick the kernels: 3 voices run the GEMV kernel on the bf16
 k-major copies, 12 voices the two-product split-bf16 kernel (bf16 K/V) or
-the folded fp32 streaming kernel on the rounded weights (fp32 K/V).
+the folded fp32 streaming kernel on the rounded weights (fp32 K/V); 64 and
+256 voices (bf16 K/V) run the split-bf16 kernel's row-tiled forms that the
+benchmark's many-voice frames use.
 """
 import numpy as np
 import pytest
@@ -21,23 +23,12 @@ import pytest
 import mockbird_amd as mb
 from mockbird_amd import synth
 from oracle import oracle
-from conftest import say
+from conftest import rounded_weights, say
 from frame_check import FrameCheck
 
 pytestmark = pytest.mark.gpu
 
 TOL = {mb.MB_KV_F32: 1e-4, mb.MB_KV_BF16: 2e-2}
-ROUNDED = ("attn.c_attn.weight", "attn.c_proj.weight", "mlp.fc_in.weight", "mlp.fc_out.weight")
-
-
-def rounded_weights(w):
-    """The model as bf16 storage holds it: the projection matrices and the
-    audio heads rounded to bf16, everything else as uploaded."""
-    out = dict(w)
-    for name, a in w.items():
-        if name.endswith(ROUNDED) or name.startswith("model.audio_lm_heads."):
-            out[name] = oracle.bf16_round(a)
-    return out
 
 
 def _prompts(B, V):
@@ -89,9 +80,64 @@ def test_bf16_weights_prefill_decode_frames(kv, B):
     assert chk.codes_equal + chk.codes_tied >= 16 * 5  # at least one voice went on every frame
 
 
+@pytest.mark.parametrize("B", [64, 256])
+def test_bf16_weights_many_voices(B):
+    """bf16 K/V and bf16 weights at the benchmark's voice counts, where the
+    decode projections run the row-tiled two-product split-bf16 kernel with
+    bf16 weights (several row tiles, the LayerNorm scale applied to the rows,
+    fc_out split over k) and the local head's projections the same at B rows.
+    The GPU runs every voice; the oracle, on the rounded weights, follows
+    six voices spread over the row tiles, teacher-forced by the GPU's codes:
+    prefill hidden states, every frame's logits and codes, and the hidden
+    state after each of 5 decode steps within the bf16 bar."""
+    say(f"bf16 weights: kv=bf16 voices={B}")
+    L, V, C = 2, 64, 128
+    w = synth.model_weights(n_layers=L, vocab=V, seed=23, bias_std=0.02, ln_std=0.1)
+    w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]  # never stops
+    m = oracle.Model(rounded_weights(w), n_layers=L, vocab=V)
+    g = np.random.default_rng(B)
+    lens = g.integers(8, 60, size=B)
+    prompts = [synth.prompt(300 + b, n_frames=int(lens[b]) // 2,
+                            n_text=int(lens[b]) - 3 - int(lens[b]) // 2, vocab=V) for b in range(B)]
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    watch = sorted({0, 17, B // 2 - 1, B // 2 + 5, B - 16, B - 1})
+    st = oracle.ModelState(m, len(watch), C, kv_bf16=True)
+    h_or = st.prefill(np.ascontiguousarray(ids[watch]), n[watch])
+    tol = TOL[mb.MB_KV_BF16]
+    chk = FrameCheck(len(watch))
+    with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=int(n.max()),
+                    kv_dtype=mb.MB_KV_BF16, vocab=V) as ctx:
+        ctx.upload_all(w)
+        ctx.set_weight_storage(mb.MB_W_BF16)
+        h = ctx.prefill(ids, n)
+        assert np.isfinite(h).all()
+        assert np.abs(h[watch] - h_or).max() < tol
+        pos = n.copy()
+        for f in range(5):
+            codes, cont = ctx.local_frame(h)
+            assert cont.all()
+            g_text, g_logits = ctx.local_logits(h, codes)
+            for i, b in enumerate(watch):
+                o_text, o_logits = m.local_logits(h_or[i], codes[b])
+                chk.frame(i, f"frame {f} voice {b}", codes[b], cont[b], o_text, o_logits, tol,
+                          g_text[b], g_logits[b])
+            rows = np.stack([synth.frame_row(codes[b]) for b in range(B)])
+            h = ctx.decode_step(rows, pos)
+            h_or = st.decode_step(rows[watch], pos[watch])
+            assert np.abs(h[watch] - h_or).max() < tol, f
+            pos = pos + 1
+    chk.summary(f"bf16 weights kv=bf16 voices={B}")
+    assert chk.codes_equal + chk.codes_tied == len(watch) * 5 * 16
+
+
 def test_weight_storage_switches_back():
     """MB_W_BF16, then MB_W_F32 again on the same context: the copies are
-    derived again and the fp32 model's results come back."""
+    derived again, the fp32 model's results come back and the bf16 period's
+    rounded copies are freed (the context's device bytes return to the fp32
+    figure)."""
     say("bf16 weights: switch back to fp32")
     L, V, B, C = 1, 32, 2, 64
     w = synth.model_weights(n_layers=L, vocab=V, seed=5, bias_std=0.02, ln_std=0.1)
@@ -102,12 +148,16 @@ def test_weight_storage_switches_back():
     with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=64, vocab=V) as ctx:
         ctx.upload_all(w)
         assert np.abs(ctx.prefill(ids, n) - want32).max() < 1e-4
+        bytes32 = ctx.device_bytes()
         ctx.set_weight_storage(mb.MB_W_BF16)
         ctx.ring_reset()
         assert np.abs(ctx.prefill(ids, n) - want16).max() < 1e-4
+        assert ctx.device_bytes() != bytes32
         ctx.set_weight_storage(mb.MB_W_F32)
         ctx.ring_reset()
         assert np.abs(ctx.prefill(ids, n) - want32).max() < 1e-4
+        # the rounded copies are freed again: the fp32 footprint comes back
+        assert ctx.device_bytes() == bytes32
         with pytest.raises(mb.MbError) as e:
             ctx.set_weight_storage(7)
         assert e.value.code == mb.MB_ERR_ARG

@@ -91,6 +91,28 @@ def test_repetition_penalty_cases():
     assert ap(np.array([np.nan, -5.0], np.float32), [])[0] == 1
 
 
+def test_repetition_penalty_f32_mode():
+    """The WGSL engine's f32 arithmetic (kernels-decode.ts:454-461), pinned
+    against numpy's float32 arithmetic on random logits and seen sets, with
+    the case where the two precisions pick differently: 1.0 / 1.2f rounds to
+    exactly fp32(0.8333333), a tie the lower id wins."""
+    ap = oracle.argmax_penalty
+    crafted = np.array([0.8333333, 1.0], np.float32)
+    assert ap(crafted, [1])[0] == 1
+    assert ap(crafted, [1], f32=True)[0] == 0
+    assert np.float32(1.0) / np.float32(1.2) == np.float32(0.8333333)
+    g = np.random.default_rng(12)
+    p32 = np.float32(1.2)
+    for _ in range(200):
+        logits = g.standard_normal(1024).astype(np.float32)
+        seen = sorted(set(g.integers(0, 1024, size=int(g.integers(0, 40))).tolist()))
+        s = logits.copy()
+        for i in seen:
+            s[i] = s[i] * p32 if s[i] < 0 else s[i] / p32
+        want = int(np.argmax(s)) if seen else int(np.argmax(logits))
+        assert ap(logits, seen, f32=True)[0] == want
+
+
 def test_stop_rule(tiny):
     m, w = tiny
     h = np.random.default_rng(4).standard_normal(768).astype(np.float32)

@@ -2,7 +2,9 @@
 against mb_linear_dev (the entry point it varies) through the C ABI.
 
 Two calls in a row on one context, the second smaller, each with split-K
-partials in the static scratch (K = 3072 at decode-sized M): outputs equal
+partials in the static scratch (K = 3072 at decode-sized M: 256 rows split
+two ways on 32-row tiles, 64 rows four ways on 16-row tiles), so the second call reuses the
+array the first one left its partials in: outputs equal
 mb_linear_dev's bit for bit (same kernels, same summation order) and are
 within 1e-4 of float64 (the fp32 bar).  The context's device memory does not
 grow across the calls, while mb_linear_dev on the same shapes grows its
@@ -18,7 +20,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = [  # (M, N, K, epi): the second call is smaller
     (256, 768, 3072, mb.MB_EPI_ADD),
-    (8, 768, 3072, mb.MB_EPI_STORE),
+    (64, 768, 3072, mb.MB_EPI_STORE),
 ]
 
 
