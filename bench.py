@@ -17,8 +17,8 @@ the output written) / the launch's average duration, from HIP events around
 the back-to-back timed launches on the stream they run on, inputs resident in
 HBM.  Set-up fills every layer ring and reads each once (as a prefill's own
 attention does); the start event is recorded behind the warm-up launches, so
-the window holds exactly the timed launches.  The roofline object is the same launch; `traffic` comes from the
-committed rocprofv3 PMC summary.  The two-launch path (append, then
+the window holds exactly the timed launches.  The roofline object is the
+same launch; `traffic` comes from the committed rocprofv3 PMC summary.  The two-launch path (append, then
 attention) is timed beside it.  cpu_baseline = the C oracle (OpenMP) on a bounded sample
 of the same workload on this host's cores.
 """
@@ -503,12 +503,13 @@ def run_gemm(reps=60, sets=12):
                         "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
                         "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
             del a, ws, c
-    # The 256-voice decode step's projections as bf16-KV contexts run them:
-    # split-bf16 products (mb_linear_split_dev, three bf16 MFMAs per fp32
-    # product) on weights split once by mb_split_weights_dev.  FLOPs are the
-    # fp32 product's 2 M N K; the matrix cores execute three times that.
-    M = 256
-    for name, N, K in (("qkv", QKV, D), ("o", D, D), ("fc_in", 4 * D, D), ("fc_out", D, 4 * D)):
+    # The projections as bf16-KV contexts run them, at the causal-prefill
+    # configuration's 8192 rows and the 256-voice decode step's 256: split-bf16
+    # products (mb_linear_split_dev, three bf16 MFMAs per fp32 product) on
+    # weights split once by mb_split_weights_dev.  FLOPs are the fp32
+    # product's 2 M N K; the matrix cores execute three times that.
+    for M, name, N, K in [(m, *p) for m in (8192, 256) for p in (
+            ("qkv", QKV, D), ("o", D, D), ("fc_in", 4 * D, D), ("fc_out", D, 4 * D))]:
         a = torch.randn((M, K), generator=g, device=dev)
         wxs = []
         for _ in range(sets):
@@ -539,7 +540,8 @@ def run_gemm(reps=60, sets=12):
         tf = flops / (us * 1e-6) / 1e12
         out.append({"proj": name, "M": M, "K": K, "N": N, "products": "split-bf16",
                     "avg_us": round(us, 2), "gflop": round(flops / 1e9, 3), "tflops": round(tf, 1),
-                    "frac_bf16_mfma_peak": round(3 * tf / BF16_MFMA_PEAK_TFLOPS, 4)})
+                    "frac_bf16_mfma_peak": round(3 * tf / BF16_MFMA_PEAK_TFLOPS, 4),
+                    "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4)})
         del a, wxs, c
     ctx.close()
     return out

@@ -204,15 +204,17 @@ int mb_linear_dev(mb_ctx* ctx, int M, int N, int K, const float* A, int64_t lda,
                   const float* bias, float* C, int64_t ldc, int epi);
 
 /* The projection of mb_linear_dev at the precision bf16-KV model contexts
- * run their decode-sized projections in: each fp32 product a w is taken as
+ * run their projections in (above 8 rows): each fp32 product a w is taken as
  * ah wh + ah wl + al wh, with ah = bf16(a) and al = bf16(a - ah) (likewise
  * w), three bf16 MFMA products summed in fp32 -- within about 2^-16 |a w| of
  * the fp32 product, for a fifth of the matrix-core time.
  * mb_split_weights_dev writes a row-major [K, N] W in that kernel's operand
  * order to Wx (2 K N bf16 = 4 K N bytes, 16-byte aligned; N % 64 == 0,
  * K % 32 == 0); mb_linear_split_dev computes C[M][N] = epi(A W + bias) from
- * it, with mb_linear_dev's epilogues.  It takes 8 < M < 1024 (or M with at
- * most 512 tiles of 64 x 64) and K % 128 == 0; other M return MB_ERR_STATE.
+ * it, with mb_linear_dev's epilogues.  It takes M > 8: below 1024 rows (or
+ * at most 512 tiles of 64 x 64) a streaming kernel that needs K % 128 == 0,
+ * above that a kernel tiled 32-128 rows x 128 columns over all of k that
+ * needs N % 128 == 0; M <= 8 returns MB_ERR_STATE.
  * Replaces the same GEMM_NT / GEMV passes as mb_linear_dev (kernels-batch.ts:
  * 156-184, kernels-decode.ts:127-166).  Enqueue only. */
 int mb_split_weights_dev(mb_ctx* ctx, const float* W, int K, int N, void* Wx);

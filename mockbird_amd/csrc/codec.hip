@@ -380,14 +380,14 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
     for (int i = 0; i < cs.cfg.layers[s]; i++) {
       const CodecLayerW& w = st.layers[i];
       const RingView ring = codec_ring(ctx, cs, cs.layer0[s] + i, s);
-      // norm1 / norm2 are folded into the projection where the streaming
-      // kernel takes the rows, else run apart; with bf16 rings those rows
-      // take the split-bf16 products
+      // With bf16 rings every projection above kGemvMaxM rows takes the
+      // split-bf16 products, norm1 / norm2 folded into them.  With fp32 rings
+      // they are folded where the streaming kernel takes the rows, else run
+      // apart.
       const bool fold_qkv = gemm_streams(M, 3 * kD), fold_f1 = gemm_streams(M, kFfn);
       const bool x3 = w.qkv_x && M > kGemvMaxM;
-      const bool x3_d = x3 && gemm_streams(M, kD);
       auto qkv_proj = [&]() {
-        if (x3 && fold_qkv)
+        if (x3)
           return launch_gemm_x3(ctx, EPI_STORE, cs.x, kD, w.qkv_x, 3 * kD, kD, nullptr, cs.qkv,
                                 3 * kD, M, w.qkv_c, w.qkv_d);
         if (fold_qkv)
@@ -397,7 +397,7 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
         return r ? r : launch_gemm(ctx, EPI_STORE, cs.h, kD, w.qkv, 3 * kD, kD, nullptr, cs.qkv, 3 * kD, M);
       };
       auto f1_proj = [&]() {
-        if (x3 && fold_f1)
+        if (x3)
           return launch_gemm_x3(ctx, EPI_GELU_ERF, cs.x, kD, w.f1_x, kFfn, kD, nullptr, cs.ffn,
                                 kFfn, M, w.f1_c, w.f1_d);
         if (fold_f1)
@@ -411,11 +411,11 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
                                   nrow, cs.q, MB_DT_F32, dense_rows(kD, n))) ||
           (rc = launch_window_attention(ctx, ring, B, n, cs.q, dense_rows(kD, n), pos, nrow,
                                         cs.att, dense_rows(kD, n))) ||
-          (rc = x3_d ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.att, kD, w.o_x, kD, kD, w.s1, cs.x, kD,
+          (rc = x3 ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.att, kD, w.o_x, kD, kD, w.s1, cs.x, kD,
                                       M, nullptr, nullptr)
                      : launch_gemm(ctx, EPI_SCALE_ADD, cs.att, kD, w.o, kD, kD, w.s1, cs.x, kD, M)) ||
           (rc = f1_proj()) ||
-          (rc = x3_d ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2_x, kD, kFfn, w.s2, cs.x,
+          (rc = x3 ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2_x, kD, kFfn, w.s2, cs.x,
                                       kD, M, nullptr, nullptr)
                      : launch_gemm(ctx, EPI_SCALE_ADD, cs.ffn, kFfn, w.f2, kD, kFfn, w.s2, cs.x, kD, M)))
         return rc;

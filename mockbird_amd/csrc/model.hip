@@ -233,8 +233,10 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   // up to kGemvMaxM rows the projections read the k-major copies
   const bool folded = M < kFoldMaxM;
   const bool gemv = M <= kGemvMaxM;
-  // bf16-KV contexts: decode-sized projections as split-bf16 products
-  const bool x3 = !gemv && folded && w.attn_wx && gemm_streams((int)M, D);
+  // bf16-KV contexts: every projection above kGemvMaxM rows as split-bf16
+  // products, the LayerNorm folded in (the streaming kernel at decode sizes,
+  // the tiled one at prefill sizes)
+  const bool x3 = !gemv && w.attn_wx;
   if (gemv) {
     if ((rc = proj_gemv(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
                         (int)M, w.attn_c, w.attn_d, w.ln1_w)))

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "kv_types.h"
+#include "lds_dma.h"
 #include "mb_internal.h"
 
 namespace mb {
@@ -124,7 +125,6 @@ constexpr float kScoreLog2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2
 constexpr int32_t kRelEmpty = INT32_MAX;  // relative position of an empty slot
 
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) bf16x4_t lds_bf16x4_t;
 
 // Maximum over the four lanes of a column, with plain v_max_f32: fmaxf
@@ -141,49 +141,6 @@ __device__ __forceinline__ float col_max_plain(float x) {
 
 // Element offset of (slot row, 8-dim chunk x) in a swizzled 64 x 64 tile.
 __device__ __forceinline__ int swz(int row, int x) { return row * HD + ((x ^ (row & 7)) << 3); }
-
-// s_waitcnt with vmcnt = n (n < 16), expcnt and lgkmcnt left at their maxima
-// (gfx9 encoding)
-#define MB_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
-
-// global -> LDS loads (global_load_lds_dword / _dwordx4): lane L's bytes land
-// at LDS byte address lds + size * L.  Issued as inline assembly so the
-// compiler does not treat them as LDS writes: it would otherwise wait for
-// every outstanding load (the two tiles in flight) before each LDS read of
-// the tile being computed.  The kernel waits for them itself (MB_WAIT_VMCNT
-// before the barrier that publishes a tile).  Loads the compiler cannot see
-// only make its own vmcnt waits stricter, never looser.  m0 carries the LDS
-// base; the statement saves and restores it, so no register the compiler
-// owns changes under it.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_void_t*)p;
-}
-// Each lane reads base + off (base and `lds` wave-uniform, held in SGPRs;
-// off a per-lane byte offset), the scalar-base form of the global load, so a
-// tile's addresses cost no vector instructions: the per-lane offsets are
-// fixed and the base advances with the tile.
-__device__ __forceinline__ uint64_t sgpr_ptr(const void* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
-}
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved) : "v"(off), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
-      : "memory");
-}
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
-      "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
-      : "=&s"(saved) : "v"(off), "s"(sgpr_ptr(base)), "s"(__builtin_amdgcn_readfirstlane(lds))
-      : "memory");
-}
 
 template <int NW>
 __global__ __launch_bounds__(64 * NW, 3 * NW / 4) void k_flash_bf16(

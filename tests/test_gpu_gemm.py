@@ -173,6 +173,10 @@ def test_gemv_rows_1_to_8(ctx):
 SPLIT_SHAPES = [  # (M, N, K): 16 / 32 / 48 / 64-row tiles, k split in two, ragged M
     (9, 2304, 768), (64, 768, 768), (100, 768, 3072), (256, 2304, 768), (256, 3072, 768),
     (256, 768, 3072), (256, 1024, 768), (300, 768, 768), (1000, 768, 768),
+    # prefill sizes, the tiled kernel: 128-, 64- and 32-row workgroup tiles,
+    # ragged M, K = 3072, the codec's N = 256 / 1024 at K = 256 / 1024
+    (8192, 2304, 768), (8192, 768, 3072), (2000, 768, 768), (4100, 256, 1024),
+    (8192, 1024, 256), (1030, 3072, 768),
 ]
 
 
@@ -233,13 +237,17 @@ def test_linear_split_bf16(ctx, M, N, K):
 
 
 def test_linear_split_rejects_bad_shapes(ctx):
-    """GEMV-sized M, K not a multiple of 128 and misaligned weights are
-    refused before any launch."""
+    """GEMV-sized M, K not a multiple of 128 (decode sizes), N not a
+    multiple of 128 (prefill sizes) and misaligned weights are refused before
+    any launch."""
     with pytest.raises(mb.MbError) as e:
         ctx.linear_split_dev(8, 768, 768, 16, 768, 16, None, 16, 768)  # M <= 8: the GEMV's
     assert e.value.code == mb.MB_ERR_STATE
     with pytest.raises(mb.MbError) as e:
         ctx.linear_split_dev(64, 768, 704, 16, 704, 16, None, 16, 768)  # K % 128 != 0
+    assert e.value.code == mb.MB_ERR_ARG
+    with pytest.raises(mb.MbError) as e:
+        ctx.linear_split_dev(8192, 704, 768, 16, 768, 16, None, 16, 704)  # N % 128 != 0
     assert e.value.code == mb.MB_ERR_ARG
     with pytest.raises(mb.MbError) as e:
         ctx.split_weights_dev(16, 768, 768, 24)  # Wx not 16-byte aligned
