@@ -14,7 +14,9 @@ import os
 import numpy as np
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libmockbird_hip.so")
+# MB_HIP_LIB names another build of the same library (the host-sanitized one
+# of mockbird_amd.build.build_sanitized); there is no other implementation
+LIB_PATH = os.environ.get("MB_HIP_LIB") or os.path.join(PKG, "libmockbird_hip.so")
 
 MB_OK, MB_ERR_ARG, MB_ERR_RANGE, MB_ERR_HIP, MB_ERR_STATE, MB_ERR_CANCELLED, MB_ERR_NOMEM = range(7)
 MB_KV_F32, MB_KV_BF16 = 0, 1

@@ -92,9 +92,79 @@ def build_addon() -> str | None:
     return ADDON
 
 
+ASAN_DIR = os.path.join(PKG, "_asan")
+ASAN_LIB = os.path.join(ASAN_DIR, "libmockbird_hip.so")
+ASAN_ADDON = os.path.join(ASAN_DIR, "engine", "mockbird_hip.node")
+# the runtime both sanitized builds link against (clang's, as hipcc's)
+ASAN_RUNTIME = os.path.join(ROCM, "llvm", "lib", "clang")
+SAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-shared-libasan"]
+
+
+def asan_runtime() -> str | None:
+    """clang's AddressSanitizer runtime (to preload into python / node)."""
+    for path in sorted(glob.glob(os.path.join(ASAN_RUNTIME, "*", "lib", "linux",
+                                              "libclang_rt.asan-x86_64.so"))):
+        return path
+    return None
+
+
+def sanitized_stale() -> bool:
+    """Whether the host-sanitized build is missing or older than a source."""
+    if not (os.path.exists(ASAN_LIB) and os.path.exists(ASAN_ADDON)):
+        return True
+    built = min(os.path.getmtime(ASAN_LIB), os.path.getmtime(ASAN_ADDON))
+    sources = (glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.h")) +
+               glob.glob(os.path.join(CSRC, "napi", "*.cc")) +
+               glob.glob(os.path.join(ROOT, "include", "*.h")))
+    return any(os.path.getmtime(f) > built for f in sources)
+
+
+def build_sanitized(jobs: int = 8) -> tuple[str, str | None]:
+    """The C ABI and the N-API addon with their host code under
+    AddressSanitizer and UndefinedBehaviorSanitizer (the GPU code is built
+    as usual): mockbird_amd/_asan/libmockbird_hip.so and
+    mockbird_amd/_asan/engine/mockbird_hip.node, which links it.  For the
+    CPU tests of the boundary (tests/test_host_sanitized.py); run with
+    clang's ASan runtime preloaded (asan_runtime())."""
+    obj_dir = os.path.join(ASAN_DIR, "_build")
+    os.makedirs(obj_dir, exist_ok=True)
+    flags = [f for f in HIP_FLAGS if f != "-O3"] + ["-O1", "-g", "-fno-omit-frame-pointer"] + SAN_HOST
+    cmds, objs = [], []
+    for src in sorted(glob.glob(os.path.join(CSRC, "*.hip"))):
+        obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
+        objs.append(obj)
+        cmds.append([HIPCC, *flags, "-c", src, "-o", obj])
+    with cf.ThreadPoolExecutor(max_workers=min(jobs, len(cmds))) as ex:
+        list(ex.map(_run, cmds))
+    tmp = ASAN_LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *SAN_HOST, "-o", tmp, *objs,
+          f"-Wl,-rpath,{ROCM}/lib"])
+    os.replace(tmp, ASAN_LIB)
+    src = os.path.join(CSRC, "napi", "mb_napi.cc")
+    node_inc = "/usr/include/node"
+    if not os.path.exists(os.path.join(node_inc, "node_api.h")):
+        return ASAN_LIB, None
+    os.makedirs(os.path.dirname(ASAN_ADDON), exist_ok=True)
+    tmp = ASAN_ADDON + ".tmp"
+    _run([os.path.join(ROCM, "llvm", "bin", "clang++"), "-O1", "-g", "-fPIC", "-shared",
+          "-std=c++17", "-fno-omit-frame-pointer", "-fsanitize=address,undefined",
+          "-fno-sanitize-recover=undefined", "-shared-libasan",
+          # globals uninstrumented: Node 12 registers the addon's module-name
+          # literal with ASan twice and ASan then reports it as misaligned;
+          # heap and stack accesses stay checked
+          "-mllvm", "-asan-globals=0", "-I", node_inc, "-I",
+          os.path.join(ROOT, "include"), src, "-o", tmp, "-L", ASAN_DIR, "-lmockbird_hip",
+          "-Wl,-rpath,$ORIGIN/..", "-Wl,--allow-shlib-undefined"])
+    os.replace(tmp, ASAN_ADDON)
+    return ASAN_LIB, ASAN_ADDON
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--lib-only", action="store_true")
+    ap.add_argument("--sanitized", action="store_true",
+                    help="also build the host-sanitized library and addon (mockbird_amd/_asan)")
     ap.add_argument("-j", type=int, default=8)
     a = ap.parse_args(argv)
     print(build_lib(a.j))
@@ -103,6 +173,8 @@ def main(argv=None) -> int:
         addon = build_addon()
         if addon:
             print(addon)
+    if a.sanitized:
+        print(*build_sanitized(a.j))
     return 0
 
 

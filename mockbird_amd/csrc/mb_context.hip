@@ -121,6 +121,8 @@ int check_cfg(const mb_config& c, std::string& why) {
     snprintf(buf, sizeof buf, "wrap must be 0 or 1, got %d", c.wrap);
   } else if (c.vocab < 0) {
     snprintf(buf, sizeof buf, "vocab %d is negative", c.vocab);
+  } else if (c.device < 0) {
+    snprintf(buf, sizeof buf, "device %d is negative", c.device);
   } else {
     return 0;
   }

@@ -10,10 +10,13 @@ const here = path.dirname(fileURLToPath(import.meta.url));
 
 let cached = null;
 
-/** The addon's exports (create, prefill, decodeStep, localFrame, ...). */
+/**
+ * The addon's exports (create, prefill, decodeStep, localFrame, ...).
+ * MB_HIP_ADDON names another build of the same addon (the host-sanitized one).
+ */
 export function loadNative() {
   if (cached) return cached;
-  const file = path.join(here, "mockbird_hip.node");
+  const file = process.env.MB_HIP_ADDON || path.join(here, "mockbird_hip.node");
   try {
     cached = require(file);
   } catch (error) {

@@ -107,6 +107,24 @@ try {
 } catch (e) {
   errs.badConfig = [e.code, e.message];
 }
+// malformed configurations: every one is refused with a JS error
+errs.createCases = [
+  null, 7, "cfg", {}, { nLayers: "12" }, { nLayers: 2.5 }, { nLayers: NaN }, { capacity: -1 },
+  { maxSeqs: 1e12 }, { kvDtype: 9 }, { wrap: 3 }, { device: -1 }, { nLayers: 2, capacity: 16 },
+].map((cfg) => {
+  try {
+    const h = native.create(cfg);
+    native.destroy(h);  // a GPU host accepts the valid ones
+    return "created";
+  } catch (e) {
+    return e.code || e.name;
+  }
+});
+try {
+  native.destroy({});
+} catch (e) {
+  errs.destroyBad = e.name;
+}
 try {
   native.prefill({}, 1, 1, new Int32Array(17), Int32Array.of(1));
 } catch (e) {

@@ -75,6 +75,16 @@ def test_errors_throw_before_device_calls(report):
     assert e["badHandle"][0] == "TypeError"
     assert e["badHandleAsync"][0] == "TypeError"  # thrown before a Promise is made
     assert e["notImplemented"] == [True, "EngineNotImplemented"]
+    assert e["destroyBad"] == "TypeError"
+    # malformed configurations: non-objects and non-numbers are type errors,
+    # fractional / non-finite / huge numbers range errors, out-of-range values
+    # the library's MB_ERR_ARG; the two valid ones reach the device (no GPU
+    # here: MB_ERR_HIP; a GPU host creates and destroys them)
+    c = e["createCases"]
+    assert c[:3] == ["ERR_INVALID_ARG_TYPE"] * 3 and c[4] == "ERR_INVALID_ARG_TYPE"
+    assert c[5] == c[6] == c[8] == "ERR_OUT_OF_RANGE"
+    assert c[7] == c[9] == c[10] == c[11] == "MB_ERR_ARG"
+    assert c[3] in ("MB_ERR_HIP", "created") and c[12] in ("MB_ERR_HIP", "created")
 
 
 def test_codec_table_resolves_by_shape_and_order(report):
