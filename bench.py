@@ -248,18 +248,92 @@ def run_fused(args, B, C, pos0, seed, workload):
             "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def run_voices_attention(args, B=256, C=1024, frames_in=150):
-    """The KV-attention kernel at the many-voice decode shape: 256 voices,
-    ring capacity 1024; positions are the many-voice prompt lengths
-    U[64, 400) (seed 33) plus `frames_in` decoded frames, so the live windows
-    span 214-549 slots and grow by one per pass over the layers."""
+def voices_positions(B=256, frames_in=150, order="natural"):
+    """The many-voice prompt lengths U[64, 400) (seed 33) plus `frames_in`
+    decoded frames; `order` "desc" / "asc" sorts the voices by position (the
+    same windows, dispatched longest or shortest first)."""
     g = np.random.default_rng(33)
-    pos0 = (g.integers(64, 400, size=B) + frames_in).astype(np.int32)
+    pos = (g.integers(64, 400, size=B) + frames_in).astype(np.int32)
+    if order == "desc":
+        return -np.sort(-pos)
+    return np.sort(pos) if order == "asc" else pos
+
+
+def run_voices_attention(args, B=256, C=1024):
+    """The KV-attention kernel at the many-voice decode shape: 256 voices,
+    ring capacity 1024; positions from voices_positions(), so the live windows
+    span 214-549 slots and grow by one per pass over the layers."""
+    pos0 = voices_positions(B, order=args.voice_order)
     if int(pos0.max()) + (args.warmup + args.steps) // 12 + 2 >= C:
         raise ValueError("positions exceed the ring")
     return run_fused(args, B, C, pos0, 11,
                      "fused ring append + decode attention, 256 voices, 12 x 64, ring 1024, "
                      "bf16 KV, windows 214-549 slots, 12 layer rings in turn")
+
+
+def block_timeline(stamps, window):
+    """Summary of one decode-attention launch's block stamps: rows of
+    {start, end (100 MHz ticks), HW_ID, XCC_ID}, one per block, and each
+    block's live window in slots."""
+    st = stamps.astype(np.int64)
+    window = np.asarray(window, np.float64)
+    t0 = st[:, 0].min()
+    start = (st[:, 0] - t0) * 0.01  # us
+    end = (st[:, 1] - t0) * 0.01
+    dur = end - start
+    cu = st[:, 3] * 256 + ((st[:, 2] >> 8) & 0xFF)
+    ucu, per_cu = np.unique(cu, return_counts=True)
+    busy = np.array([dur[cu == c].sum() for c in ucu])
+    pct = lambda a, qs: {str(q): round(float(np.percentile(a, q)), 2) for q in qs}
+    hist = dict(zip(*np.unique(per_cu, return_counts=True)))
+    # blocks running, and the window's K/V bytes read per microsecond (each
+    # block's window x 64 dims x K,V x 2 bytes spread evenly over its
+    # duration), in 4 us bins over the launch
+    edges = np.arange(0.0, float(end.max()) + 4.0, 4.0)
+    rate = window * HD * 2 * 2 / dur  # bytes per us
+    flight, gbs_t = [], []
+    for lo, hi in zip(edges[:-1], edges[1:]):
+        overlap = np.clip(np.minimum(end, hi) - np.maximum(start, lo), 0.0, None)
+        flight.append(round(float(overlap.sum() / (hi - lo)), 1))
+        gbs_t.append(round(float((overlap * rate).sum() / (hi - lo) / 1e3), 1))
+    return {"blocks": len(st), "span_us": round(float(end.max()), 2),
+            "last_start_us": round(float(start.max()), 2),
+            "block_us": pct(dur, (0, 10, 50, 90, 100)),
+            "block_end_us": pct(end, (10, 50, 90, 99, 100)),
+            "ns_per_window_slot": pct(dur / window * 1e3, (10, 50, 90)),
+            "corr_block_us_window": (round(float(np.corrcoef(dur, window)[0, 1]), 3)
+                                     if dur.std() > 0 and window.std() > 0 else None),
+            "cus": int(len(ucu)), "blocks_per_cu": {str(k): int(v) for k, v in hist.items()},
+            "cu_busy_us": pct(busy, (0, 50, 100)),
+            "mean_blocks_in_flight_per_cu": round(float(busy.mean() / end.max()), 2),
+            "bin_us": 4.0, "blocks_in_flight_by_bin": flight, "window_gbs_by_bin": gbs_t}
+
+
+def run_timeline(args, B=256, C=1024):
+    """Per-block timeline of the 256-voice decode-attention launch: runs the
+    voices leg on the timeline build of the library (ring.hip under
+    MB_BLOCK_TIMELINE, loaded through MB_HIP_LIB), then reads the last
+    launch's stamps: each block's start and end (100 MHz counter) and the CU
+    (XCC_ID, and HW_ID bits 8-15: CU, shader array and engine) that ran it.
+    Reports the launch span, the spread of block starts, block durations and
+    their correlation with the block's window, blocks and busy time per CU."""
+    import ctypes
+
+    import mockbird_amd as mb
+
+    lib = mb.load()
+    if not hasattr(lib, "mb_probe_block_stamps"):
+        raise SystemExit("the timeline leg needs the timeline build: python -m mockbird_amd.build, "
+                         "then MB_HIP_LIB=mockbird_amd/libmockbird_hip_timeline.so")
+    lib.mb_probe_block_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    run = run_voices_attention(args, B, C)
+    n = B * H
+    raw = np.zeros(4 * n, np.uint64)
+    if lib.mb_probe_block_stamps(raw.ctypes.data, n) != 0:
+        raise RuntimeError("mb_probe_block_stamps failed")
+    last = args.warmup + args.steps - 1  # the launch whose stamps survive
+    window = np.repeat(np.minimum(voices_positions(B, order=args.voice_order) + last // H + 1, C), H)
+    return {"launch": run, **block_timeline(raw.reshape(n, 4), window)}
 
 
 def run_c4(args, B=32, C=4096):
@@ -751,9 +825,12 @@ def main():
                          "ceiling: a streaming read probe and torch's sum over 4 GiB), gemm "
                          "(QKV and O projections at M = 8192 and 256), c1 (append + decode "
                          "attention, 64 sequences, C=2048), voices (the same at 256 voices, "
-                         "C=1024), c4 (the same at 32 sequences, C=4096, wrapped), c2 "
+                         "C=1024), timeline (per-block timeline of the voices launch; needs "
+                         "the timeline build through MB_HIP_LIB), c4 (the same at 32 sequences, C=4096, wrapped), c2 "
                          "(prefill attention), codec (codec decoder frames/s at 64 and 256 "
                          "voices), frames (model decode frames/s); the JSON line needs c1")
+    ap.add_argument("--voice-order", default="natural", choices=["natural", "desc", "asc"],
+                    help="voice order of the voices and timeline legs (desc: longest window first)")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     ap.add_argument("--frames-weights", default="f32,bf16",
                     help="weight storage of the frames leg's runs (f32, bf16 or both)")
@@ -774,6 +851,7 @@ def main():
     ceiling = run_read_ceiling() if "ceiling" in legs else None
     gemm = run_gemm() if "gemm" in legs else None
     voices = run_voices_attention(args) if "voices" in legs else None
+    timeline = run_timeline(args) if "timeline" in legs else None
     c4 = run_c4(args) if "c4" in legs else None
     codec = ([run_codec(args, 64, "f32"), run_codec(args, 256, "bf16")]
              if "codec" in legs else None)
@@ -800,10 +878,10 @@ def main():
                           for b in map(int, args.frames_b.split(","))]
     if "c1" not in legs:
         print(json.dumps({"hbm_copy": copy, "hbm_read_ceiling": ceiling, "gemm": gemm,
-                          "kv_attention_256_voices": voices,
+                          "kv_attention_256_voices": voices, "timeline_256_voices": timeline,
                           "kv_attention_c4_wrapped": c4, "prefill_attention": c2,
                           "codec": codec, "frames_detail": frames,
-                          "frames_bf16_weights": frames_w16}), flush=True)
+                          "frames_detail_bf16_weights": frames_w16}), flush=True)
         return 0
     bf16 = run_c1(args, "bf16")
     f32 = run_c1(args, "f32") if args.kv == "both" else None
@@ -853,6 +931,7 @@ def main():
         "hbm_read_ceiling": ceiling,
         "gemm": gemm,
         "kv_attention_256_voices": voices,
+        "timeline_256_voices": timeline,
         "kv_attention_c4_wrapped": c4,
         "prefill_attention": c2,
         "codec": codec,

@@ -2,6 +2,7 @@
 
     python -m mockbird_amd.build            # library + addon
     python -m mockbird_amd.build --lib-only
+    python -m mockbird_amd.build --sanitized  # also the host-sanitized build
 
 hipcc compiles each csrc/*.hip file for gfx950 only; objects go to
 mockbird_amd/_build/ and the shared library to mockbird_amd/libmockbird_hip.so.
@@ -23,6 +24,7 @@ CSRC = os.path.join(PKG, "csrc")
 BUILD = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libmockbird_hip.so")
 PROBE_LIB = os.path.join(PKG, "libmb_probe.so")
+TIMELINE_LIB = os.path.join(PKG, "libmockbird_hip_timeline.so")
 ADDON = os.path.join(PKG, "engine", "mockbird_hip.node")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
@@ -72,6 +74,25 @@ def build_probe() -> str:
     _run([HIPCC, *HIP_FLAGS, "-shared", src, "-o", tmp, f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp, PROBE_LIB)
     return PROBE_LIB
+
+
+def build_timeline() -> str:
+    """libmockbird_hip_timeline.so: the library with ring.hip built under
+    -DMB_BLOCK_TIMELINE=1, so that every decode-attention block records its
+    start and end times and the CU that ran it (mb_probe_block_stamps).  For
+    bench.py's timeline leg only (measurement, loaded through MB_HIP_LIB);
+    links the other objects of build_lib()."""
+    obj = os.path.join(BUILD, "ring.timeline.o")
+    _run([HIPCC, *HIP_FLAGS, "-DMB_BLOCK_TIMELINE=1", "-c", os.path.join(CSRC, "ring.hip"),
+          "-o", obj])
+    objs = [os.path.join(BUILD, os.path.basename(src) + ".o")
+            for src in sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+            if os.path.basename(src) != "ring.hip"]
+    tmp = TIMELINE_LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, obj,
+          f"-Wl,-rpath,{ROCM}/lib"])
+    os.replace(tmp, TIMELINE_LIB)
+    return TIMELINE_LIB
 
 
 def build_addon() -> str | None:
@@ -170,6 +191,7 @@ def main(argv=None) -> int:
     print(build_lib(a.j))
     if not a.lib_only:
         print(build_probe())
+        print(build_timeline())
         addon = build_addon()
         if addon:
             print(addon)

@@ -228,6 +228,20 @@ __device__ __forceinline__ void merge_state(float& m, float& l, float* acc, floa
   m = mn;
 }
 
+// Block timeline (measurement builds only, -DMB_BLOCK_TIMELINE=1): each
+// k_attn_unit block records {start, end} from the 100 MHz s_memrealtime
+// counter and the HW_ID / XCC_ID registers of the CU that ran it, one vector
+// store per word from lane 0 of wave 0, for the first kTimelineBlocks blocks of
+// every launch (the last launch's stamps survive).  The production build
+// compiles none of it.
+#ifndef MB_BLOCK_TIMELINE
+#define MB_BLOCK_TIMELINE 0
+#endif
+#if MB_BLOCK_TIMELINE
+constexpr int kTimelineBlocks = 8192;
+__device__ uint64_t g_block_stamps[4 * kTimelineBlocks];
+#endif
+
 // 16-byte streaming load (global_load_dwordx4 ... nt): the K/V window is read
 // once per launch, and the non-temporal hint lets the caches stream it.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -325,6 +339,9 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
   __shared__ float fold[MAXNW][PART];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#if MB_BLOCK_TIMELINE
+  const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
+#endif
   const int qidx = blockIdx.x / H, head = blockIdx.x % H;
   const int b = qidx / rows, r = qidx % rows;
   if (n_rows && r >= n_rows[b]) return;  // uniform per block
@@ -562,6 +579,19 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   float o = 0.f;
   for (int s = 0; s < nw; s++) o = fmaf(__shfl(w, s), fold[s][lane], o);
   out[row_at(out_rows, b, r) + head * HD + lane] = L > 0.f ? o / L : 0.f;
+#if MB_BLOCK_TIMELINE
+  if (lane == 0 && blockIdx.x < kTimelineBlocks) {
+    uint32_t hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+    uint64_t* st = g_block_stamps + 4 * blockIdx.x;
+    st[0] = t_begin;
+    st[1] = t_end;
+    st[2] = hw;
+    st[3] = xcc;
+  }
+#endif
 }
 
 // Fused append + attention for windows of at most kShortWindow slots in an
@@ -803,3 +833,14 @@ int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv
 }
 
 }  // namespace mb
+
+#if MB_BLOCK_TIMELINE
+// Copies the stamps of the first n blocks ({start, end, HW_ID, XCC_ID} per
+// block) of the last decode-attention launch to host memory.  Exported by the
+// timeline build only.
+extern "C" int mb_probe_block_stamps(uint64_t* host, int n) {
+  if (!host || n < 0 || n > mb::kTimelineBlocks) return -1;
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(mb::g_block_stamps), sizeof(uint64_t) * 4 * n,
+                                  0, hipMemcpyDeviceToHost);
+}
+#endif

@@ -1,0 +1,123 @@
+"""Per-frame kernel breakdown from a rocprofv3 kernel trace.
+
+    python -m mockbird_amd.profile_frames TRACE.csv --delimiter k_frame_emit [--skip 3]
+    python -m mockbird_amd.profile_frames TRACE.csv --delimiter k_codec_head --last 24
+
+TRACE.csv is the `*_kernel_trace.csv` of `rocprofv3 --kernel-trace
+--output-format csv`.  Dispatches are split into runs wherever the GPU sat
+idle for more than `--gap-ms` (set-up between two benchmark runs), and each
+run into frames at the delimiting kernel (the last launch of a frame: the
+decode frame's `k_frame_emit`, the codec frame's `k_codec_head`).  For each
+run the tool prints one markdown table: launches per frame, per-kernel
+launches, mean duration and time per frame, over the frames kept (`--skip`
+drops the first frames as warm-up, `--last` keeps only the last n).  The
+"span" is the time from one delimiter's end to the next one's, the frame's
+wall time on the GPU; under the tracer it includes the tracer's per-launch
+overhead, the kernel time does not.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import re
+import sys
+
+
+def load(path: str) -> list[dict]:
+    rows = list(csv.DictReader(open(path)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return rows
+
+
+def split_runs(rows: list[dict], gap_ns: float) -> list[list[dict]]:
+    runs, cur, last_end = [], [], None
+    for r in rows:
+        s, e = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if last_end is not None and s - last_end > gap_ns and cur:
+            runs.append(cur)
+            cur = []
+        cur.append(r)
+        last_end = e if last_end is None else max(last_end, e)
+    if cur:
+        runs.append(cur)
+    return runs
+
+
+def short_name(name: str) -> str:
+    """Kernel name without its argument list (template arguments kept)."""
+    name = name.replace("(anonymous namespace)::", "")
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            name = name[:i]
+            break
+    return re.sub(r"^void ", "", name).strip()
+
+
+def frames_of(run: list[dict], delimiter: str, skip: int, last: int | None):
+    """[(first index, last index)] of each kept frame: the launches after one
+    delimiter up to and including the next."""
+    ends = [i for i, r in enumerate(run) if delimiter in r["Kernel_Name"]]
+    fr = list(zip(ends[:-1], ends[1:]))
+    fr = fr[skip:]
+    if last is not None:
+        fr = fr[-last:]
+    return fr
+
+
+def breakdown(run: list[dict], frames) -> dict:
+    agg = collections.defaultdict(lambda: [0, 0.0])
+    span = 0.0
+    for a, b in frames:
+        span += (int(run[b]["End_Timestamp"]) - int(run[a]["End_Timestamp"])) / 1e3
+        for r in run[a + 1:b + 1]:
+            k = short_name(r["Kernel_Name"])
+            agg[k][0] += 1
+            agg[k][1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+    n = len(frames)
+    kernels = sorted(((k, c / n, t / c, t / n) for k, (c, t) in agg.items()), key=lambda x: -x[3])
+    total = sum(x[3] for x in kernels)
+    return {"frames": n, "launches": sum(x[1] for x in kernels), "kernel_us": total,
+            "span_us": span / n, "kernels": kernels}
+
+
+def grid_of(run: list[dict], kernel: str) -> str:
+    for r in run:
+        if kernel in r["Kernel_Name"]:
+            return r.get("Grid_Size_X", r.get("Grid_Size", "?"))
+    return "?"
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("trace")
+    ap.add_argument("--delimiter", required=True, help="name of a frame's last kernel")
+    ap.add_argument("--skip", type=int, default=0, help="frames dropped at the start of each run")
+    ap.add_argument("--last", type=int, default=None, help="keep only the last n frames of a run")
+    ap.add_argument("--gap-ms", type=float, default=5.0, help="idle time that separates runs")
+    ap.add_argument("--top", type=int, default=14, help="kernels listed per run")
+    ap.add_argument("--grid-of", default=None,
+                    help="kernel whose grid size is printed per run (to tell runs apart)")
+    a = ap.parse_args(argv)
+    for run in split_runs(load(a.trace), a.gap_ms * 1e6):
+        fr = frames_of(run, a.delimiter, a.skip, a.last)
+        if not fr:
+            continue
+        b = breakdown(run, fr)
+        grid = f", {a.grid_of} grid {grid_of(run, a.grid_of)}" if a.grid_of else ""
+        print(f"\n{b['frames']} frames{grid}: {b['launches']:.0f} launches/frame, kernel time "
+              f"{b['kernel_us']:.1f} us/frame, span {b['span_us']:.1f} us/frame\n")
+        print("| kernel | per frame | avg us | us per frame | share |")
+        print("|---|---:|---:|---:|---:|")
+        for k, c, avg, per in b["kernels"][:a.top]:
+            print(f"| `{k}` | {c:.0f} | {avg:.2f} | {per:.1f} | {100 * per / b['kernel_us']:.1f} % |")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,61 @@
+"""mockbird_amd.profile_frames on a hand-made kernel trace (CPU only): runs
+split at idle gaps, frames cut at the delimiting kernel, warm-up frames
+dropped, per-kernel counts and times per frame."""
+import csv
+import os
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+from mockbird_amd import profile_frames as pf  # noqa: E402
+
+
+def _trace(path):
+    rows, t = [], 0
+    def add(name, dur_us, grid=64, gap_us=1):
+        nonlocal t
+        t += int(gap_us * 1000)
+        rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + int(dur_us * 1000),
+                     "Grid_Size_X": grid})
+        t += int(dur_us * 1000)
+    for run, grid in ((0, 64), (1, 256)):
+        if run:
+            t += 20_000_000  # 20 ms idle: a new run
+        for f in range(5):
+            add("void mb::k_gemm<2, 2, 0>(float const*, long)", 10 + run, grid)
+            add("void mb::k_gemm<2, 2, 0>(float const*, long)", 10 + run, grid)
+            add("mb::k_attn(int)", 30 if f == 0 else 20, grid)
+            add("mb::(anonymous namespace)::k_add_i32(int*, int, int)", 1, grid)
+            add("mb::k_frame_emit(int*)", 2, grid)
+    with open(path, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+
+
+def test_runs_frames_and_breakdown(tmp_path):
+    p = str(tmp_path / "t.csv")
+    _trace(p)
+    runs = pf.split_runs(pf.load(p), 5e6)
+    assert len(runs) == 2 and all(len(r) == 25 for r in runs)
+    fr = pf.frames_of(runs[0], "k_frame_emit", skip=1, last=None)
+    assert len(fr) == 3  # 5 delimiters -> 4 frames after the first, one skipped
+    b = pf.breakdown(runs[0], fr)
+    k = {name: (c, avg, per) for name, c, avg, per in b["kernels"]}
+    assert k["mb::k_gemm<2, 2, 0>"] == (2, 10.0, 20.0)
+    assert k["mb::k_attn"] == (1, 20.0, 20.0)
+    assert k["mb::k_add_i32"] == (1, 1.0, 1.0)
+    assert b["launches"] == 5 and b["kernel_us"] == 43.0
+    assert abs(b["span_us"] - 48.0) < 1e-9  # 43 us of kernels + 5 gaps of 1 us
+    last = pf.breakdown(runs[1], pf.frames_of(runs[1], "k_frame_emit", 0, 2))
+    assert last["frames"] == 2 and dict((n, c) for n, c, _, _ in last["kernels"])["mb::k_gemm<2, 2, 0>"] == 2
+    assert pf.grid_of(runs[1], "k_frame_emit") == "256"
+
+
+def test_cli_prints_a_table_per_run(tmp_path, capsys):
+    p = str(tmp_path / "t.csv")
+    _trace(p)
+    assert pf.main([p, "--delimiter", "k_frame_emit", "--skip", "1", "--grid-of", "k_frame_emit"]) == 0
+    out = capsys.readouterr().out
+    assert out.count("| kernel |") == 2 and "grid 256" in out and "`mb::k_attn` | 1 | 20.00" in out
