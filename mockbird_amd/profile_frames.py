@@ -25,7 +25,8 @@ import sys
 
 
 def load(path: str) -> list[dict]:
-    rows = list(csv.DictReader(open(path)))
+    with open(path, newline="") as fh:
+        rows = list(csv.DictReader(fh))
     rows.sort(key=lambda r: int(r["Start_Timestamp"]))
     return rows
 
