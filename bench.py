@@ -284,6 +284,12 @@ def block_timeline(stamps, window):
     cu = st[:, 3] * 256 + ((st[:, 2] >> 8) & 0xFF)
     ucu, per_cu = np.unique(cu, return_counts=True)
     busy = np.array([dur[cu == c].sum() for c in ucu])
+    busy_window = np.array([window[cu == c].sum() for c in ucu])
+    # placement: the dispatcher's XCC for block b, and whether block b + 256
+    # lands on block b's CU (a fixed round-robin over the CUs)
+    b = np.arange(len(st))
+    xcc_rr = float(np.mean(st[:, 3] == b % 8))
+    same_256 = float(np.mean(cu[:-256] == cu[256:])) if len(st) > 256 else None
     pct = lambda a, qs: {str(q): round(float(np.percentile(a, q)), 2) for q in qs}
     hist = dict(zip(*np.unique(per_cu, return_counts=True)))
     # blocks running, and the window's K/V bytes read per microsecond (each
@@ -305,18 +311,24 @@ def block_timeline(stamps, window):
                                      if dur.std() > 0 and window.std() > 0 else None),
             "cus": int(len(ucu)), "blocks_per_cu": {str(k): int(v) for k, v in hist.items()},
             "cu_busy_us": pct(busy, (0, 50, 100)),
+            "cu_window_slots": pct(busy_window, (0, 50, 100)),
+            "xcc_is_block_mod_8": round(xcc_rr, 4),
+            "cu_of_block_plus_256_same": None if same_256 is None else round(same_256, 4),
             "mean_blocks_in_flight_per_cu": round(float(busy.mean() / end.max()), 2),
             "bin_us": 4.0, "blocks_in_flight_by_bin": flight, "window_gbs_by_bin": gbs_t}
 
 
-def run_timeline(args, B=256, C=1024):
-    """Per-block timeline of the 256-voice decode-attention launch: runs the
-    voices leg on the timeline build of the library (ring.hip under
-    MB_BLOCK_TIMELINE, loaded through MB_HIP_LIB), then reads the last
-    launch's stamps: each block's start and end (100 MHz counter) and the CU
-    (XCC_ID, and HW_ID bits 8-15: CU, shader array and engine) that ran it.
+def run_timeline(args):
+    """Per-block timeline of a fused decode-attention launch, run on the
+    timeline build of the library (ring.hip under MB_BLOCK_TIMELINE, loaded
+    through MB_HIP_LIB): the voices leg's shape (256 voices, ring 1024) or
+    C1's (64 sequences, ring 2048, positions U[1, 6144)), bf16 KV.  Reads the
+    last launch's stamps: each block's start and end (100 MHz counter) and the
+    CU (XCC_ID, and HW_ID bits 8-15: CU, shader array and engine) that ran it.
     Reports the launch span, the spread of block starts, block durations and
-    their correlation with the block's window, blocks and busy time per CU."""
+    their correlation with the block's window, blocks, busy time and window
+    slots per CU, and where the dispatcher placed the blocks;
+    `--timeline-out` also saves the raw stamps and windows (.npz)."""
     import ctypes
 
     import mockbird_amd as mb
@@ -326,14 +338,24 @@ def run_timeline(args, B=256, C=1024):
         raise SystemExit("the timeline leg needs the timeline build: python -m mockbird_amd.build, "
                          "then MB_HIP_LIB=mockbird_amd/libmockbird_hip_timeline.so")
     lib.mb_probe_block_stamps.argtypes = [ctypes.c_void_p, ctypes.c_int]
-    run = run_voices_attention(args, B, C)
+    if args.timeline_shape == "c1":
+        B, C = 64, 2048
+        pos0 = c1_positions(B)
+        run = run_fused(args, B, C, pos0, 17, "fused ring append + decode attention, 64 sequences, "
+                        "12 x 64, ring 2048, bf16 KV, positions U[1,6144), 12 layer rings in turn")
+    else:
+        B, C = 256, 1024
+        pos0 = voices_positions(B, order=args.voice_order)
+        run = run_voices_attention(args, B, C)
     n = B * H
     raw = np.zeros(4 * n, np.uint64)
     if lib.mb_probe_block_stamps(raw.ctypes.data, n) != 0:
         raise RuntimeError("mb_probe_block_stamps failed")
     last = args.warmup + args.steps - 1  # the launch whose stamps survive
-    window = np.repeat(np.minimum(voices_positions(B, order=args.voice_order) + last // H + 1, C), H)
-    return {"launch": run, **block_timeline(raw.reshape(n, 4), window)}
+    window = np.repeat(np.minimum(pos0 + last // H + 1, C), H)
+    if args.timeline_out:
+        np.savez(args.timeline_out, stamps=raw.reshape(n, 4), window=window)
+    return {"shape": args.timeline_shape, "launch": run, **block_timeline(raw.reshape(n, 4), window)}
 
 
 def run_c4(args, B=32, C=4096):
@@ -831,6 +853,9 @@ def main():
                          "voices), frames (model decode frames/s); the JSON line needs c1")
     ap.add_argument("--voice-order", default="natural", choices=["natural", "desc", "asc"],
                     help="voice order of the voices and timeline legs (desc: longest window first)")
+    ap.add_argument("--timeline-shape", default="voices", choices=["voices", "c1"],
+                    help="launch shape of the timeline leg")
+    ap.add_argument("--timeline-out", default=None, help="the timeline leg's raw stamps (.npz)")
     ap.add_argument("--frames-b", default="1,64,256", help="voice counts of the frames leg")
     ap.add_argument("--frames-weights", default="f32,bf16",
                     help="weight storage of the frames leg's runs (f32, bf16 or both)")

@@ -742,11 +742,13 @@ __global__ __launch_bounds__(256) void k_attn_short(
 // wave per 820 slots, at most MAXNW.  With alternating batches, measured on
 // one MI355X with the fused launch (fractions of 8 TB/s, same GPU per row):
 //   - 64 sequences, C = 2048, mixed windows, bf16, 4-load batches: 4 waves
-//     0.76, 3 waves 0.72, 2 waves 0.68, 8 waves 0.68;
+//     0.76, 5 waves 0.72, 6 waves 0.65, 3 waves 0.72, 2 waves 0.68, 8 waves
+//     0.68; 8-load batches at 4 waves 0.72 (127 VGPRs against 94: fewer
+//     waves resident);
 //   - 256 voices, C = 1024, windows 215-550, bf16, 8-load batches: 4 waves
 //     0.71, 3 waves 0.70, 6 waves 0.64; 4-load batches 0.69-0.70;
 //   - 32 sequences, C = 4096, full windows, bf16, 4-load batches: 5 waves
-//     0.71, 2 waves 0.46;
+//     0.71, 2 waves 0.46; 8-load batches 0.70 against 0.75 (same GPU);
 //   - 64 sequences, C = 2048, fp32, 12-load batches: 4 waves 0.78 (8-load
 //     0.77).
 // Windows up to this many slots run the bf16 kernel with 8-load batches.
