@@ -10,9 +10,10 @@
 //  - the projections are one GEMM each over B x positions rows, with the
 //    layer-scale residual add and the GELU fused into their epilogues;
 //  - a layer appends the frame's positions to its ring and then attends to
-//    them in one pass over the window (k_attn_window: the window split
-//    across the waves of a workgroup, all of the chunk's queries per wave).
-//    Position i of the chunk
+//    them in one pass over the window, in one launch (k_attn_window: each
+//    (voice, head) workgroup ropes and stores its head's new rows, then its
+//    waves take the window's slot groups in turn, all of the chunk's queries
+//    per wave).  Position i of the chunk
 //    must not see i + 1 ..; the window rule (stored position <= cur) gives
 //    that, and each ring holds its window plus one frame of positions, so an
 //    append never overwrites a position that an earlier query of the same
@@ -76,8 +77,8 @@ struct CodecState {
   int32_t* slot_pos = nullptr;
   int32_t* pos = nullptr;   // [4][max_voices]: the next absolute position of each stage
   int32_t* nrow = nullptr;  // [4][max_voices]: positions per frame of each stage
-  float *acc = nullptr, *x = nullptr, *h = nullptr, *qkv = nullptr, *q = nullptr,
-        *att = nullptr, *ffn = nullptr, *wide = nullptr;
+  float *acc = nullptr, *x = nullptr, *h = nullptr, *qkv = nullptr, *att = nullptr,
+        *ffn = nullptr, *wide = nullptr;
   int32_t* frame = nullptr;  // the frame a decode call is at (device counter)
   std::vector<void*> owned;
   // one captured frame of mb_codec_decode_dev and what it was captured for
@@ -407,9 +408,7 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
         return r ? r : launch_gemm(ctx, EPI_GELU_ERF, cs.h, kD, w.f1, kFfn, kD, nullptr, cs.ffn, kFfn, M);
       };
       if ((rc = qkv_proj()) ||
-          (rc = launch_ring_write(ctx, ring, B, n, cs.qkv, MB_DT_F32, dense_rows(3 * kD, n), pos,
-                                  nrow, cs.q, MB_DT_F32, dense_rows(kD, n))) ||
-          (rc = launch_window_attention(ctx, ring, B, n, cs.q, dense_rows(kD, n), pos, nrow,
+          (rc = launch_window_attention(ctx, ring, B, n, cs.qkv, dense_rows(3 * kD, n), pos, nrow,
                                         cs.att, dense_rows(kD, n))) ||
           (rc = x3 ? launch_gemm_x3(ctx, EPI_SCALE_ADD, cs.att, kD, w.o_x, kD, kD, w.s1, cs.x, kD,
                                       M, nullptr, nullptr)
@@ -502,13 +501,12 @@ extern "C" int mb_codec_init(mb_ctx* ctx, const mb_codec_config* cfg) {
   cs->x = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
   cs->h = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
   cs->qkv = (float*)dev_alloc(ctx, *cs, (size_t)rows * 3 * kD * 4);
-  cs->q = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
   cs->att = (float*)dev_alloc(ctx, *cs, (size_t)rows * kD * 4);
   cs->ffn = (float*)dev_alloc(ctx, *cs, (size_t)rows * kFfn * 4);
   cs->wide = (float*)dev_alloc(ctx, *cs, (size_t)rows * kRvqOut * 4);
   for (void* p : {cs->ring_k, cs->ring_v, (void*)cs->slot_pos, (void*)cs->pos, (void*)cs->nrow,
                   (void*)cs->frame,
-                  (void*)cs->acc, (void*)cs->x, (void*)cs->h, (void*)cs->qkv, (void*)cs->q,
+                  (void*)cs->acc, (void*)cs->x, (void*)cs->h, (void*)cs->qkv,
                   (void*)cs->att, (void*)cs->ffn, (void*)cs->wide})
     if (!p) {
       codec_free(ctx);

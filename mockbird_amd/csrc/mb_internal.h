@@ -282,11 +282,13 @@ int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv
 int launch_prefill_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
                              const void* q, int q_dtype, const Rows& q_rows, const int32_t* pos0,
                              const int32_t* n_rows, float* out, const Rows& out_rows);
-// Chunks of up to 32 consecutive fp32 queries per sequence against long
-// windows (the codec's stages), out of the causal windowed rule.
-int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const float* q,
-                            const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
-                            float* out, const Rows& out_rows);
+// Chunks of up to 32 consecutive rows per sequence against long windows
+// (the codec's stages), out of the causal windowed rule: qkv holds the fused
+// fp32 rows (q | k | v, ring.heads x 64 each); every row is roped and written
+// into the ring as launch_ring_write writes it, then its query attends.
+int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
+                            const float* qkv, const Rows& qkv_rows, const int32_t* pos0,
+                            const int32_t* n_rows, float* out, const Rows& out_rows);
 int launch_fill_i32(mb_ctx* ctx, int32_t* p, int64_t n, int32_t value);
 int launch_fill_kv(mb_ctx* ctx, void* p, int64_t n, float value);
 

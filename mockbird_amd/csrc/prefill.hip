@@ -21,6 +21,7 @@
 #include "kv_types.h"
 #include "lds_dma.h"
 #include "mb_internal.h"
+#include "rope.h"
 
 namespace mb {
 
@@ -654,13 +655,14 @@ __global__ __launch_bounds__(256) void k_flash_f32(
 // visible to a query at cur iff 0 <= cur - p < W.
 template <bool KV_BF16, int QB, int NW>
 __global__ __launch_bounds__(64 * NW) void k_attn_window(
-    const float* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
-    const int32_t* __restrict__ n_rows, const void* __restrict__ ring_k,
-    const void* __restrict__ ring_v, const int32_t* __restrict__ slot_pos,
-    int64_t ring_seq_stride, int C, int W, float* __restrict__ out, Rows out_rows) {
+    const float* __restrict__ qkv, Rows qkv_rows, const int32_t* __restrict__ pos0,
+    const int32_t* __restrict__ n_rows, void* __restrict__ ring_k, void* __restrict__ ring_v,
+    int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C, int W, int wrap,
+    const float2* __restrict__ rope_tab, float* __restrict__ out, Rows out_rows) {
   constexpr int NQ = 16 * QB;
   __shared__ float red_ml[NW][2][NQ];        // per wave: max (log2 units), sum
   __shared__ float red_acc[NW][NQ][HD + 1];  // per wave: unnormalised output
+  __shared__ __align__(16) float q_l[NQ][HD];  // the chunk's roped q rows (this head)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qc = lane & 15, g = lane >> 4;
   const int h = blockIdx.x, b = blockIdx.y;
@@ -710,7 +712,52 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
     }
   };
 
-  // the wave's first group is in flight while q is loaded and split
+  // The chunk's rows enter the ring first, as k_ring_write writes them but
+  // for this head only: thread (r, d0) ropes q and k of row r's dims d0 ..
+  // d0 + 7 at position p0 + r, stores K and V at slot pos mod C (only the
+  // last C rows of a call longer than C) and keeps q in LDS; every head's
+  // workgroup records the slots' positions (the same values), so each reads
+  // only what it wrote itself once the barrier below has passed.
+  {
+    const int Dw = (int)gridDim.x * HD;  // width of each of q, k, v in a fused row
+    for (int t = threadIdx.x; t < NQ * 8; t += 64 * NW) {
+      const int r = t >> 3, d0 = (t & 7) * 8;
+      const int64_t p64 = p0 + r;
+      const bool ok = r < n && p64 >= 0 && p64 <= INT32_MAX && (wrap || p64 < C);
+      float qo[8], ko[8], vv[8];
+      if (ok) {
+        const int32_t pos = (int32_t)p64;
+        float qi[8], ki[8];
+        const int64_t roff = row_at(qkv_rows, b, r) + h * HD + d0;
+        load8<false>(qkv, roff, qi);
+        load8<false>(qkv, roff + Dw, ki);
+        load8<false>(qkv, roff + 2 * Dw, vv);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          float c, sn;
+          rope_cs(rope_tab, pos, (d0 >> 1) + j, c, sn);
+          rope_pair(qi[2 * j], qi[2 * j + 1], c, sn, qo[2 * j], qo[2 * j + 1]);
+          rope_pair(ki[2 * j], ki[2 * j + 1], c, sn, ko[2 * j], ko[2 * j + 1]);
+        }
+        if (!(n > C && r < n - C)) {
+          const int slot = wrap ? (int)(p64 % C) : (int)p64;
+          const int64_t koff = (int64_t)b * ring_seq_stride + ((int64_t)h * C + slot) * HD + d0;
+          store8<KV_BF16>(ring_k, koff, ko);
+          store8<KV_BF16>(ring_v, koff, vv);
+          if (d0 == 0) slot_pos[(int64_t)b * C + slot] = pos;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; e++) qo[e] = 0.f;
+      }
+      *(float4*)&q_l[r][d0] = make_float4(qo[0], qo[1], qo[2], qo[3]);
+      *(float4*)&q_l[r][d0 + 4] = make_float4(qo[4], qo[5], qo[6], qo[7]);
+    }
+  }
+  __threadfence_block();
+  __syncthreads();  // the rows are in the ring and q in LDS for every wave
+
+  // the wave's first group is in flight while q is split
   Raw cur, nxt;
   if (wave < groups) load_group(wave, cur);
   // Positions relative to the sequence's first query, clamped so the window
@@ -724,11 +771,10 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
   for (int qb = 0; qb < QB; qb++) {
     const int r = qb * 16 + qc;
     crel[qb] = r < n ? r : -kFar;
-    const float* qp = q + (r < n ? row_at(q_rows, b, r) : 0) + h * HD;
 #pragma unroll
     for (int i = 0; i < 16; i += 4) {
       const int dim = KV_BF16 ? (i >> 3) * 32 + g * 8 + (i & 7) : g * 16 + i;
-      const float4 t = r < n ? *(const float4*)(qp + dim) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 t = r < n ? *(const float4*)&q_l[r][dim] : make_float4(0.f, 0.f, 0.f, 0.f);
       qv[qb][i] = t.x; qv[qb][i + 1] = t.y; qv[qb][i + 2] = t.z; qv[qb][i + 3] = t.w;
     }
   }
@@ -899,11 +945,12 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
   }
 }
 
-// Chunks of up to 32 consecutive fp32 queries per sequence against a ring
-// (the codec's stages); rows_max bounds n_rows.
-int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const float* q,
-                            const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows,
-                            float* out, const Rows& out_rows) {
+// Chunks of up to 32 consecutive rows per sequence (the codec's stages):
+// each row's K/V enters the ring and its query attends the window in one
+// launch; rows_max bounds n_rows.
+int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_max,
+                            const float* qkv, const Rows& qkv_rows, const int32_t* pos0,
+                            const int32_t* n_rows, float* out, const Rows& out_rows) {
   if (rows_max < 1 || rows_max > 32)
     return fail(ctx, MB_ERR_ARG, "window attention takes 1..32 rows per sequence, not %d", rows_max);
   if (B > 65535) return fail(ctx, MB_ERR_ARG, "at most 65535 sequences per call");
@@ -911,9 +958,9 @@ int launch_window_attention(mb_ctx* ctx, const RingView& ring, int B, int rows_m
   constexpr int NW = 8;
   const dim3 grid((unsigned)ring.heads, (unsigned)B);
 #define MB_WIN(BF, QB)                                                                            \
-  hipLaunchKernelGGL((k_attn_window<BF, QB, NW>), grid, dim3(64 * NW), 0, ctx->stream, q, q_rows, \
-                     pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C, ring.window, \
-                     out, out_rows)
+  hipLaunchKernelGGL((k_attn_window<BF, QB, NW>), grid, dim3(64 * NW), 0, ctx->stream, qkv,      \
+                     qkv_rows, pos0, n_rows, ring.k, ring.v, ring.sp, ring.seq_stride, ring.C,   \
+                     ring.window, ring.wrap, ctx->rope_tab, out, out_rows)
   if (ring.bf16) {
     if (rows_max <= 16) MB_WIN(true, 1); else MB_WIN(true, 2);
   } else {
