@@ -92,7 +92,7 @@ struct CodecState {
 
 namespace {
 
-int positions(int s) { return 4 << s; }
+__host__ __device__ constexpr int positions(int s) { return 4 << s; }
 
 // ------------------------------------------------------------------ kernels
 
@@ -155,9 +155,17 @@ __global__ __launch_bounds__(256) void k_codec_head(const float* __restrict__ la
       latent[((int64_t)b * kMaxPos + pos) * kD + c * 120 + j];
 }
 
-__global__ void k_add_i32(int32_t* __restrict__ p, int n, int32_t v) {
+// The end of a frame: every stage's positions advance by its positions per
+// frame for voices b < B (pos [4][V]; each stage's layers read only their
+// own stage's positions, so all four move here, once the frame's last stage
+// has run), and the frame counter by one.
+__global__ void k_frame_advance(int32_t* __restrict__ pos, int V, int B, int32_t* __restrict__ frame) {
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) p[i] += v;
+  if (i < B) {
+#pragma unroll
+    for (int s = 0; s < kStages; s++) pos[(int64_t)s * V + i] += positions(s);
+  }
+  if (i == 0) *frame += 1;
 }
 
 // ------------------------------------------------------------------ helpers
@@ -422,14 +430,12 @@ int codec_frame(mb_ctx* ctx, int B, const int32_t* codes, float* pcm, int64_t T)
     const int out_w = s == kStages - 1 ? kD : kRvqOut;
     if ((rc = launch_gemm(ctx, EPI_STORE, cs.x, kD, st.out_proj, out_w, kD, nullptr, cs.wide, out_w, M)))
       return rc;
-    hipLaunchKernelGGL(k_add_i32, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, ctx->stream, pos,
-                       B, n);
-    MB_HIP(ctx, hipGetLastError());
     in_w = 384;
   }
   hipLaunchKernelGGL(k_codec_head, dim3((unsigned)(((int64_t)B * 2 * kSamples + 255) / 256)),
                      dim3(256), 0, ctx->stream, cs.wide, B, cs.frame, T, pcm);
-  hipLaunchKernelGGL(k_add_i32, dim3(1), dim3(256), 0, ctx->stream, cs.frame, 1, 1);
+  hipLaunchKernelGGL(k_frame_advance, dim3((unsigned)((B + 255) / 256)), dim3(256), 0, ctx->stream,
+                     cs.pos, V, B, cs.frame);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }
