@@ -131,6 +131,17 @@ int mb_ring_poison(mb_ctx* ctx, int layer, int seq, int n_slots, float sentinel)
 int mb_read_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, float* k, float* v,
                  int32_t* slot_pos);
 
+/* The inverse of mb_read_ring: store k, v [n][768] fp32 (rounded to nearest
+ * even bf16 for bf16 rings) and slot_pos[n] into slots [slot0, slot0+n) of
+ * (layer, seq).  A NULL input leaves that part of the slots as it is.  Every
+ * position must be -1 (empty) or one the ring itself puts in that slot (pos
+ * mod C; pos itself on a non-wrapping ring), else MB_ERR_ARG and nothing is
+ * written.  With mb_read_ring it dumps and reloads a prefilled cache, as the
+ * reference's oracle does with its prefill cache file
+ * (tools/onnx-probe/ref-decode.mjs:327-372). */
+int mb_write_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, const float* k,
+                  const float* v, const int32_t* slot_pos);
+
 /* Append one row per sequence b < B at absolute position pos[b]: q is roped
  * into q_out[b][768], K = rope(k) and V = v are stored at slot pos mod C of
  * `layer`, and the slot records pos.  qkv is [B][2304].

@@ -32,7 +32,7 @@ D, H, HD, QKV, FFN, NVQ, ROW, PAD, CODES = 768, 12, 64, 2304, 3072, 16, 17, 1024
 EXPORTS = (
     "mb_abi_version", "mb_create", "mb_destroy", "mb_last_error", "mb_set_stream",
     "mb_get_stream", "mb_synchronize", "mb_device_bytes", "mb_upload_tensor", "mb_cancel",
-    "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_ring_append", "mb_ring_write_rows",
+    "mb_ring_reset", "mb_ring_poison", "mb_read_ring", "mb_write_ring", "mb_ring_append", "mb_ring_write_rows",
     "mb_decode_attention", "mb_prefill_attention", "mb_ring_append_dev",
     "mb_ring_write_rows_dev", "mb_decode_attention_dev", "mb_prefill_attention_dev",
     "mb_set_local_head", "mb_set_penalty_precision", "mb_set_weight_storage", "mb_prefill", "mb_prefill_rows", "mb_decode_step", "mb_local_frame",
@@ -99,6 +99,7 @@ def load():
         "mb_ring_reset": ([_vp, C.c_int, _vp], C.c_int),
         "mb_ring_poison": ([_vp, C.c_int, C.c_int, C.c_int, _f32], C.c_int),
         "mb_read_ring": ([_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
+        "mb_write_ring": ([_vp, C.c_int, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_ring_append": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
         "mb_ring_write_rows": ([_vp, C.c_int, C.c_int, C.c_int, _vp, _vp, _vp, _vp], C.c_int),
         "mb_decode_attention": ([_vp, C.c_int, C.c_int, _vp, _vp, _vp], C.c_int),
@@ -240,6 +241,23 @@ class Context:
         self.check(self.lib.mb_read_ring(self.h, layer, seq, slot0, n, k.ctypes.data, v.ctypes.data,
                                          sp.ctypes.data))
         return k, v, sp
+
+    def write_ring(self, layer: int, seq: int, slot0: int = 0, k=None, v=None, slot_pos=None):
+        """Store k, v [n][768] and slot_pos [n] (any may be None) into slots
+        [slot0, slot0 + n): the inverse of read_ring."""
+        parts = [x for x in (k, v, slot_pos) if x is not None]
+        if not parts:
+            return
+        n = len(parts[0])
+        k = None if k is None else _f32c(k).reshape(n, D)
+        v = None if v is None else _f32c(v).reshape(n, D)
+        sp = None if slot_pos is None else _i32c(slot_pos).reshape(n)
+        if any(len(x) != n for x in (k, v, sp) if x is not None):
+            raise ValueError("k, v and slot_pos cover different numbers of slots")
+        self.check(self.lib.mb_write_ring(self.h, layer, seq, slot0, n,
+                                          None if k is None else k.ctypes.data,
+                                          None if v is None else v.ctypes.data,
+                                          None if sp is None else sp.ctypes.data))
 
     def ring_append(self, layer: int, qkv: np.ndarray, pos) -> np.ndarray:
         qkv, pos = _f32c(qkv), _i32c(pos)

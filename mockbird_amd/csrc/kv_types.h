@@ -9,8 +9,8 @@
 
 namespace mb {
 
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __builtin_bit_cast(uint32_t, f);
   if ((u & 0x7f800000u) == 0x7f800000u) {  // inf / nan: keep, quiet the nan
     const uint32_t nan = (u & 0x007fffffu) ? 0x0040u : 0u;
     return (uint16_t)((u >> 16) | nan);

@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstring>
 
+#include "kv_types.h"
 #include "mb_internal.h"
 
 namespace mb {
@@ -407,6 +408,56 @@ int mb_read_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, float* k, fl
   if (slot_pos) {
     MB_HIP(ctx, hipMemcpyAsync(slot_pos, ctx->slot_pos + slot_base(ctx, layer, seq) + slot0,
                                (size_t)n * 4, hipMemcpyDeviceToHost, ctx->stream));
+    MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  }
+  return MB_OK;
+}
+
+int mb_write_ring(mb_ctx* ctx, int layer, int seq, int slot0, int n, const float* k,
+                  const float* v, const int32_t* slot_pos) {
+  MB_DEVICE_GUARD(ctx);
+  int rc = check_common(ctx, layer, 0);
+  if (rc) return rc;
+  const int C = ctx->cfg.capacity;
+  if (seq < 0 || seq >= ctx->cfg.max_seqs || slot0 < 0 || n < 0 || slot0 + n > C)
+    return fail(ctx, MB_ERR_ARG, "mb_write_ring: seq %d slots [%d, %d) out of range", seq, slot0,
+                slot0 + n);
+  if (n == 0) return MB_OK;
+  // Every stored position must be one the ring's own writes could have left
+  // in that slot: empty (-1), or pos mod C (pos itself on a non-wrapping ring).
+  if (slot_pos)
+    for (int i = 0; i < n; i++) {
+      const int32_t p = slot_pos[i], s = slot0 + i;
+      const bool ok = p == -1 || (p >= 0 && (ctx->cfg.wrap ? p % C == s : p == s));
+      if (!ok)
+        return fail(ctx, MB_ERR_ARG, "mb_write_ring: position %d cannot sit in slot %d of a "
+                    "%s ring of %d slots", p, s, ctx->cfg.wrap ? "wrapping" : "non-wrapping", C);
+    }
+  const size_t e = kv_elem_bytes(ctx);
+  std::vector<uint8_t> host((size_t)H * n * HD * e);
+  for (int which = 0; which < 2; which++) {
+    const float* src = which == 0 ? k : v;
+    if (!src) continue;
+    // reference [slot][head*64 + dim] -> device [head][slot][dim]
+    for (int h = 0; h < H; h++)
+      for (int s = 0; s < n; s++)
+        for (int d = 0; d < HD; d++) {
+          const size_t i = ((size_t)h * n + s) * HD + d;
+          const float f = src[(size_t)s * D + h * HD + d];
+          if (e == 2) ((uint16_t*)host.data())[i] = f32_to_bf16(f);  // the kernels' rounding
+          else ((float*)host.data())[i] = f;
+        }
+    char* dst = (char*)(which == 0 ? ctx->ring_k : ctx->ring_v);
+    for (int h = 0; h < H; h++) {
+      const int64_t off = ring_base(ctx, layer, seq) + ((int64_t)h * C + slot0) * HD;
+      MB_HIP(ctx, hipMemcpyAsync(dst + off * e, host.data() + (size_t)h * n * HD * e,
+                                 (size_t)n * HD * e, hipMemcpyHostToDevice, ctx->stream));
+    }
+    MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  }
+  if (slot_pos) {
+    MB_HIP(ctx, hipMemcpyAsync(ctx->slot_pos + slot_base(ctx, layer, seq) + slot0, slot_pos,
+                               (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
     MB_HIP(ctx, hipStreamSynchronize(ctx->stream));
   }
   return MB_OK;

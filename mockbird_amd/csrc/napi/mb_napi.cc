@@ -576,6 +576,28 @@ napi_value ReadRing(napi_env env, napi_callback_info info) {
   return o;
 }
 
+// writeRing(h, layer, seq, slot0, n, key[n*768] | null, value[n*768] | null,
+// slotPos[n] | null): the inverse of readRing; a null part is left as it is
+napi_value WriteRing(napi_env env, napi_callback_info info) {
+  Args a(env, info);
+  mb_ctx* ctx = get_ctx(env, a.at(0));
+  if (!ctx) return nullptr;
+  int layer, seq, slot0, n;
+  if (!get_int(env, a.at(1), &layer, "layer") || !get_int(env, a.at(2), &seq, "seq") ||
+      !get_int(env, a.at(3), &slot0, "slot0") || !get_int(env, a.at(4), &n, "n"))
+    return nullptr;
+  if (n < 0) return throw_range(env, "n must be >= 0");
+  float *k, *v;
+  int32_t* sp;
+  if (!get_array(env, a.at(5), napi_float32_array, (int64_t)n * kD, &k, nullptr, "key", true) ||
+      !get_array(env, a.at(6), napi_float32_array, (int64_t)n * kD, &v, nullptr, "value", true) ||
+      !get_array(env, a.at(7), napi_int32_array, n, &sp, nullptr, "slotPos", true))
+    return nullptr;
+  int rc = mb_write_ring(ctx, layer, seq, slot0, n, k, v, sp);
+  if (rc) return throw_status(env, ctx, rc);
+  return undef(env);
+}
+
 // ringAppend(h, layer, B, qkv Float32Array[B*2304], pos Int32Array[B]) -> q Float32Array[B*768]
 napi_value RingAppend(napi_env env, napi_callback_info info) {
   Args a(env, info);
@@ -879,6 +901,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"clearSeen", SeqListCall<mb_clear_seen>},
       {"ringPoison", RingPoison},
       {"readRing", ReadRing},
+      {"writeRing", WriteRing},
       {"ringAppend", RingAppend},
       {"ringWriteRows", RingWriteRows},
       {"decodeAttention", DecodeAttention},

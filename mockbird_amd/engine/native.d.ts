@@ -40,6 +40,16 @@ export interface Native {
     slot0: number,
     n: number,
   ): { key: Float32Array; value: Float32Array; slotPos: Int32Array };
+  writeRing(
+    h: NativeHandle,
+    layer: number,
+    seq: number,
+    slot0: number,
+    n: number,
+    key: Float32Array | null,
+    value: Float32Array | null,
+    slotPos: Int32Array | null,
+  ): void;
   ringAppend(h: NativeHandle, layer: number, B: number, qkv: Float32Array, pos: Int32Array): Float32Array;
   ringWriteRows(
     h: NativeHandle,

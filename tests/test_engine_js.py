@@ -14,7 +14,7 @@ ADDON = os.path.join(ROOT, "mockbird_amd", "engine", "mockbird_hip.node")
 BINDINGS = {
     "KV", "abiVersion", "cancel", "clearSeen", "create", "decodeAttention", "decodeFrames",
     "decodeStep", "destroy", "deviceBytes", "lastError", "localFrame", "localSteps", "prefill",
-    "prefillAttention", "readRing", "ringAppend", "ringPoison", "ringReset", "ringWriteRows",
+    "prefillAttention", "readRing", "writeRing", "ringAppend", "ringPoison", "ringReset", "ringWriteRows",
     "setLocalHead", "setWeightStorage", "setPenaltyPrecision", "uploadTensor", "codecInit", "codecReset", "codecDecode",
     "prefillAsync", "decodeStepAsync", "localFrameAsync", "decodeFramesAsync", "codecDecodeAsync",
 }
