@@ -69,8 +69,9 @@ def attn_bytes(pos, C, e):
 
 
 def append_bytes(B, e):
-    """q | k | v read (fp32), roped q written (fp32), K and V written (e bytes)."""
-    return B * (QKV * 4 + D * 4 + 2 * D * e)
+    """q | k | v read (fp32), roped q written (fp32), K and V written (e bytes),
+    the slot's position written (4 bytes)."""
+    return B * (QKV * 4 + D * 4 + 2 * D * e + 4)
 
 
 def fused_bytes(pos, C, e):
@@ -127,7 +128,7 @@ def run_c1(args, kv_name):
     are stepped in turn and every sequence advances one position after each
     pass over the twelve.  The same steps through the two separate entry
     points (mb_ring_append_dev, then mb_decode_attention_dev) are timed beside
-    it on a shorter run."""
+    it on a shorter run, and then the append alone (mb_ring_append_dev)."""
     import torch
 
     import mockbird_amd as mb
@@ -153,7 +154,7 @@ def run_c1(args, kv_name):
             ctx.ring_write_rows_dev(layer, B, chunk, qkv.data_ptr(), p0.data_ptr(), n.data_ptr(), 0)
     torch.cuda.synchronize()
     unfused_steps = min(args.steps, 240)
-    total = args.warmup + args.steps + 2 + unfused_steps
+    total = args.warmup + args.steps + 2 * (2 + unfused_steps)
     tokens = total // L + 2
     pos_all = torch.from_numpy((pos0[None, :] + np.arange(tokens)[:, None]).astype(np.int32)).to(dev)
     qkv_l = [torch.randn((B, QKV), generator=tg, device=dev) for _ in range(L)]
@@ -172,9 +173,30 @@ def run_c1(args, kv_name):
         ctx.ring_append_dev(layer, B, qkv_l[layer].data_ptr(), p.data_ptr(), q.data_ptr())
         ctx.decode_attention_dev(layer, B, q.data_ptr(), p.data_ptr(), max_pos, out.data_ptr())
 
+    def step_append(s):
+        layer, tok = s % L, s // L
+        ctx.ring_append_dev(layer, B, qkv_l[layer].data_ptr(), pos_all[tok].data_ptr(), q.data_ptr())
+
     prime_rings(ctx, L, B, pos0, max_pos)
     ms_total = timed_launches(stream, step, 0, args.warmup, args.steps)
     ms_unfused = timed_launches(stream, step_unfused, args.warmup + args.steps, 2, unfused_steps)
+    ms_append = timed_launches(stream, step_append, args.warmup + args.steps + 2 + unfused_steps, 2,
+                               unfused_steps)
+    # the same kernel at a prefill chunk's size (192 rows per voice; the ring
+    # fills above use 256-row launches, so a trace tells the two apart),
+    # where its bytes rather than its launch set the time; written at
+    # positions past every step above, after them
+    R, n_chunks = 192, 24
+    qkv_c = torch.randn((B, R, QKV), generator=tg, device=dev)
+    q_c = torch.empty((B, R, D), device=dev)
+    p0_c = torch.from_numpy((pos0 + tokens).astype(np.int32)).to(dev)
+    n_c = torch.full((B,), R, dtype=torch.int32, device=dev)
+
+    def step_chunk(s):
+        ctx.ring_write_rows_dev(s % L, B, R, qkv_c.data_ptr(), p0_c.data_ptr(), n_c.data_ptr(),
+                                q_c.data_ptr())
+
+    ms_chunk = timed_launches(stream, step_chunk, 0, 2, n_chunks)
 
     def mean_bytes(fn, first, n):
         tot = 0
@@ -193,6 +215,12 @@ def run_c1(args, kv_name):
         "gbs": b_fused / (ms_step * 1e-3) / 1e9,
         "unfused_ms_per_step": ms_unfused / unfused_steps,
         "unfused_gbs": b_unfused / (ms_unfused / unfused_steps * 1e-3) / 1e9,
+        "append_ms_per_step": ms_append / unfused_steps,
+        "append_bytes_per_step": append_bytes(B, e),
+        "append_gbs": append_bytes(B, e) / (ms_append / unfused_steps * 1e-3) / 1e9,
+        "chunk_ms_per_launch": ms_chunk / n_chunks,
+        "chunk_bytes_per_launch": append_bytes(B * R, e),
+        "chunk_gbs": append_bytes(B * R, e) / (ms_chunk / n_chunks * 1e-3) / 1e9,
         "mean_valid": float(np.minimum(pos0 + (args.warmup + args.steps // 2) // L + 1, C).mean()),
     }
     ctx.close()
@@ -780,13 +808,14 @@ def cpu_baseline_frames(weights, seconds=8.0):
     this host's cores: the stand-in for the reference's CPU path, ORT-wasm
     running the published graphs, which is not available offline.
 
-    B = 1: the single-stream prompt (281 rows) is prefilled (untimed), then
-    frames -- the 17-step local head with the repetition penalty, then the
-    12-layer decode step of the frame row -- run until `seconds` have passed;
-    the GEMMs split their columns over the threads.  B = 64: one frame for
-    each of 64 voices at a time, the voices spread over the threads (each
-    voice's GEMMs on one thread), on rings filled with 300 positions of
-    placeholder K/V (the timing does not depend on their values)."""
+    Each of three samples runs for a third of `seconds`.  B = 1: the
+    single-stream prompt (281 rows) is prefilled (untimed), then frames --
+    the 17-step local head with the repetition penalty, then the 12-layer
+    decode step of the frame row -- run; the GEMMs split their columns over
+    the threads.  B = 64 and B = 256: one frame for each of the voices at a
+    time, the voices spread over the threads (each voice's GEMMs on one
+    thread), on rings filled with 300 positions of placeholder K/V (the
+    timing does not depend on their values)."""
     from mockbird_amd import synth
     from oracle import oracle
 
@@ -801,7 +830,7 @@ def cpu_baseline_frames(weights, seconds=8.0):
     h = st.prefill_all(0, rows)[-1][None]
     pos = rows.shape[0]
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 2:
+    while time.perf_counter() - t0 < seconds / 3:
         codes, _, _ = st.local_frame(h)
         h = st.decode_step(synth.frame_row(codes[0])[None], [pos])
         pos += 1
@@ -810,24 +839,25 @@ def cpu_baseline_frames(weights, seconds=8.0):
     out["B1"] = {"value": round(n / dt, 2), "sample": f"{n} frames after a 281-row prefill, "
                  f"{dt:.1f} s, GEMM columns over {threads} threads"}
     del st
-    B, P = 64, 300
-    st = oracle.ModelState(m, B, 1024, kv_bf16=False)
-    st.K[:] = 0.01
-    st.V[:] = 0.01
-    st.slot_pos[:, :, :P] = np.arange(P, dtype=np.int32)
+    P = 300
     g = np.random.default_rng(3)
-    h = g.standard_normal((B, D), dtype=np.float32)
-    pos = np.full(B, P, np.int32)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 2:
-        codes, _, _ = st.local_frame(h)
-        h = st.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
-        pos = pos + 1
-        n += 1
-    dt = time.perf_counter() - t0
-    out["B64"] = {"value": round(B * n / dt, 2), "sample": f"{n} frames of 64 voices at positions "
-                  f"300+, {dt:.1f} s, voices over {threads} threads"}
-    del st
+    for B in (64, 256):
+        st = oracle.ModelState(m, B, 1024, kv_bf16=False)
+        st.K[:, :, :P] = 0.01
+        st.V[:, :, :P] = 0.01
+        st.slot_pos[:, :, :P] = np.arange(P, dtype=np.int32)
+        h = g.standard_normal((B, D), dtype=np.float32)
+        pos = np.full(B, P, np.int32)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds / 3:
+            codes, _, _ = st.local_frame(h)
+            h = st.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
+            pos = pos + 1
+            n += 1
+        dt = time.perf_counter() - t0
+        out[f"B{B}"] = {"value": round(B * n / dt, 2), "sample": f"{n} frames of {B} voices at "
+                        f"positions 300+, {dt:.1f} s, voices over {threads} threads"}
+        del st
     return out
 
 
@@ -913,7 +943,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline_c1(args.cpu_seconds)
-        cpu["frames_per_sec"] = cpu_baseline_frames(w, args.cpu_seconds * 2 / 3)
+        cpu["frames_per_sec"] = cpu_baseline_frames(w, args.cpu_seconds)
     line = {
         "metric": METRIC,
         "value": round(bf16["gbs"], 2),
@@ -947,6 +977,19 @@ def main():
         "cpu_baseline": cpu,
         "two_launch_bf16": {"ms_per_step": round(bf16["unfused_ms_per_step"], 5),
                             "gbs": round(bf16["unfused_gbs"], 1)},
+        "append_only_bf16": {
+            "what": "the ring append alone (k_ring_write: q | k | v rows in, RoPE, K and V "
+                    "into bf16 rings, roped q out)",
+            "step": {"rows": "64 voices x 1 row (mb_ring_append_dev), launched back to back "
+                             "from Python: the host's call rate, not the kernel, sets this",
+                     "us_per_launch": round(bf16["append_ms_per_step"] * 1e3, 2),
+                     "bytes_per_launch": bf16["append_bytes_per_step"],
+                     "gbs": round(bf16["append_gbs"], 1)},
+            "chunk": {"rows": "64 voices x 192 rows (mb_ring_write_rows_dev)",
+                      "us_per_launch": round(bf16["chunk_ms_per_launch"] * 1e3, 2),
+                      "bytes_per_launch": bf16["chunk_bytes_per_launch"],
+                      "gbs": round(bf16["chunk_gbs"], 1),
+                      "frac": round(bf16["chunk_gbs"] / HBM_PEAK_GBS, 4)}},
         "f32_kv": None if f32 is None else {
             "value": round(f32["gbs"], 2), "unit": "GB/s",
             "ms_per_step": round(f32["ms_per_step"], 5),

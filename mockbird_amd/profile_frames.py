@@ -2,6 +2,7 @@
 
     python -m mockbird_amd.profile_frames TRACE.csv --delimiter k_frame_emit [--skip 3]
     python -m mockbird_amd.profile_frames TRACE.csv --delimiter k_codec_head --last 24
+    python -m mockbird_amd.profile_frames TRACE.csv --grids k_ring_write
 
 TRACE.csv is the `*_kernel_trace.csv` of `rocprofv3 --kernel-trace
 --output-format csv`.  Dispatches are split into runs wherever the GPU sat
@@ -14,6 +15,12 @@ drops the first frames as warm-up, `--last` keeps only the last n).  The
 "span" is the time from one delimiter's end to the next one's, the frame's
 wall time on the GPU; under the tracer it includes the tracer's per-launch
 overhead, the kernel time does not.
+
+`--grids KERNEL` instead lists the dispatches of the kernels whose name
+contains KERNEL grouped by kernel and grid size (one launch shape each):
+dispatches, mean, min and max duration.  Given the `*_counter_collection.csv`
+of a `rocprofv3 --pmc` run instead, it lists each counter's median value per
+dispatch for each launch shape.
 """
 from __future__ import annotations
 
@@ -94,10 +101,42 @@ def grid_of(run: list[dict], kernel: str) -> str:
     return "?"
 
 
+def by_grid(rows: list[dict], kernel: str):
+    """[(kernel, grid, workgroup, n, mean us, min us, max us)] per (kernel, grid, workgroup)."""
+    agg = collections.defaultdict(list)
+    for r in rows:
+        if kernel in r["Kernel_Name"]:
+            key = (short_name(r["Kernel_Name"]), int(r.get("Grid_Size_X", r.get("Grid_Size", 0))),
+                   int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 0))))
+            agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return [(k, g, w, len(d), sum(d) / len(d), min(d), max(d))
+            for (k, g, w), d in sorted(agg.items())]
+
+
+def counters_by_grid(path: str, kernel: str):
+    """[(kernel, grid, counter, dispatches, median value)] from a counter
+    collection CSV (one row per dispatch and counter)."""
+    agg = collections.defaultdict(list)
+    with open(path, newline="") as fh:
+        for r in csv.DictReader(fh):
+            if kernel in r["Kernel_Name"]:
+                agg[(short_name(r["Kernel_Name"]), int(r["Grid_Size"]), r["Counter_Name"])].append(
+                    float(r["Counter_Value"]))
+    out = []
+    for (k, g, c), vals in sorted(agg.items()):
+        vals.sort()
+        n = len(vals)
+        med = vals[n // 2] if n % 2 else 0.5 * (vals[n // 2 - 1] + vals[n // 2])
+        out.append((k, g, c, n, med))
+    return out
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("trace")
-    ap.add_argument("--delimiter", required=True, help="name of a frame's last kernel")
+    ap.add_argument("--delimiter", help="name of a frame's last kernel")
+    ap.add_argument("--grids", default=None, metavar="KERNEL",
+                    help="list KERNEL's dispatches by grid size instead of frames")
     ap.add_argument("--skip", type=int, default=0, help="frames dropped at the start of each run")
     ap.add_argument("--last", type=int, default=None, help="keep only the last n frames of a run")
     ap.add_argument("--gap-ms", type=float, default=5.0, help="idle time that separates runs")
@@ -105,6 +144,22 @@ def main(argv=None) -> int:
     ap.add_argument("--grid-of", default=None,
                     help="kernel whose grid size is printed per run (to tell runs apart)")
     a = ap.parse_args(argv)
+    if a.grids:
+        with open(a.trace, newline="") as fh:
+            header = next(csv.reader(fh))
+        if "Counter_Value" in header:
+            print("| kernel | grid (threads) | counter | dispatches | median per dispatch |")
+            print("|---|---:|---|---:|---:|")
+            for k, g, c, n, med in counters_by_grid(a.trace, a.grids):
+                print(f"| `{k}` | {g} | {c} | {n} | {med:.1f} |")
+            return 0
+        print("| kernel | grid (threads) | workgroup | dispatches | avg us | min us | max us |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for k, g, w, n, avg, lo, hi in by_grid(load(a.trace), a.grids):
+            print(f"| `{k}` | {g} | {w} | {n} | {avg:.2f} | {lo:.2f} | {hi:.2f} |")
+        return 0
+    if not a.delimiter:
+        ap.error("--delimiter or --grids is required")
     for run in split_runs(load(a.trace), a.gap_ms * 1e6):
         fr = frames_of(run, a.delimiter, a.skip, a.last)
         if not fr:

@@ -59,3 +59,36 @@ def test_cli_prints_a_table_per_run(tmp_path, capsys):
     assert pf.main([p, "--delimiter", "k_frame_emit", "--skip", "1", "--grid-of", "k_frame_emit"]) == 0
     out = capsys.readouterr().out
     assert out.count("| kernel |") == 2 and "grid 256" in out and "`mb::k_attn` | 1 | 20.00" in out
+
+
+def test_grids_lists_one_launch_shape_per_line(tmp_path, capsys):
+    p = str(tmp_path / "t.csv")
+    _trace(p)
+    g = pf.by_grid(pf.load(p), "k_gemm")
+    assert [(k, grid, n, avg) for k, grid, _, n, avg, _, _ in g] == [
+        ("mb::k_gemm<2, 2, 0>", 64, 10, 10.0), ("mb::k_gemm<2, 2, 0>", 256, 10, 11.0)]
+    assert pf.main([p, "--grids", "k_attn"]) == 0
+    out = capsys.readouterr().out
+    assert "| `mb::k_attn` | 64 | 0 | 5 | 22.00 | 20.00 | 30.00 |" in out
+
+
+def test_grids_on_a_counter_collection(tmp_path, capsys):
+    p = str(tmp_path / "c.csv")
+    rows = []
+    for d, (grid, val) in enumerate([(64, 10.0), (64, 30.0), (64, 20.0), (256, 5.0), (256, 7.0)]):
+        for c, scale in (("FETCH_SIZE", 1.0), ("WRITE_SIZE", 0.5)):
+            rows.append({"Dispatch_Id": d, "Kernel_Name": "mb::k_ring_write<true>(int)",
+                         "Grid_Size": grid, "Counter_Name": c, "Counter_Value": val * scale})
+    rows.append({"Dispatch_Id": 9, "Kernel_Name": "other", "Grid_Size": 64,
+                 "Counter_Name": "FETCH_SIZE", "Counter_Value": 1.0})
+    with open(p, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    got = pf.counters_by_grid(p, "k_ring_write")
+    assert got == [("mb::k_ring_write<true>", 64, "FETCH_SIZE", 3, 20.0),
+                   ("mb::k_ring_write<true>", 64, "WRITE_SIZE", 3, 10.0),
+                   ("mb::k_ring_write<true>", 256, "FETCH_SIZE", 2, 6.0),
+                   ("mb::k_ring_write<true>", 256, "WRITE_SIZE", 2, 3.0)]
+    assert pf.main([p, "--grids", "k_ring_write"]) == 0
+    assert "| `mb::k_ring_write<true>` | 256 | FETCH_SIZE | 2 | 6.0 |" in capsys.readouterr().out
