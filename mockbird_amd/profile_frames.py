@@ -16,6 +16,10 @@ drops the first frames as warm-up, `--last` keeps only the last n).  The
 wall time on the GPU; under the tracer it includes the tracer's per-launch
 overhead, the kernel time does not.
 
+`--nth KERNEL` adds, per run, the mean duration of the i-th launch of the
+kernels whose name contains KERNEL within a frame (i = 1, 2, ...: a frame's
+layers or stages in launch order).
+
 `--grids KERNEL` instead lists the dispatches of the kernels whose name
 contains KERNEL grouped by kernel and grid size (one launch shape each):
 dispatches, mean, min and max duration.  Given the `*_counter_collection.csv`
@@ -94,6 +98,20 @@ def breakdown(run: list[dict], frames) -> dict:
             "span_us": span / n, "kernels": kernels}
 
 
+def nth_launches(run: list[dict], frames, kernel: str):
+    """{name: [mean us of the i-th launch of that kernel in a frame]} over the
+    frames (a, b]."""
+    agg = collections.defaultdict(lambda: collections.defaultdict(list))
+    for a, b in frames:
+        seen = collections.Counter()
+        for r in run[a + 1:b + 1]:
+            if kernel in r["Kernel_Name"]:
+                k = short_name(r["Kernel_Name"])
+                agg[k][seen[k]].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+                seen[k] += 1
+    return {k: [sum(v[i]) / len(v[i]) for i in sorted(v)] for k, v in sorted(agg.items())}
+
+
 def grid_of(run: list[dict], kernel: str) -> str:
     for r in run:
         if kernel in r["Kernel_Name"]:
@@ -135,6 +153,8 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("trace")
     ap.add_argument("--delimiter", help="name of a frame's last kernel")
+    ap.add_argument("--nth", default=None, metavar="KERNEL",
+                    help="also list the mean duration of each launch of KERNEL by its order in a frame")
     ap.add_argument("--grids", default=None, metavar="KERNEL",
                     help="list KERNEL's dispatches by grid size instead of frames")
     ap.add_argument("--skip", type=int, default=0, help="frames dropped at the start of each run")
@@ -172,6 +192,10 @@ def main(argv=None) -> int:
         print("|---|---:|---:|---:|---:|")
         for k, c, avg, per in b["kernels"][:a.top]:
             print(f"| `{k}` | {c:.0f} | {avg:.2f} | {per:.1f} | {100 * per / b['kernel_us']:.1f} % |")
+        if a.nth:
+            for k, means in nth_launches(run, fr, a.nth).items():
+                print(f"\n`{k}` by launch order in the frame (us): " +
+                      ", ".join(f"{m:.2f}" for m in means))
     return 0
 
 

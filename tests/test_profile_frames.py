@@ -92,3 +92,14 @@ def test_grids_on_a_counter_collection(tmp_path, capsys):
                    ("mb::k_ring_write<true>", 256, "WRITE_SIZE", 2, 3.0)]
     assert pf.main([p, "--grids", "k_ring_write"]) == 0
     assert "| `mb::k_ring_write<true>` | 256 | FETCH_SIZE | 2 | 6.0 |" in capsys.readouterr().out
+
+
+def test_nth_launch_means(tmp_path, capsys):
+    p = str(tmp_path / "t.csv")
+    _trace(p)
+    run = pf.split_runs(pf.load(p), 5e6)[0]
+    fr = pf.frames_of(run, "k_frame_emit", skip=0, last=None)
+    got = pf.nth_launches(run, fr, "k_gemm")
+    assert got == {"mb::k_gemm<2, 2, 0>": [10.0, 10.0]}
+    assert pf.main([p, "--delimiter", "k_frame_emit", "--nth", "k_attn"]) == 0
+    assert "`mb::k_attn` by launch order in the frame (us): 20.00" in capsys.readouterr().out
