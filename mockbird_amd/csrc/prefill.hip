@@ -633,12 +633,15 @@ __global__ __launch_bounds__(256) void k_flash_f32(
 // positions per frame and attend over windows of 500..3248.  A workgroup is
 // one (sequence, head); its NW waves take the slot range's 16-slot groups in
 // turn (wave w: groups w, w + NW, ...), so the workgroup reads its
-// (sequence, head) run front to back as one stream, and each wave computes
+// (sequence, head) run front to back as one stream (against each wave
+// streaming a contiguous run: 64 voices 1.214 -> 1.198 ms, 256 voices 2.266
+// -> 2.248 ms per codec frame, same GPU, alternating), and each wave computes
 // every query of the chunk against its groups, reading K and V straight from
 // HBM into MFMA operands (no LDS staging).  A wave's first group is issued
-// before its q rows are loaded and split.  (Against each wave streaming a
-// contiguous run: 64 voices 1.214 -> 1.198 ms, 256 voices 2.266 -> 2.248 ms
-// per codec frame, same GPU, alternating.)  Scores are S^T[16 slots][16 queries]; the P V output block
+// before the chunk's rows are written when it holds none of their slots
+// (else after), and is in flight while its q rows are loaded and split
+// (64 voices 1.158 -> 1.150 ms per codec frame, 256 voices level).  Scores
+// are S^T[16 slots][16 queries]; the P V output block
 // d holds dims 4i + d in row i, so in the step for slot 4g + j (g = lane/16)
 // a lane feeds 4 contiguous dims of that V row and its own score element j.
 //  - fp32 rings: v_mfma_f32_16x16x4f32; lane l feeds K[slot l%16][16g + kc]
@@ -712,6 +715,31 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
     }
   };
 
+  // The wave's first group is issued before the chunk's rows are written
+  // when it holds none of the slots they go to (the slots of rows
+  // max(0, n - C) .. n - 1, at p0 + r mod C): the other slots' K, V and
+  // positions are not written by this launch, so the loads see what they
+  // would see after the barrier.  A group that may hold a written slot loads
+  // after the barrier.
+  Raw cur, nxt;
+  bool early = false;
+  if (wave < groups && p0 >= 0) {
+    const int lo = wave * 16, hi = min(lo + 16, kv_end);
+    const int wr0 = n > C ? n - C : 0;
+    const int len = n - wr0;
+    bool hit = true;
+    if (len <= 0) {
+      hit = false;
+    } else if (len < C) {
+      const int64_t first = p0 + wr0;
+      const int start = wrap ? (int)(first % C) : (int)min(first, (int64_t)C);
+      const int end = start + len;  // the range [start, end) taken mod C
+      hit = end <= C ? (start < hi && lo < end) : (start < hi || lo < end - C);
+    }
+    early = !hit;
+    if (early) load_group(wave, cur);
+  }
+
   // The chunk's rows enter the ring first, as k_ring_write writes them but
   // for this head only: thread (r, d0) ropes q and k of row r's dims d0 ..
   // d0 + 7 at position p0 + r, stores K and V at slot pos mod C (only the
@@ -758,8 +786,7 @@ __global__ __launch_bounds__(64 * NW) void k_attn_window(
   __syncthreads();  // the rows are in the ring and q in LDS for every wave
 
   // the wave's first group is in flight while q is split
-  Raw cur, nxt;
-  if (wave < groups) load_group(wave, cur);
+  if (wave < groups && !early) load_group(wave, cur);
   // Positions relative to the sequence's first query, clamped so the window
   // test is one unsigned compare; an empty slot and a query past n are
   // outside every window.
