@@ -1155,12 +1155,20 @@ static void xt_go(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint4
 template <int MI, bool LNF, bool W1, bool GAM>
 static int xt_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint4* Wx, int N,
                      int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
-                     const float* lnd, const float* gamma) {
+                     const float* lnd, const float* gamma, bool three) {
   // Two workgroups per CU, with three stages where they still fit the 160 KB
   // of LDS (else two).  Measured at 8192 rows (QKV / O / fc_in / fc_out):
   // one workgroup per CU with four stages took 162 / 66 / 193 / 221 us
-  // against 118 / 42 / 130 / 136 us.
+  // against 118 / 42 / 130 / 136 us.  `three`: three workgroups per CU with
+  // two stages each (64-row tiles; see the caller).
   constexpr int SB = xt_stage_bytes<MI, W1, GAM>();
+  if constexpr (6 * SB <= 160 * 1024) {
+    if (three) {
+      xt_go<MI, 2, 3, LNF, W1, GAM>(ctx, epi, A, lda, Wx, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+      MB_HIP(ctx, hipGetLastError());
+      return MB_OK;
+    }
+  }
   xt_go<MI, 3 * SB <= 80 * 1024 ? 3 : 2, 2, LNF, W1, GAM>(ctx, epi, A, lda, Wx, N, K, bias, Cm,
                                                           ldc, M, lnc, lnd, gamma);
   MB_HIP(ctx, hipGetLastError());
@@ -1188,15 +1196,28 @@ static int gemm_x3_any(mb_ctx* ctx, int epi, const float* A, int64_t lda, const 
         ((uintptr_t)gamma & 15))
       return fail(ctx, MB_ERR_ARG, "split-bf16 gemm shape/alignment unsupported (M %d N %d K %d)",
                   M, N, K);
-    // (128-row tiles over 64-row ones at 8192 rows: QKV 118 against 130 us)
+    // (128-row tiles over 64-row ones at 8192 rows: QKV 118 against 130 us,
+    // both at two workgroups per CU.)  Where the 128-row tiles leave the last
+    // of their rounds (512 per round, two per CU) part full and 64-row tiles
+    // fill at least one round of 768, the 64-row tiles run three per CU with
+    // two stages each: at 8192 rows QKV (1152 tiles of 128 rows, 2.25 rounds)
+    // 106.8 -> 102.6 us, O and fc_out (384 tiles) 36.8 -> 34.9 and 126.5 ->
+    // 117.8 us, the 256-voice codec frame 2.146 -> 2.130 ms (same GPU,
+    // alternating); fc_in (1536 tiles, three whole rounds) went 118.3 ->
+    // 123.8 us that way and keeps the 128-row tiles.
     auto tiles = [&](int mi) { return (int64_t)(N / 128) * ((M + 32 * mi - 1) / (32 * mi)); };
-    const int mi = tiles(4) >= 256 ? 4 : tiles(2) >= 256 ? 2 : 1;
+    const bool three = tiles(2) >= 768 && tiles(4) % 512 != 0;
+    const int mi = three ? 2 : tiles(4) >= 256 ? 4 : tiles(2) >= 256 ? 2 : 1;
     auto go = [&](auto mi_) {
       constexpr int T = decltype(mi_)::value;
       if (lnf && gamma)
-        return xt_launch<T, true, W1, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
-      if (lnf) return xt_launch<T, true, W1, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd, nullptr);
-      return xt_launch<T, false, W1, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, nullptr, nullptr, nullptr);
+        return xt_launch<T, true, W1, true>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, lnc, lnd,
+                                            gamma, three);
+      if (lnf)
+        return xt_launch<T, true, W1, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, lnc,
+                                             lnd, nullptr, three);
+      return xt_launch<T, false, W1, false>(ctx, epi, A, lda, W, N, K, bias, Cm, ldc, M, nullptr,
+                                            nullptr, nullptr, three);
     };
     if (mi == 4) return go(std::integral_constant<int, 4>{});
     if (mi == 2) return go(std::integral_constant<int, 2>{});
