@@ -22,7 +22,9 @@ layers or stages in launch order).
 
 `--grids KERNEL` instead lists the dispatches of the kernels whose name
 contains KERNEL grouped by kernel and grid size (one launch shape each):
-dispatches, mean, min and max duration.  Given the `*_counter_collection.csv`
+dispatches, mean, min and max duration; with `--by-run` each unbroken run
+of one shape's dispatches (in dispatch order) is a line of its own, which
+tells apart two projections that share a grid.  Given the `*_counter_collection.csv`
 of a `rocprofv3 --pmc` run instead, it lists each counter's median value per
 dispatch for each launch shape.
 """
@@ -119,29 +121,45 @@ def grid_of(run: list[dict], kernel: str) -> str:
     return "?"
 
 
-def by_grid(rows: list[dict], kernel: str):
-    """[(kernel, grid, workgroup, n, mean us, min us, max us)] per (kernel, grid, workgroup)."""
+def by_grid(rows: list[dict], kernel: str, by_run: bool = False):
+    """[(kernel, grid, workgroup, n, mean us, min us, max us)] per (kernel, grid,
+    workgroup), or with by_run per unbroken run of such dispatches among the
+    matching ones (in start order), runs listed in order."""
     agg = collections.defaultdict(list)
+    run, last = 0, None
     for r in rows:
         if kernel in r["Kernel_Name"]:
             key = (short_name(r["Kernel_Name"]), int(r.get("Grid_Size_X", r.get("Grid_Size", 0))),
                    int(r.get("Workgroup_Size_X", r.get("Workgroup_Size", 0))))
-            agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    return [(k, g, w, len(d), sum(d) / len(d), min(d), max(d))
-            for (k, g, w), d in sorted(agg.items())]
+            if by_run and key != last:
+                run += 1
+                last = key
+            agg[(run, key) if by_run else key].append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    items = sorted(agg.items())
+    if by_run:
+        items = [(k, d) for (_, k), d in items]
+    return [(k, g, w, len(d), sum(d) / len(d), min(d), max(d)) for (k, g, w), d in items]
 
 
-def counters_by_grid(path: str, kernel: str):
+def counters_by_grid(path: str, kernel: str, by_run: bool = False):
     """[(kernel, grid, counter, dispatches, median value)] from a counter
-    collection CSV (one row per dispatch and counter)."""
-    agg = collections.defaultdict(list)
+    collection CSV (one row per dispatch and counter); with by_run, per
+    unbroken run of one shape's dispatches in dispatch order."""
     with open(path, newline="") as fh:
-        for r in csv.DictReader(fh):
-            if kernel in r["Kernel_Name"]:
-                agg[(short_name(r["Kernel_Name"]), int(r["Grid_Size"]), r["Counter_Name"])].append(
-                    float(r["Counter_Value"]))
+        rows = [r for r in csv.DictReader(fh) if kernel in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r.get("Dispatch_Id", 0)))
+    agg = collections.defaultdict(list)
+    run, last, last_id = 0, None, None
+    for r in rows:
+        shape = (short_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+        if by_run and shape != last and r.get("Dispatch_Id") != last_id:
+            run += 1
+            last = shape
+        last_id = r.get("Dispatch_Id")
+        agg[(run, shape[0], shape[1], r["Counter_Name"])].append(float(r["Counter_Value"]))
     out = []
-    for (k, g, c), vals in sorted(agg.items()):
+    for (_, k, g, c), vals in sorted(agg.items()):
         vals.sort()
         n = len(vals)
         med = vals[n // 2] if n % 2 else 0.5 * (vals[n // 2 - 1] + vals[n // 2])
@@ -157,6 +175,8 @@ def main(argv=None) -> int:
                     help="also list the mean duration of each launch of KERNEL by its order in a frame")
     ap.add_argument("--grids", default=None, metavar="KERNEL",
                     help="list KERNEL's dispatches by grid size instead of frames")
+    ap.add_argument("--by-run", action="store_true",
+                    help="with --grids: one line per unbroken run of a shape's dispatches")
     ap.add_argument("--skip", type=int, default=0, help="frames dropped at the start of each run")
     ap.add_argument("--last", type=int, default=None, help="keep only the last n frames of a run")
     ap.add_argument("--gap-ms", type=float, default=5.0, help="idle time that separates runs")
@@ -170,12 +190,12 @@ def main(argv=None) -> int:
         if "Counter_Value" in header:
             print("| kernel | grid (threads) | counter | dispatches | median per dispatch |")
             print("|---|---:|---|---:|---:|")
-            for k, g, c, n, med in counters_by_grid(a.trace, a.grids):
+            for k, g, c, n, med in counters_by_grid(a.trace, a.grids, a.by_run):
                 print(f"| `{k}` | {g} | {c} | {n} | {med:.1f} |")
             return 0
         print("| kernel | grid (threads) | workgroup | dispatches | avg us | min us | max us |")
         print("|---|---:|---:|---:|---:|---:|---:|")
-        for k, g, w, n, avg, lo, hi in by_grid(load(a.trace), a.grids):
+        for k, g, w, n, avg, lo, hi in by_grid(load(a.trace), a.grids, a.by_run):
             print(f"| `{k}` | {g} | {w} | {n} | {avg:.2f} | {lo:.2f} | {hi:.2f} |")
         return 0
     if not a.delimiter:

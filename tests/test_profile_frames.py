@@ -103,3 +103,43 @@ def test_nth_launch_means(tmp_path, capsys):
     assert got == {"mb::k_gemm<2, 2, 0>": [10.0, 10.0]}
     assert pf.main([p, "--delimiter", "k_frame_emit", "--nth", "k_attn"]) == 0
     assert "`mb::k_attn` by launch order in the frame (us): 20.00" in capsys.readouterr().out
+
+
+def test_grids_by_run_splits_shapes_sharing_a_grid(tmp_path):
+    p = str(tmp_path / "r.csv")
+    rows, t = [], 0
+    for name, dur, n in (("mb::k_gemm<1>(int)", 5, 3), ("mb::k_other(int)", 1, 1),
+                         ("mb::k_gemm<1>(int)", 9, 2), ("mb::k_gemm<2>(int)", 4, 2),
+                         ("mb::k_gemm<1>(int)", 7, 1)):
+        for _ in range(n):
+            rows.append({"Kernel_Name": name, "Start_Timestamp": t, "End_Timestamp": t + dur * 1000,
+                         "Grid_Size_X": 64, "Workgroup_Size_X": 256})
+            t += dur * 1000 + 100
+    with open(p, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    runs = pf.by_grid(pf.load(p), "k_gemm", by_run=True)
+    # the k_other dispatch between the two k_gemm<1> runs does not match the
+    # filter, so those two runs join; k_gemm<2> splits them from the last
+    assert [(k, n, avg) for k, _, _, n, avg, _, _ in runs] == [
+        ("mb::k_gemm<1>", 5, 6.6), ("mb::k_gemm<2>", 2, 4.0), ("mb::k_gemm<1>", 1, 7.0)]
+    assert [(k, n) for k, _, _, n, _, _, _ in pf.by_grid(pf.load(p), "k_gemm")] == [
+        ("mb::k_gemm<1>", 6), ("mb::k_gemm<2>", 2)]
+
+
+def test_counters_by_run(tmp_path):
+    p = str(tmp_path / "c.csv")
+    rows = []
+    for d, (name, val) in enumerate([("mb::k_g<1>(int)", 10.0), ("mb::k_g<1>(int)", 12.0),
+                                     ("mb::k_g<2>(int)", 5.0), ("mb::k_g<1>(int)", 30.0)]):
+        rows.append({"Dispatch_Id": d, "Kernel_Name": name, "Grid_Size": 64,
+                     "Counter_Name": "MfmaUtil", "Counter_Value": val})
+    with open(p, "w", newline="") as fh:
+        w = csv.DictWriter(fh, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    assert pf.counters_by_grid(p, "k_g", by_run=True) == [
+        ("mb::k_g<1>", 64, "MfmaUtil", 2, 11.0), ("mb::k_g<2>", 64, "MfmaUtil", 1, 5.0),
+        ("mb::k_g<1>", 64, "MfmaUtil", 1, 30.0)]
+    assert pf.counters_by_grid(p, "k_g")[0] == ("mb::k_g<1>", 64, "MfmaUtil", 3, 12.0)
