@@ -1662,6 +1662,141 @@ int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float
   return MB_OK;
 }
 
+// The attention's output projection at up to kPartsMaxSeqs rows, reading
+// the attention as per-wave partials (k_attn_unit's PARTS form): part holds,
+// for row m, head h and wave w < nwp, acc[64], max and sum at
+// ((m * 12 + h) * nwp + w) * PART.  Each workgroup first merges them into its
+// input rows in LDS -- per (row, head) the waves' states weighted by
+// exp(max_w - max) and divided by the weighted sum, the fold k_attn_unit does
+// through LDS within one block -- with its weight loads already in flight,
+// then takes k_gemv_k16's products (one wave per column, 8 bf16 weights per
+// lane and 512-k step) and epilogue.  Only the bf16-weight store runs it: with
+// fp32 weights the merged path measured no faster per frame than the unit
+// attention followed by k_gemv_k.
+template <int EPI, int MR>
+__global__ __launch_bounds__(256) void k_gemv_parts(const float* part, int nwp,
+                                                    const uint16_t* __restrict__ Wk, int N,
+                                                    const float* __restrict__ bias,
+                                                    float* __restrict__ Cm, int64_t ldc, int M) {
+  constexpr int K = D, ST = (K + 511) / 512;
+  __shared__ __align__(16) float xs[MR][K];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + wave;
+  uint4 w16[ST];
+#pragma unroll
+  for (int st = 0; st < ST; st++)
+    w16[st] = *(const uint4*)(Wk + (int64_t)n * K + min(st * 512 + 8 * lane, K - 8));
+  const int le = min(lane, M - 1);
+  const float ep_b = bias ? bias[n] : 0.f;
+  const float ep_c = (EPI == EPI_ADD || EPI == EPI_SCALE_ADD) ? Cm[(int64_t)le * ldc + n] : 0.f;
+  // (row, 4-dim quad) pairs over the 256 threads; each issues all of its
+  // partials' loads at once (unused ones re-read the last partial), so a
+  // pair costs one round trip
+  constexpr int NP = 16;
+  for (int i = threadIdx.x; i < M * (K / 4); i += 256) {
+    const int m = i / (K / 4), q = i % (K / 4), h = q / 16, d4 = (q % 16) * 4;
+    const float* pb = part + (int64_t)(m * H + h) * nwp * PART;
+    float2 ml[NP];
+    float4 av[NP];
+#pragma unroll
+    for (int v = 0; v < NP; v++) {
+      const float* pv = pb + min(v, nwp - 1) * PART;
+      ml[v] = *(const float2*)(pv + 64);
+      av[v] = *(const float4*)(pv + d4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every load above issues before the first use
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NP; v++)
+      if (v < nwp) mx = fmaxf(mx, ml[v].x);
+    // an empty wave (max -inf) weighs 0, so no branch holds a load back
+    float L = 0.f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int v = 0; v < NP; v++) {
+      const float sv = v < nwp && ml[v].x != -INFINITY ? __expf(ml[v].x - mx) : 0.f;
+      L += ml[v].y * sv;
+      o.x = fmaf(sv, av[v].x, o.x);
+      o.y = fmaf(sv, av[v].y, o.y);
+      o.z = fmaf(sv, av[v].z, o.z);
+      o.w = fmaf(sv, av[v].w, o.w);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *(float4*)&xs[m][h * HD + d4] = make_float4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+  }
+  __syncthreads();
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; m++) acc[m] = 0.f;
+#pragma unroll
+  for (int st = 0; st < ST; st++) {
+    // lanes past K (the second step's upper half) add zeros
+    const bool in = st * 512 + 8 * lane < K;
+    const int k = min(st * 512 + 8 * lane, K - 8);
+    const uint32_t wb[4] = {in ? w16[st].x : 0u, in ? w16[st].y : 0u, in ? w16[st].z : 0u,
+                            in ? w16[st].w : 0u};
+    float wf[8];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      wf[2 * t] = __uint_as_float(wb[t] << 16);
+      wf[2 * t + 1] = __uint_as_float(wb[t] & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) {
+      const float4 a0 = *(const float4*)&xs[min(m, M - 1)][k];
+      const float4 a1 = *(const float4*)&xs[min(m, M - 1)][k + 4];
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int t = 0; t < 8; t++) acc[m] = fmaf(av[t], wf[t], acc[m]);
+    }
+  }
+  float mine = 0.f;
+#pragma unroll
+  for (int m = 0; m < MR; m++) {
+    if (m >= M) break;
+    float v = acc[m];
+#pragma unroll
+    for (int sh = 1; sh < 16; sh <<= 1) v += __shfl_xor(v, sh);
+    v = col_sum(v);
+    if (lane == m) mine = v;
+  }
+  if (lane >= M) return;
+  float o = mine;
+  if (EPI == EPI_SCALE_ADD) {
+    o = ep_c + ep_b * o;
+  } else {
+    if (bias) o += ep_b;
+    if (EPI == EPI_GELU) o = gelu_tanh(o);
+    if (EPI == EPI_GELU_ERF) o = gelu_erf(o);
+    if (EPI == EPI_ADD) o = ep_c + o;
+  }
+  Cm[(int64_t)lane * ldc + n] = o;
+}
+
+int launch_gemv_k_parts(mb_ctx* ctx, int epi, const float* part, int nwp, const uint16_t* Wk,
+                        int N, const float* bias, float* Cm, int64_t ldc, int M) {
+  if (M <= 0) return MB_OK;
+  if (M > kPartsMaxSeqs || N % 4 || nwp < 1 || nwp > 16 || ((uintptr_t)part & 15) ||
+      ((uintptr_t)Wk & 15))
+    return fail(ctx, MB_ERR_ARG, "partials gemv shape unsupported (M %d N %d, %d partials)", M, N,
+                nwp);
+  const dim3 grid((unsigned)(N / 4));
+  with_epi(epi, [&](auto e) {
+    constexpr int E = decltype(e)::value;
+    auto go = [&](auto mr) {
+      constexpr int MRv = decltype(mr)::value;
+      hipLaunchKernelGGL((k_gemv_parts<E, MRv>), grid, dim3(256), 0, ctx->stream, part, nwp, Wk, N,
+                         bias, Cm, ldc, M);
+    };
+    if (M <= 1) go(std::integral_constant<int, 1>{});
+    else if (M <= 2) go(std::integral_constant<int, 2>{});
+    else if (M <= 4) go(std::integral_constant<int, 4>{});
+    else go(std::integral_constant<int, 8>{});
+  });
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
+}
+
 // ---------------------------------------------------------------------------
 // bf16 weight storage (mb_set_weight_storage): the projection weights are
 // rounded to bf16 once (k_round_bf16) and the decode-sized kernels read them

@@ -269,6 +269,14 @@ __host__ __device__ inline int64_t row_at(const Rows& R, int b, int r) {
 int launch_ring_write(mb_ctx* ctx, const RingView& ring, int B, int rows_max, const void* qkv,
                       int qkv_dtype, const Rows& qkv_rows, const int32_t* pos0,
                       const int32_t* n_rows, void* q_out, int q_dtype, const Rows& q_rows);
+// Decode steps of at most this many sequences, with bf16 weight storage,
+// run their attention as per-wave partials merged by the O projection
+// (launch_append_attn_parts, launch_gemv_k_parts).
+constexpr int kPartsMaxSeqs = 8;
+int launch_append_attn_parts(mb_ctx* ctx, const RingView& ring, int B, const float* qkv,
+                             const int32_t* pos, int64_t max_valid, float* part, int& nw_out);
+int launch_gemv_k_parts(mb_ctx* ctx, int epi, const float* part, int nwp, const uint16_t* Wk,
+                        int N, const float* bias, float* Cm, int64_t ldc, int M);
 int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float* q,
                 const Rows& q_rows, const int32_t* pos0, const int32_t* n_rows, int64_t max_valid,
                 float* out, const Rows& out_rows);

@@ -254,6 +254,17 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
     if ((rc = launch_gemm(ctx, EPI_STORE, a.norm, D, w.attn_w, QKV, D, w.attn_b, a.qkv, QKV, (int)M)))
       return rc;
   }
+  // The decode step of up to kPartsMaxSeqs sequences with bf16 weights (the
+  // global layers; the local head's attention is k_attn_short): the
+  // attention as per-wave partials merged by the O projection.
+  const bool parts = !prefill && gemv && ctx->w_bf16 && pos_const < 0 && B <= kPartsMaxSeqs &&
+                     ring.heads == H && ring.window == ring.C;
+  float* part = nullptr;
+  int nwp = 0;
+  if (parts) {
+    part = (float*)scratch(ctx, "attn_parts", (size_t)B * H * 16 * PART * sizeof(float));
+    if (!part) return fail(ctx, MB_ERR_NOMEM, "attention partials");
+  }
   Rows qkv_rows, q_rows;
   if (prefill) {
     qkv_rows.row_stride = QKV;
@@ -270,6 +281,10 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
       return rc;
     rc = launch_prefill_attention(ctx, ring, B, rows_max, a.q, MB_DT_F32, q_rows, pos0, n_rows,
                                   a.att, q_rows);
+  } else if (parts) {
+    // a few sequences: the attention's waves spread over one-wave blocks and
+    // leave their partial states, which the O projection merges as it reads
+    rc = launch_append_attn_parts(ctx, ring, B, a.qkv, pos0, max_valid, part, nwp);
   } else {
     // one launch appends this row's K/V and attends the ring including it
     rc = launch_append_attn(ctx, ring, B, a.qkv, MB_DT_F32, qkv_rows, pos0, max_valid, nullptr,
@@ -278,7 +293,9 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   if (rc) return rc;
   // decode sizes read the column-block-major copies of O and fc_out
   const bool tiled = gemm_streams((int)M, D);
-  if ((rc = gemv ? proj_gemv(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
+  if ((rc = parts ? launch_gemv_k_parts(ctx, EPI_ADD, part, nwp, (const uint16_t*)w.proj_wk, D,
+                                        w.proj_b, a.x, D, (int)M)
+           : gemv ? proj_gemv(ctx, EPI_ADD, a.att, D, w.proj_wk, D, D, w.proj_b, a.x, D, (int)M,
                              nullptr, nullptr, nullptr)
            : x3 ? proj_split(ctx, EPI_ADD, a.att, D, w.proj_wx, D, D, w.proj_b, a.x, D, (int)M,
                              nullptr, nullptr, nullptr)

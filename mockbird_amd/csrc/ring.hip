@@ -287,13 +287,21 @@ __device__ __forceinline__ uint4 pack16(const float* x) {
 // a K half-batch in flight under its softmax.  With 12 waves per CU (64
 // sequences, C = 2048) that extra depth cost 0.9 %; with 7.5 (32 sequences,
 // C = 4096) it gained 2.4 %.
-template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16, bool EARLY = false>
+//
+// PARTS (few units, the one-to-eight-voice decode step): each of a unit's nwp
+// waves is a one-wave block of its own, so a unit's window is read on up to
+// nwp CUs instead of one, and each wave stores its online-softmax state --
+// acc[64], max, sum -- to out[(unit * nwp + wave) * PART] instead of folding
+// through LDS; the next projection merges them as it reads its input
+// (k_gemv_k's PIN form).
+template <bool KV_BF16, int U, int MAXNW, bool APPEND, bool IN_BF16, bool EARLY = false,
+          bool PARTS = false>
 __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn_unit(
     const void* __restrict__ q, Rows q_rows, const int32_t* __restrict__ pos0,
     const int32_t* __restrict__ n_rows, int rows, void* __restrict__ ring_k,
     void* __restrict__ ring_v, int32_t* __restrict__ slot_pos, int64_t ring_seq_stride, int C,
     int wrap, const float2* __restrict__ rope_tab, float* __restrict__ q_out, Rows qo_rows,
-    float* __restrict__ out, Rows out_rows) {
+    float* __restrict__ out, Rows out_rows, int nwp) {
   constexpr int VD = KV_BF16 ? 8 : 4;
   constexpr int LR = 64 / VD;
   constexpr int G = VD;
@@ -301,11 +309,14 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
   static_assert(GU <= 64, "one stored position per lane covers a batch");
   constexpr int ROWB = HD * (KV_BF16 ? 2 : 4);  // bytes of one slot's 64-dim row
   __shared__ float fold[MAXNW][PART];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = PARTS ? (int)blockIdx.x % nwp : (int)threadIdx.x >> 6;
+  const int nw = PARTS ? nwp : (int)blockDim.x >> 6;
+  const int unit = PARTS ? (int)blockIdx.x / nwp : (int)blockIdx.x;
 #if MB_BLOCK_TIMELINE
   const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 #endif
-  const int qidx = blockIdx.x / H, head = blockIdx.x % H;
+  const int qidx = unit / H, head = unit % H;
   const int b = qidx / rows, r = qidx % rows;
   if (n_rows && r >= n_rows[b]) return;  // uniform per block
   const int g = lane / LR, sub = lane % LR;
@@ -517,6 +528,16 @@ __global__ __launch_bounds__(64 * MAXNW, !KV_BF16 && APPEND ? 3 : 1) void k_attn
 #pragma unroll
     for (int i = 0; i < VD; i++) ao[i] = __shfl_xor(acc[i], off);
     merge_state<VD>(m, l, acc, mo, lo, ao);
+  }
+  if constexpr (PARTS) {
+    if (g == 0) {
+      float* pp = out + ((int64_t)unit * nwp + wave) * PART;
+#pragma unroll
+      for (int i = 0; i < VD; i += 4)
+        *(float4*)(pp + sub * VD + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+      if (sub == 0) *(float2*)(pp + 64) = make_float2(m, l);
+    }
+    return;
   }
   if (g == 0) {
 #pragma unroll
@@ -760,21 +781,21 @@ static int launch_unit(mb_ctx* ctx, const RingView& ring, int B, int rows, const
     if (max_valid <= kAttnShortWindow)
       hipLaunchKernelGGL((k_attn_unit<true, 8, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                          ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
-                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows, 0);
     else if (nq * H * nw <= 8 * cus)  // at most 8 waves per CU: deeper loads
       hipLaunchKernelGGL((k_attn_unit<true, 4, MAXNW, APPEND, IN_BF16, true>), grid, dim3(64 * nw),
                          0, ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
-                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows, 0);
     else
       hipLaunchKernelGGL((k_attn_unit<true, 4, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                          ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
-                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+                         ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows, 0);
   } else {
     constexpr int U = 12, MAXNW = 8;
     const int nw = short_waves(unit_waves(max_valid, 256, MAXNW), 4 * U, MAXNW);
     hipLaunchKernelGGL((k_attn_unit<false, U, MAXNW, APPEND, IN_BF16>), grid, dim3(64 * nw), 0,
                        ctx->stream, q, q_rows, pos0, n_rows, rows, ring.k, ring.v, ring.sp,
-                       ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows);
+                       ring.seq_stride, C, ring.wrap, ctx->rope_tab, q_out, qo_rows, out, out_rows, 0);
   }
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
@@ -785,6 +806,42 @@ int launch_attn(mb_ctx* ctx, const RingView& ring, int B, int rows, const float*
                 float* out, const Rows& out_rows) {
   return launch_unit<false, false>(ctx, ring, B, rows, q, q_rows, pos0, n_rows, max_valid, nullptr,
                                    Rows{}, out, out_rows);
+}
+
+// The appended decode step of B <= kPartsMaxSeqs sequences as per-wave
+// partials (k_attn_unit's PARTS form): fp32 q | k | v rows, one row each.
+// `part` holds B * 12 * nw_out * PART floats; nw_out is at most 16.
+int launch_append_attn_parts(mb_ctx* ctx, const RingView& ring, int B, const float* qkv,
+                             const int32_t* pos, int64_t max_valid, float* part, int& nw_out) {
+  if (ring.heads != H || ring.window != ring.C)
+    return fail(ctx, MB_ERR_ARG, "single-query decode attention runs on the model's 12-head rings");
+  if (B < 1 || B > kPartsMaxSeqs) return fail(ctx, MB_ERR_ARG, "partials take 1..%d sequences", kPartsMaxSeqs);
+  const int C = ring.C;
+  if (max_valid > C) max_valid = C;
+  if (max_valid < 1) max_valid = 1;
+  const int nunits = B * H;
+  const Rows qkv_rows = dense_rows(QKV, 1);
+  if (ring.bf16) {
+    constexpr int U = 8, MAXNW = 16;
+    const int nw = (int)std::min<int64_t>(MAXNW, std::max<int64_t>(unit_waves(max_valid, 180, MAXNW),
+                                                                  (max_valid + 63) / 64));
+    hipLaunchKernelGGL((k_attn_unit<true, U, MAXNW, true, false, false, true>),
+                       dim3((unsigned)(nunits * nw)), dim3(64), 0, ctx->stream, qkv, qkv_rows, pos,
+                       nullptr, 1, ring.k, ring.v, ring.sp, ring.seq_stride, C, ring.wrap,
+                       ctx->rope_tab, nullptr, Rows{}, part, Rows{}, nw);
+    nw_out = nw;
+  } else {
+    constexpr int U = 12, MAXNW = 8;
+    const int nw = (int)std::min<int64_t>(MAXNW, std::max<int64_t>(unit_waves(max_valid, 256, MAXNW),
+                                                                  (max_valid + 4 * U - 1) / (4 * U)));
+    hipLaunchKernelGGL((k_attn_unit<false, U, MAXNW, true, false, false, true>),
+                       dim3((unsigned)(nunits * nw)), dim3(64), 0, ctx->stream, qkv, qkv_rows, pos,
+                       nullptr, 1, ring.k, ring.v, ring.sp, ring.seq_stride, C, ring.wrap,
+                       ctx->rope_tab, nullptr, Rows{}, part, Rows{}, nw);
+    nw_out = nw;
+  }
+  MB_HIP(ctx, hipGetLastError());
+  return MB_OK;
 }
 
 int launch_append_attn(mb_ctx* ctx, const RingView& ring, int B, const void* qkv, int qkv_dtype,
