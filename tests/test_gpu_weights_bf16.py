@@ -12,7 +12,9 @@ scales and biases, so the LayerNorm scale that bf16 storage applies to the
 rows instead of folding into the weights is exercised.
 
 Voice counts pick the kernels: 3 voices run the GEMV kernel on the bf16
-k-major copies, 12 voices the two-product split-bf16 kernel (bf16 K/V) or
+k-major copies (and up to 8 voices the decode attention as per-wave partials
+merged by the O projection, over windows of hundreds of slots and a wrapping
+ring in the long-window cases), 12 voices the two-product split-bf16 kernel (bf16 K/V) or
 the folded fp32 streaming kernel on the rounded weights (fp32 K/V); 64 and
 256 voices (bf16 K/V) run the split-bf16 kernel's row-tiled forms that the
 benchmark's many-voice frames use.
@@ -78,6 +80,63 @@ def test_bf16_weights_prefill_decode_frames(kv, B):
             pos = pos + 1
     chk.summary(f"bf16 weights kv={kv} voices={B}")
     assert chk.codes_equal + chk.codes_tied >= 16 * 5  # at least one voice went on every frame
+
+
+@pytest.mark.parametrize("kv,C,lens", [
+    (mb.MB_KV_BF16, 1024, (600,)),
+    (mb.MB_KV_F32, 1024, (560, 300, 64, 129, 200)),
+    (mb.MB_KV_BF16, 256, (253, 250, 120, 255, 40)),
+])
+def test_bf16_weights_few_voices_long_windows(kv, C, lens):
+    """Up to 8 voices with bf16 weights: the global layers' decode attention
+    leaves per-wave partial states and the O projection merges them.
+    Windows of hundreds of slots spread each (voice, head) over several waves
+    (up to 16 on a bf16 ring, 8 on fp32), the short voices of a launch get
+    waves with no live slot, and the 256-slot ring wraps during the frames
+    (voices at 253 and 255 cross position 256)."""
+    B = len(lens)
+    say(f"bf16 weights, few voices, long windows: kv={kv} C={C} lens={lens}")
+    L, V = 2, 64
+    w = synth.model_weights(n_layers=L, vocab=V, seed=13, bias_std=0.02, ln_std=0.1)
+    # every voice goes on (assistant column = audio_end column), so every
+    # frame's codes are compared
+    w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]
+    m = oracle.Model(rounded_weights(w), n_layers=L, vocab=V)
+    prompts = [synth.prompt(40 + b, n_frames=n - 3 - (4 + b), n_text=4 + b, vocab=V)
+               for b, n in enumerate(lens)]
+    n = np.array([p.shape[0] for p in prompts], np.int32)
+    assert tuple(n) == lens
+    ids = np.full((B, n.max(), 17), 1024, np.int32)
+    ids[:, :, 0] = 0
+    for b, p in enumerate(prompts):
+        ids[b, :n[b]] = p
+    st = oracle.ModelState(m, B, C, kv_bf16=(kv == mb.MB_KV_BF16))
+    chk = FrameCheck(B)
+    frames = 5
+    with mb.Context(n_layers=L, capacity=C, max_seqs=B, max_rows=int(n.max()), kv_dtype=kv,
+                    vocab=V) as ctx:
+        ctx.upload_all(w)
+        ctx.set_weight_storage(mb.MB_W_BF16)
+        h = ctx.prefill(ids, n)
+        h_or = st.prefill(ids, n)
+        assert np.abs(h - h_or).max() < TOL[kv]
+        pos = n.copy()
+        for f in range(frames):
+            codes, cont = ctx.local_frame(h)
+            g_text, g_logits = ctx.local_logits(h, codes)
+            for b in range(B):
+                o_text, o_logits = m.local_logits(h_or[b], codes[b])
+                chk.frame(b, f"frame {f} voice {b}", codes[b], cont[b], o_text, o_logits, TOL[kv],
+                          g_text[b], g_logits[b])
+            rows = np.stack([synth.frame_row(codes[b]) for b in range(B)])
+            h = ctx.decode_step(rows, pos)
+            h_or = st.decode_step(rows, pos)
+            assert np.abs(h - h_or).max() < TOL[kv], f
+            pos = pos + 1
+        if C == 256:
+            assert pos.max() > C  # the ring wrapped
+    chk.summary(f"bf16 weights few voices kv={kv} C={C}")
+    assert chk.codes_equal + chk.codes_tied == 16 * frames * B
 
 
 @pytest.mark.parametrize("B", [64, 256])
