@@ -19,6 +19,7 @@
 #include "kv_types.h"
 #include "lds_dma.h"
 #include "mb_internal.h"
+#include "pick.h"
 
 namespace mb {
 
@@ -1497,11 +1498,12 @@ static int gemv_launch(mb_ctx* ctx, int epi, const float* A, int64_t lda, const 
 // (At most 4 waves per SIMD are asked for: a grid is N / 4 workgroups, one
 // column per wave, so at 768 and 3072 columns there are 0.75 and 3 waves per
 // SIMD, and the registers go to keeping every load of a round in flight.)
-template <int EPI, bool LNF, int MR, int KC = 0>
+template <int EPI, bool LNF, int MR, int KC = 0, bool PICK = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_gemv_k(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ Wk, int N, int K,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
-    const float* __restrict__ lnc, const float* __restrict__ lnd) {
+    const float* __restrict__ lnc, const float* __restrict__ lnd, PickIn pk) {
+  static_assert(!PICK || (MR == 1 && KC == D && LNF && EPI == EPI_STORE), "PICK: one row of 768");
   constexpr int RI = MR <= 2 ? 12 : MR <= 4 ? 6 : 3;  // k steps (256 rows each) per round of loads
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + wave;
@@ -1522,8 +1524,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 #pragma unroll
   for (int m = 0; m < MR; m++) {
     acc[m] = s1[m] = s2[m] = 0.f;
-    x0[m] = LNF ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
+    x0[m] = LNF && !PICK ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
   }
+  const float* Ar = A;  // PICK: the chosen code's embedding row
   const int Kx = KC > 0 ? KC : K;  // a constant where the launch fixed it
   // one k step (256 k): lane l's float4 at k = 256 step + 4 l.  Lanes past K
   // (only in a last, partial step) add zeros: no branch, so no load is sunk
@@ -1549,21 +1552,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
       }
     }
   };
-  auto step_load = [&](int st, float4& w, float4* a) {
+  auto load_w = [&](int st, float4& w) { w = *(const float4*)(wp + min(st * 256 + 4 * lane, Kx - 4)); };
+  auto load_a = [&](int st, float4* a) {
     const int k = min(st * 256 + 4 * lane, Kx - 4);
-    w = *(const float4*)(wp + k);
 #pragma unroll
-    for (int m = 0; m < MR; m++) a[m] = *(const float4*)(A + (int64_t)min(m, M - 1) * lda + k);
+    for (int m = 0; m < MR; m++) a[m] = *(const float4*)(Ar + (int64_t)min(m, M - 1) * lda + k);
+  };
+  auto step_load = [&](int st, float4& w, float4* a) {
+    load_w(st, w);
+    load_a(st, a);
   };
   if constexpr (KC > 0) {
     constexpr int SPR = (KC + 255) / 256;
     constexpr int RK = SPR < RI ? SPR : RI;
+    static_assert(!PICK || RK == SPR, "PICK: one round of loads");
     static_for<(SPR + RK - 1) / RK>([&](auto r_) {
       constexpr int r = decltype(r_)::value;
       constexpr int NI = (r + 1) * RK <= SPR ? RK : SPR - r * RK;
       float4 w[NI], a[NI][MR];
+      if constexpr (PICK) {
+        // the choice's logits first, the weights behind them, then the
+        // choice (waiting for the logits only) and the chosen row
+        const ChoiceIn c = pick_load(pk, lane);
 #pragma unroll
-      for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], a[i]);
+        for (int i = 0; i < NI; i++) load_w(i, w[i]);
+        Ar = pick_row(pk, c, lane, blockIdx.x == 0 && wave == 0);
+        x0[0] = Ar[0];
+#pragma unroll
+        for (int i = 0; i < NI; i++) load_a(i, a[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], a[i]);
+      }
       asm volatile("" ::: "memory");  // the round's loads stay in front, none sunk into a branch
 #pragma unroll
       for (int i = 0; i < NI; i++) step_mac(r * RK + i, w[i], a[i]);
@@ -1621,9 +1641,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 
 int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* Wk, int N, int K,
                   const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
-                  const float* lnd) {
+                  const float* lnd, const PickIn* pick) {
   if (M <= 0) return MB_OK;
   const bool lnf = lnc != nullptr;
+  if (pick) {
+    if (M != 1 || K != D || !lnf || !lnd || epi != EPI_STORE || N % 4 || ((uintptr_t)Wk & 15))
+      return fail(ctx, MB_ERR_ARG, "gemv with the code choice: one row of %d, folded LayerNorm "
+                  "(M %d N %d K %d)", D, M, N, K);
+    hipLaunchKernelGGL((k_gemv_k<EPI_STORE, true, 1, D, true>), dim3((unsigned)(N / 4)), dim3(256),
+                       0, ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, *pick);
+    MB_HIP(ctx, hipGetLastError());
+    return MB_OK;
+  }
   if (M > kGemvMaxM || N % 4 || K % 4 || lda % 4 || ((uintptr_t)A & 15) || ((uintptr_t)Wk & 15) ||
       (lnf && !lnd))
     return fail(ctx, MB_ERR_ARG, "k-major gemv shape/alignment unsupported (M %d N %d K %d)", M, N, K);
@@ -1641,10 +1670,10 @@ int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float
         if (lnf) {
           if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF)
             hipLaunchKernelGGL((k_gemv_k<E, true, MRv, KCv>), grid, dim3(256), 0, ctx->stream, A,
-                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd);
+                               lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, PickIn{});
         } else {
           hipLaunchKernelGGL((k_gemv_k<E, false, MRv, KCv>), grid, dim3(256), 0, ctx->stream, A,
-                             lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd);
+                             lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, PickIn{});
         }
       };
       if constexpr (MRv == 1) {
@@ -1810,12 +1839,13 @@ int launch_gemv_k_parts(mb_ctx* ctx, int epi, const float* part, int nwp, const 
 // contiguous per load), with the matching two float4 of every A row (and of
 // gamma with GAM), all issued before the first multiply-add.  The LayerNorm
 // sums of LNF are taken over the raw rows, as in k_gemv_k.
-template <int EPI, bool LNF, bool GAM, int MR, int KC = 0>
+template <int EPI, bool LNF, bool GAM, int MR, int KC = 0, bool PICK = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void k_gemv_k16(
     const float* __restrict__ A, int64_t lda, const uint16_t* __restrict__ Wk, int N, int K,
     const float* __restrict__ bias, float* __restrict__ Cm, int64_t ldc, int M,
     const float* __restrict__ lnc, const float* __restrict__ lnd,
-    const float* __restrict__ gamma) {
+    const float* __restrict__ gamma, PickIn pk) {
+  static_assert(!PICK || (MR == 1 && KC == D && LNF && EPI == EPI_STORE), "PICK: one row of 768");
   constexpr int RI = MR <= 2 ? 6 : MR <= 4 ? 3 : 2;  // k steps (512 each) per round of loads
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n = blockIdx.x * 4 + wave;
@@ -1833,22 +1863,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 #pragma unroll
   for (int m = 0; m < MR; m++) {
     acc[m] = s1[m] = s2[m] = 0.f;
-    x0[m] = LNF ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
+    x0[m] = LNF && !PICK ? A[(int64_t)min(m, M - 1) * lda] : 0.f;
   }
+  const float* Ar = A;  // PICK: the chosen code's embedding row
   const int Kx = KC > 0 ? KC : K;  // a constant where the launch fixed it
-  auto step_load = [&](int st, uint4& w, float4* g, float4 (*a)[2]) {
+  auto load_w = [&](int st, uint4& w, float4* g) {
     const int k = min(st * 512 + 8 * lane, Kx - 8);
     w = *(const uint4*)(wp + k);
     if (GAM) {
       g[0] = *(const float4*)(gamma + k);
       g[1] = *(const float4*)(gamma + k + 4);
     }
+  };
+  auto load_a = [&](int st, float4 (*a)[2]) {
+    const int k = min(st * 512 + 8 * lane, Kx - 8);
 #pragma unroll
     for (int m = 0; m < MR; m++) {
-      const float* ar = A + (int64_t)min(m, M - 1) * lda + k;
+      const float* ar = Ar + (int64_t)min(m, M - 1) * lda + k;
       a[m][0] = *(const float4*)ar;
       a[m][1] = *(const float4*)(ar + 4);
     }
+  };
+  auto step_load = [&](int st, uint4& w, float4* g, float4 (*a)[2]) {
+    load_w(st, w, g);
+    load_a(st, a);
   };
   // lanes past K (only in a last, partial step) add zeros, with no branch
   auto step_mac = [&](int st, const uint4& w, const float4* g, const float4 (*a)[2]) {
@@ -1882,13 +1920,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   if constexpr (KC > 0) {
     constexpr int SPR = (KC + 511) / 512;
     constexpr int RK = SPR < RI ? SPR : RI;
+    static_assert(!PICK || RK == SPR, "PICK: one round of loads");
     static_for<(SPR + RK - 1) / RK>([&](auto r_) {
       constexpr int r = decltype(r_)::value;
       constexpr int NI = (r + 1) * RK <= SPR ? RK : SPR - r * RK;
       uint4 w[NI];
       float4 g[NI][2], a[NI][MR][2];
+      if constexpr (PICK) {
+        // as in k_gemv_k: the choice's logits, the weights, the choice, the row
+        const ChoiceIn c = pick_load(pk, lane);
 #pragma unroll
-      for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], g[i], a[i]);
+        for (int i = 0; i < NI; i++) load_w(i, w[i], g[i]);
+        Ar = pick_row(pk, c, lane, blockIdx.x == 0 && wave == 0);
+        x0[0] = Ar[0];
+#pragma unroll
+        for (int i = 0; i < NI; i++) load_a(i, a[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < NI; i++) step_load(r * RK + i, w[i], g[i], a[i]);
+      }
       asm volatile("" ::: "memory");  // the round's loads stay in front, none sunk into a branch
 #pragma unroll
       for (int i = 0; i < NI; i++) step_mac(r * RK + i, w[i], g[i], a[i]);
@@ -1947,9 +1997,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 
 int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint16_t* Wk,
                     int N, int K, const float* bias, float* Cm, int64_t ldc, int M,
-                    const float* lnc, const float* lnd, const float* gamma) {
+                    const float* lnc, const float* lnd, const float* gamma,
+                    const PickIn* pick) {
   if (M <= 0) return MB_OK;
   const bool lnf = lnc != nullptr;
+  if (pick) {
+    if (M != 1 || K != D || !lnf || !lnd || epi != EPI_STORE || N % 4 || ((uintptr_t)Wk & 15) ||
+        ((uintptr_t)gamma & 15))
+      return fail(ctx, MB_ERR_ARG, "gemv with the code choice: one row of %d, folded LayerNorm "
+                  "(M %d N %d K %d)", D, M, N, K);
+    if (gamma)
+      hipLaunchKernelGGL((k_gemv_k16<EPI_STORE, true, true, 1, D, true>), dim3((unsigned)(N / 4)),
+                         dim3(256), 0, ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd,
+                         gamma, *pick);
+    else
+      hipLaunchKernelGGL((k_gemv_k16<EPI_STORE, true, false, 1, D, true>), dim3((unsigned)(N / 4)),
+                         dim3(256), 0, ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd,
+                         gamma, *pick);
+    MB_HIP(ctx, hipGetLastError());
+    return MB_OK;
+  }
   if (M > kGemvMaxM || N % 4 || K % 8 || lda % 4 || ((uintptr_t)A & 15) || ((uintptr_t)Wk & 15) ||
       ((uintptr_t)gamma & 15) || (lnf && !lnd))
     return fail(ctx, MB_ERR_ARG, "bf16 k-major gemv shape/alignment unsupported (M %d N %d K %d)", M, N, K);
@@ -1967,14 +2034,14 @@ int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uin
           if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF) {
             if (gamma)
               hipLaunchKernelGGL((k_gemv_k16<E, true, true, MRv, KCv>), grid, dim3(256), 0,
-                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
             else
               hipLaunchKernelGGL((k_gemv_k16<E, true, false, MRv, KCv>), grid, dim3(256), 0,
-                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
           }
         } else {
           hipLaunchKernelGGL((k_gemv_k16<E, false, false, MRv, KCv>), grid, dim3(256), 0,
-                             ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma);
+                             ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
         }
       };
       if constexpr (MRv == 1) {

@@ -2,6 +2,7 @@
 // local head's embeddings, the continue/stop text-head decision, greedy
 // argmax with the repetition penalty, and frame-row feedback.
 #include "mb_internal.h"
+#include "pick.h"
 
 namespace mb {
 
@@ -225,94 +226,48 @@ int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, in
   return MB_OK;
 }
 
-// Greedy argmax over 1024 logits with the HuggingFace repetition penalty on
-// this channel's seen set: a seen id's score is multiplied by the penalty
-// when negative and divided when not (argmaxWithRepetitionPenalty,
-// policy.ts:273-290; ARGMAX_PENALTY, kernels-decode.ts:428-478).  Penalty
-// and score are doubles, as the JS numbers of the reference's CPU path are
-// (audio_repetition_penalty is the double 1.2, mossTtsRuntime.js:506-521);
-// with `f32` (wave-uniform) they are f32, as in the WGSL engine: the penalty
-// rounded to f32 and a correctly rounded f32 multiply or divide (taken in
-// double and rounded once to f32, which for a product or quotient of two
-// floats is the correctly rounded f32 result, since 53 >= 2 * 24 + 2), whose
-// result the double compare then orders exactly as an f32 compare would.  Strict '>' keeps the lowest id on ties and a
-// NaN never wins.  The winner goes to tokens[b][ch]; the seen bit is set only
-// for sequences that continue (the reference stops before drawing codes).
-// One wave per sequence.  Lane l takes ids 16l .. 16l+15: four 16-byte logit
-// loads and the one seen-mask word that holds their 16 bits, all issued up
-// front; the penalised values are compared in double (policy.ts:273-290 works
-// on JS numbers) with strict > so the lowest id wins a tie, within the lane
-// (ascending ids) and across lanes (the lower id on equal values).  With
-// `x`, the wave also writes the next step's input row, next_emb[winner]
-// (EMBED_ROW_LOCAL mode 2: the next step embeds this channel's code).
+// The greedy code choice of channel `ch` for every sequence: the penalised
+// argmax of its 1024 logits (choice_load / choice_take, pick.h) goes to tokens[b][ch],
+// and the seen bit is set only for sequences that continue (the reference
+// stops before drawing codes).  One wave per sequence; the seen word the
+// update changes is already in a register, so the update is a store with no
+// load in front of it.  With `x`, the wave also writes the next step's input
+// row, next_emb[winner] (EMBED_ROW_LOCAL mode 2: the next step embeds this
+// channel's code).  Channels rec0 .. ch-1 were picked by the one-row
+// projections of the steps after them (PickIn, pick.h), which only read the
+// seen sets: their winners, already in tokens, are recorded here.
 __global__ __launch_bounds__(256) void k_argmax_penalty(const float* __restrict__ logits, int B,
-                                                        int ch, double penalty, int f32,
+                                                        int ch, int rec0, double penalty, int f32,
                                                         uint32_t* __restrict__ seen,
                                                         const int32_t* __restrict__ cont,
                                                         int32_t* __restrict__ tokens,
                                                         const float* __restrict__ next_emb,
                                                         float* __restrict__ x) {
-  static_assert(CODES == 64 * 16, "one wave covers the codebook, 16 ids per lane");
   const int lane = threadIdx.x & 63;
   const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= B) return;
   uint32_t* sm = seen + ((int64_t)b * NVQ + ch) * 32;
-  const float4* lp = (const float4*)(logits + (int64_t)b * CODES + 16 * lane);
-  float v[16];
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const float4 t = lp[q];
-    v[4 * q] = t.x; v[4 * q + 1] = t.y; v[4 * q + 2] = t.z; v[4 * q + 3] = t.w;
-  }
-  const uint32_t word = sm[lane >> 1];
   const bool go_on = !cont || cont[b];  // loaded with the logits, not after the choice
-  const uint32_t bits = (word >> (16 * (lane & 1))) & 0xffffu;
-  // the penalty applies once the channel has emitted anything (policy.ts:282)
-  const bool any = __ballot(word != 0u) != 0ull;
-  const bool apply = any && penalty != 1.0;
-  double best = -INFINITY;
-  int idx = 0x7fffffff;
-  const float pf = (float)penalty;
-#pragma unroll
-  for (int j = 0; j < 16; j++) {
-    double s = v[j];
-    if (apply && ((bits >> j) & 1u)) {
-      if (f32)  // f32 result: the double product / quotient of two floats rounded once
-        s = (double)(float)(v[j] < 0.f ? (double)v[j] * (double)pf : (double)v[j] / (double)pf);
-      else
-        s = s < 0 ? s * penalty : s / penalty;
-    }
-    if (s > best) {
-      best = s;
-      idx = 16 * lane + j;
-    }
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const double ob = __shfl_xor(best, off);
-    const int oi = __shfl_xor(idx, off);
-    if (ob > best || (ob == best && oi < idx)) {
-      best = ob;
-      idx = oi;
-    }
-  }
-  // the butterfly leaves every lane with the same winner; the seen word it
-  // updates is already in a register (lanes 2w and 2w + 1 hold word w), so
-  // the update is a store with no load in front of it
-  const int tok = idx == 0x7fffffff ? 0 : idx;
-  const uint32_t wtok = __shfl(word, (tok >> 5) * 2);
+  const int rt = lane >= rec0 && lane < ch ? tokens[b * NVQ + lane] : 0;
+  const ChoiceIn c = choice_load(logits + (int64_t)b * CODES, sm, lane);
+  const int tok = choice_take(c, penalty, f32, lane);
+  const uint32_t wtok = __shfl(c.word, (tok >> 5) * 2);
   if (lane == 0) {
     tokens[b * NVQ + ch] = tok;
     if (go_on) sm[tok >> 5] = wtok | (1u << (tok & 31));
   }
+  if (go_on && lane >= rec0 && lane < ch)
+    seen[((int64_t)b * NVQ + lane) * 32 + (rt >> 5)] |= 1u << (rt & 31);
   if (x) copy_row(next_emb, tok, x, b, lane);
 }
 
-int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
-                          bool penalty_f32, uint32_t* seen, const int32_t* cont, int32_t* tokens,
-                          const float* next_emb, float* x) {
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, int rec0,
+                          double penalty, bool penalty_f32, uint32_t* seen, const int32_t* cont,
+                          int32_t* tokens, const float* next_emb, float* x) {
+  if (rec0 < 0 || rec0 > ch) return fail(ctx, MB_ERR_ARG, "channels %d .. %d to record", rec0, ch);
   hipLaunchKernelGGL(k_argmax_penalty, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, ctx->stream,
-                     logits, B, ch, penalty, (int)penalty_f32, seen, cont, tokens, next_emb, x);
+                     logits, B, ch, rec0, penalty, (int)penalty_f32, seen, cont, tokens, next_emb,
+                     x);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

@@ -328,9 +328,13 @@ int launch_kmajor_w(mb_ctx* ctx, const float* W, int K, int N, const float* gamm
 // C = epi(A Wk^T + bias) for M <= kGemvMaxM rows on a k-major weight copy;
 // with lnc (and lnd) the rows are the raw residual stream and the LayerNorm
 // is folded in (c, d from launch_fold_ln, Wk from launch_kmajor_w with gamma).
+// With `pick` (one row, K = 768, a folded LayerNorm, EPI_STORE) the row is
+// not read from A: the launch makes the previous audio channel's greedy
+// choice itself and takes that code's embedding row (PickIn, pick.h).
+struct PickIn;
 int launch_gemv_k(mb_ctx* ctx, int epi, const float* A, int64_t lda, const float* Wk, int N, int K,
                   const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
-                  const float* lnd);
+                  const float* lnd, const PickIn* pick = nullptr);
 
 // LayerNorm folded into the projection after it: Wg, c, d from
 // launch_fold_ln (Wg column-block-major, as launch_tile_w writes it);
@@ -370,7 +374,8 @@ int launch_round_bf16(mb_ctx* ctx, const float* W, int64_t n, float* Wr);
 int launch_kmajor_w16(mb_ctx* ctx, const float* W, int K, int N, uint16_t* Wk);
 int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uint16_t* Wk,
                     int N, int K, const float* bias, float* Cm, int64_t ldc, int M,
-                    const float* lnc, const float* lnd, const float* gamma);
+                    const float* lnc, const float* lnd, const float* gamma,
+                    const PickIn* pick = nullptr);
 int launch_split_w1(mb_ctx* ctx, const float* Wt, int K, int N, void* Wx, bool tiled = true);
 int launch_gemm_x2(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* Wx1, int N,
                    int K, const float* bias, float* Cm, int64_t ldc, int M, const float* lnc,
@@ -390,9 +395,9 @@ int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assis
 int launch_text_decide(mb_ctx* ctx, const float* h, int B, const float* head, int vocab, int end_id,
                        int assistant_id, const int32_t* alive, int32_t* cont,
                        const float* wte = nullptr, float* x = nullptr, double* te = nullptr);
-int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, double penalty,
-                          bool penalty_f32, uint32_t* seen, const int32_t* cont, int32_t* tokens,
-                          const float* next_emb = nullptr, float* x = nullptr);
+int launch_argmax_penalty(mb_ctx* ctx, const float* logits, int B, int ch, int rec0,
+                          double penalty, bool penalty_f32, uint32_t* seen, const int32_t* cont,
+                          int32_t* tokens, const float* next_emb = nullptr, float* x = nullptr);
 int launch_frame_rows(mb_ctx* ctx, const int32_t* tokens, int B, int assistant_id, int32_t* rows17);
 int launch_frame_emit(mb_ctx* ctx, const int32_t* tokens, const int32_t* cont, int B,
                       int32_t* frame_idx, int32_t* codes, int32_t* cont_out, int32_t* pos,

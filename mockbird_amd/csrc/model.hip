@@ -8,6 +8,7 @@
 #include <cstring>
 
 #include "mb_internal.h"
+#include "pick.h"
 
 namespace mb {
 
@@ -130,11 +131,11 @@ int fold_layer(mb_ctx* ctx, const std::string& key, LayerW& w) {
 // `gamma` is the folded LayerNorm's (used with lnc under bf16 storage).
 int proj_gemv(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* wk, int N, int K,
               const float* bias, float* C, int64_t ldc, int M, const float* lnc, const float* lnd,
-              const float* gamma) {
+              const float* gamma, const PickIn* pick = nullptr) {
   if (ctx->w_bf16)
     return launch_gemv_k16(ctx, epi, A, lda, (const uint16_t*)wk, N, K, bias, C, ldc, M, lnc, lnd,
-                           lnc ? gamma : nullptr);
-  return launch_gemv_k(ctx, epi, A, lda, (const float*)wk, N, K, bias, C, ldc, M, lnc, lnd);
+                           lnc ? gamma : nullptr, pick);
+  return launch_gemv_k(ctx, epi, A, lda, (const float*)wk, N, K, bias, C, ldc, M, lnc, lnd, pick);
 }
 int proj_split(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void* wx, int N, int K,
                const float* bias, float* C, int64_t ldc, int M, const float* lnc, const float* lnd,
@@ -224,10 +225,11 @@ int cancelled(mb_ctx* ctx) {
 
 // One d=768 layer over M rows held in a.x.  Rows belong to B sequences with
 // n_rows[b] rows at positions pos0[b] + r (packed by `packed` when prefill is
-// set, else one row per sequence).
+// set, else one row per sequence).  With `pick` (one row) the QKV projection
+// makes the previous channel's code choice and writes a.x itself.
 int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int rows_max, int64_t M,
               const int32_t* pos0, const int32_t* n_rows, const int32_t* row_off, bool prefill,
-              int64_t max_valid, Act& a, int pos_const = -1) {
+              int64_t max_valid, Act& a, int pos_const = -1, const PickIn* pick = nullptr) {
   int rc;
   // decode-sized M: each LayerNorm is folded into the projection after it;
   // up to kGemvMaxM rows the projections read the k-major copies
@@ -237,9 +239,12 @@ int run_layer(mb_ctx* ctx, const LayerW& w, const RingView& ring, int B, int row
   // products, the LayerNorm folded in (the streaming kernel at decode sizes,
   // the tiled one at prefill sizes)
   const bool x3 = !gemv && w.attn_wx;
+  if (pick && !(gemv && M == 1))
+    return fail(ctx, MB_ERR_STATE, "the code choice rides on a one-row projection (M %lld)",
+                (long long)M);
   if (gemv) {
     if ((rc = proj_gemv(ctx, EPI_STORE, a.x, D, w.attn_wk, QKV, D, w.attn_b, a.qkv, QKV,
-                        (int)M, w.attn_c, w.attn_d, w.ln1_w)))
+                        (int)M, w.attn_c, w.attn_d, w.ln1_w, pick)))
       return rc;
   } else if (x3) {
     if ((rc = proj_split(ctx, EPI_STORE, a.x, D, w.attn_wx, QKV, D, w.attn_b, a.qkv, QKV,
@@ -426,6 +431,12 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
   const RingView ring = local_ring(ctx);
   const int64_t S = ctx->cfg.max_seqs;
   const bool heads = pick || probe;
+  // One voice: the code choice of every channel but the last is made by the
+  // next step's QKV projection (PickIn), not by a launch of its own; the
+  // last channel's argmax launch records them all in the seen sets.
+  const bool fuse = pick && B == 1;
+  PickIn pending{};
+  bool have_pending = false;
   for (int step = 0; step <= last_step; step++) {
     if ((rc = cancelled(ctx))) return rc;
     // picking, the previous step's decision kernel already wrote this step's
@@ -438,8 +449,9 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
       return rc;
     // (every voice's local step sits at position `step`)
     if ((rc = run_layer(ctx, m.local, ring, B, 1, B, ctx->local_pos + (int64_t)step * S, nullptr,
-                        nullptr, false, step + 1, a, step)))
+                        nullptr, false, step + 1, a, step, have_pending ? &pending : nullptr)))
       return rc;
+    have_pending = false;
     // the audio heads take ln_f folded in (decode-sized B); the text decision
     // and the step probe read ln_f itself
     const bool folded_head = heads && step > 0 && B < kFoldMaxM;
@@ -470,11 +482,16 @@ int local_steps(mb_ctx* ctx, int B, const float* hidden, int last_step, bool pic
         rc = launch_gemm(ctx, EPI_STORE, a.norm, D, m.audio_heads.t[ch], CODES, D, nullptr, lg, ldl,
                          B);
       if (rc) return rc;
-      if (pick)
-        rc = launch_argmax_penalty(ctx, a.logits, B, ch, ctx->penalty, ctx->penalty_f32, ctx->seen,
-                                   ctx->cont,
-                                   ctx->tokens, embed_next ? m.audio_emb.t[ch] : nullptr,
+      if (pick && fuse && embed_next) {
+        pending = PickIn{a.logits, ctx->seen, ctx->tokens, m.audio_emb.t[ch], a.x, ctx->penalty,
+                         ch, (int)ctx->penalty_f32};
+        have_pending = true;
+      } else if (pick) {
+        rc = launch_argmax_penalty(ctx, a.logits, B, ch, fuse ? 0 : ch, ctx->penalty,
+                                   ctx->penalty_f32, ctx->seen, ctx->cont, ctx->tokens,
+                                   embed_next ? m.audio_emb.t[ch] : nullptr,
                                    embed_next ? a.x : nullptr);
+      }
     }
     if (rc) return rc;
   }

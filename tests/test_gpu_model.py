@@ -308,6 +308,13 @@ def _crafted_head_weights(hi=3, lo=5):
     decision is text_head[0][9] = 1 against text_head[0][7] = 0 (always go
     on).  Row 0 of every head holds 1.0 at id `hi`, fp32(0.8333333) at id
     `lo`, 0.81 at id 11 and -1 elsewhere."""
+    row = np.full(1024, -1.0, np.float32)
+    row[hi], row[lo], row[11] = 1.0, np.float32(0.8333333), 0.81
+    return _row_head_weights(row), row
+
+
+def _row_head_weights(row):
+    """_crafted_head_weights' model with `row` as every audio head's logits."""
     w = synth.model_weights(n_layers=2, vocab=64, seed=5)
     w["model.local_transformer.ln_f.weight"] = np.zeros(768, np.float32)
     e0 = np.zeros(768, np.float32)
@@ -315,11 +322,9 @@ def _crafted_head_weights(hi=3, lo=5):
     w["model.local_transformer.ln_f.bias"] = e0
     th = w["model.text_lm_head.weight"]
     th[0, 7], th[0, 9] = 0.0, 1.0
-    row = np.full(1024, -1.0, np.float32)
-    row[hi], row[lo], row[11] = 1.0, np.float32(0.8333333), 0.81
     for k in range(16):
         w[f"model.audio_lm_heads.{k}.weight"][0] = row
-    return w, row
+    return w
 
 
 def _expected_codes(row, n_frames, penalty, seen, f32=False):
@@ -331,7 +336,8 @@ def _expected_codes(row, n_frames, penalty, seen, f32=False):
     return out
 
 
-def test_penalty_is_the_double_and_settings_reach_the_frame_graph():
+@pytest.mark.parametrize("B", [1, 2])
+def test_penalty_is_the_double_and_settings_reach_the_frame_graph(B):
     """The repetition penalty is applied as the double 1.2: after id 3 (logit
     1.0) is drawn, 1.0 / 1.2 = 0.83333333 still beats id 5's fp32(0.8333333)
     = 0.83333331, which 1.0 / 1.2f = 0.83333330 would not.  Then the penalty
@@ -349,7 +355,6 @@ def test_penalty_is_the_double_and_settings_reach_the_frame_graph():
     assert want2 == [5, 11, 3]
     stale = _expected_codes(row, 2, 1.2, {3, 5})
     assert stale[0] == 3  # what a replay with the old penalty would pick
-    B = 2
     ids, n = _prompt_batch(B, 64, 90)
     with _ctx(w, 2, 64, B, 64) as ctx:
         h = ctx.prefill(ids, n)
@@ -372,7 +377,8 @@ def test_penalty_is_the_double_and_settings_reach_the_frame_graph():
             pos = pos + 1
 
 
-def test_penalty_precision_f32_is_the_wgsl_arithmetic():
+@pytest.mark.parametrize("B", [1, 2])
+def test_penalty_precision_f32_is_the_wgsl_arithmetic(B):
     """MB_PENALTY_F32, the WGSL engine's arithmetic (kernels-decode.ts:454-461):
     id 5 holds 1.0 and id 3 fp32(0.8333333).  Once 5 has been drawn, its f32
     penalised score 1.0 / 1.2f rounds to exactly fp32(0.8333333), a tie that
@@ -387,7 +393,6 @@ def test_penalty_precision_f32_is_the_wgsl_arithmetic():
     want64 = _expected_codes(row, 3, 1.2, set())
     want32 = _expected_codes(row, 3, 1.2, set(), f32=True)
     assert want64[:2] == [5, 5] and want32[:2] == [5, 3]  # the case discriminates
-    B = 2
     ids, n = _prompt_batch(B, 64, 90)
     with _ctx(w, 2, 64, B, 64) as ctx:
         h = ctx.prefill(ids, n)
@@ -410,6 +415,38 @@ def test_penalty_precision_f32_is_the_wgsl_arithmetic():
             codes, cont = ref.local_frame(h)
             assert (codes == want32[f]).all(), (f, codes)
             h = ref.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
+            pos = pos + 1
+
+
+@pytest.mark.parametrize("B,f32", [(1, False), (1, True), (2, False)])
+def test_code_choice_ties_nan_and_penalised_candidates(B, f32):
+    """The greedy choice on a crafted row (every channel's logits): 2.0 at ids
+    40 and 41 (one lane's ids) and 700 (another lane's), 1.7 at 300, NaN at
+    ids 5 and 1000, -3e38 elsewhere.  Frame by frame the lowest id of the
+    highest score wins, a NaN never does, the seen ids' penalised scores
+    (2.0 / 1.2) tie each other across lanes and lose to 1.7 until it is seen
+    too: codes 40, 41, 700, 300, then 40 again.  One voice makes each choice
+    but the last inside the next step's projection, two voices in the argmax
+    launch; both follow the oracle's penalised argmax."""
+    say(f"code choice: ties, NaN, penalised candidates (B={B}, f32={f32})")
+    row = np.full(1024, -3e38, np.float32)
+    row[[40, 41, 700]] = 2.0
+    row[300] = 1.7
+    row[[5, 1000]] = np.nan
+    w = _row_head_weights(row)
+    frames = 6
+    want = _expected_codes(row, frames, 1.2, set(), f32=f32)
+    assert want == [40, 41, 700, 300, 40, 40], want  # the row discriminates
+    ids, n = _prompt_batch(B, 64, 90)
+    with _ctx(w, 2, 64, B, 64) as ctx:
+        if f32:
+            ctx.set_penalty_precision(mb.MB_PENALTY_F32)
+        h = ctx.prefill(ids, n)
+        pos = n.copy()
+        for f in range(frames):
+            codes, cont = ctx.local_frame(h)
+            assert cont.all() and (codes == want[f]).all(), (f, codes)
+            h = ctx.decode_step(np.stack([synth.frame_row(c) for c in codes]), pos)
             pos = pos + 1
 
 
