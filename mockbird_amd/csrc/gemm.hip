@@ -2034,14 +2034,17 @@ int launch_gemv_k16(mb_ctx* ctx, int epi, const float* A, int64_t lda, const uin
           if constexpr (E == EPI_STORE || E == EPI_GELU || E == EPI_GELU_ERF) {
             if (gamma)
               hipLaunchKernelGGL((k_gemv_k16<E, true, true, MRv, KCv>), grid, dim3(256), 0,
-                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma,
+                                 PickIn{});
             else
               hipLaunchKernelGGL((k_gemv_k16<E, true, false, MRv, KCv>), grid, dim3(256), 0,
-                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
+                                 ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma,
+                                 PickIn{});
           }
         } else {
           hipLaunchKernelGGL((k_gemv_k16<E, false, false, MRv, KCv>), grid, dim3(256), 0,
-                             ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma, PickIn{});
+                             ctx->stream, A, lda, Wk, N, K, bias, Cm, ldc, M, lnc, lnd, gamma,
+                             PickIn{});
         }
       };
       if constexpr (MRv == 1) {
