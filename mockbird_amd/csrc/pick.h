@@ -117,7 +117,8 @@ __device__ __forceinline__ int choice_take(const ChoiceIn& c, double penalty, in
 // first wave also writes the winner to tokens[ch] and the row to x (the
 // step's residual).  The seen set is only read here: the launch that picks
 // the frame's last channel records these channels' winners (each channel's
-// set is read by that channel's choice alone, once per frame).
+// set is read by that channel's choice alone, once per frame).  A frame that
+// a cancellation cuts short therefore records none of its choices.
 struct PickIn {
   const float* logits;   // [1024]: channel ch's audio-head logits
   const uint32_t* seen;  // [NVQ][32]: the voice's seen sets
