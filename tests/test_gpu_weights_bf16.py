@@ -220,3 +220,46 @@ def test_weight_storage_switches_back():
         with pytest.raises(mb.MbError) as e:
             ctx.set_weight_storage(7)
         assert e.value.code == mb.MB_ERR_ARG
+
+
+def test_bf16_weights_c0_single_voice_60_frames():
+    """The benchmark's one-voice frame with bf16 storage at full size: 12
+    layers, vocab 32000, the 281-row voice-clone prompt, ring 1024 (fp32
+    K/V), 60 greedy frames per call.  Each frame runs the global layers'
+    attention as per-wave partials merged by the O projection and makes the
+    code choices of channels 0-14 inside the next local step's QKV
+    projection; every code, logit and hidden state is compared with the
+    oracle on the rounded weights."""
+    say("bf16 weights, C0 size: prefill 281 rows + 60 frames, B=1")
+    w = synth.model_weights(n_layers=12, vocab=32000, seed=0)
+    w["model.text_lm_head.weight"][:, 9] = w["model.text_lm_head.weight"][:, 7]  # never ends
+    m = oracle.Model(rounded_weights(w), n_layers=12, vocab=32000)
+    rows = synth.prompt(0, n_frames=150, n_text=128, vocab=32000)
+    st = oracle.ModelState(m, 1, 1024)
+    h_or = st.prefill_all(0, rows)[-1][None]
+    chk = FrameCheck(1)
+    tol = TOL[mb.MB_KV_F32]
+    with mb.Context(n_layers=12, capacity=1024, max_seqs=1, max_rows=512, vocab=32000) as ctx:
+        ctx.upload_all(w)
+        ctx.set_weight_storage(mb.MB_W_BF16)
+        h = ctx.prefill(rows[None], [rows.shape[0]])
+        max_h = float(np.abs(h - h_or).max())
+        assert max_h < tol
+        pos = rows.shape[0]
+        for f in range(60):
+            codes, cont = ctx.local_frame(h)
+            g_text, g_logits = ctx.local_logits(h, codes)
+            o_text, o_logits = m.local_logits(h_or[0], codes[0])
+            chk.frame(0, f"frame {f}", codes[0], cont[0], o_text, o_logits, tol, g_text[0],
+                      g_logits[0])
+            assert cont[0]
+            row = synth.frame_row(codes[0])[None]
+            h = ctx.decode_step(row, [pos])
+            h_or = st.decode_step(row, [pos])
+            d = float(np.abs(h - h_or).max())
+            max_h = max(max_h, d)
+            assert d < tol, f
+            pos += 1
+    chk.summary("bf16 weights C0")
+    say(f"  bf16 weights C0: max |hidden diff| {max_h:.2e}")
+    assert chk.codes_equal + chk.codes_tied == 960
