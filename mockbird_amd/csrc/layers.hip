@@ -79,18 +79,23 @@ int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* sr
 // summed in fp32 in channel order (EMBED_ROWS, kernels-batch.ts:45-92;
 // embedRowFor, promptRows.ts:21-36).  An id outside its table contributes
 // nothing (the host rejects such ids before launching).
+// With `codes` (ids null) row b is the frame row [assistant_id, codes[b][0..15]]
+// (buildFrameRow, policy.ts:83-88) read from the chosen codes directly.
 __global__ __launch_bounds__(256) void k_embed_rows(const int32_t* __restrict__ ids, int M,
                                                     const float* __restrict__ wte, int vocab,
-                                                    AudioTables audio, float* __restrict__ x) {
+                                                    AudioTables audio, float* __restrict__ x,
+                                                    const int32_t* __restrict__ codes,
+                                                    int assistant_id) {
   const int row = blockIdx.x;
   if (row >= M) return;
-  const int32_t* id = ids + (int64_t)row * ROW;
+  // the row's 16 audio ids: ids[row][1..16], or the row's chosen codes
+  const int32_t* aid = ids ? ids + (int64_t)row * ROW + 1 : codes + (int64_t)row * NVQ;
   // Every table read is issued before the first add (ids clamped into their
   // tables, the skipped ones then left out of the sum), so a row costs one
   // memory round trip, not one per channel; the sum keeps channel order.
   static_assert(D % 256 == 0, "whole rows per block");
   constexpr int DI = D / 256;
-  const int t = id[0];
+  const int t = ids ? ids[(int64_t)row * ROW] : assistant_id;
   const bool tv = t >= 0 && t < vocab;
   const int tc = tv ? t : 0;
   float tw[DI], av[NVQ][DI];
@@ -99,7 +104,7 @@ __global__ __launch_bounds__(256) void k_embed_rows(const int32_t* __restrict__ 
   bool ok[NVQ];
 #pragma unroll
   for (int k = 0; k < NVQ; k++) {
-    const int a = id[1 + k];
+    const int a = aid[k];
     ok[k] = a != PAD && a >= 0 && a < CODES;
     const int ac = ok[k] ? a : 0;
 #pragma unroll
@@ -115,10 +120,11 @@ __global__ __launch_bounds__(256) void k_embed_rows(const int32_t* __restrict__ 
 }
 
 int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, int vocab,
-                      const AudioTables& audio, float* x) {
+                      const AudioTables& audio, float* x, const int32_t* codes, int assistant_id) {
   if (M <= 0) return MB_OK;
+  if (!ids == !codes) return fail(ctx, MB_ERR_ARG, "frame rows come from ids or from codes");
   hipLaunchKernelGGL(k_embed_rows, dim3((unsigned)M), dim3(256), 0, ctx->stream, ids, M, wte, vocab,
-                     audio, x);
+                     audio, x, codes, assistant_id);
   MB_HIP(ctx, hipGetLastError());
   return MB_OK;
 }

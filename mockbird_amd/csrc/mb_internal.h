@@ -384,8 +384,11 @@ int launch_gemm_x2(mb_ctx* ctx, int epi, const float* A, int64_t lda, const void
 // layers.hip
 int launch_layernorm(mb_ctx* ctx, const float* x, int64_t ldx, const int32_t* src_row, int M,
                      const float* w, const float* b, float* y, int64_t ldy, int width = D);
+// x[row] = the row's embedding sum, the row being ids[row] (17 ids) or, with
+// ids null, the frame row [assistant_id, codes[row][0..15]].
 int launch_embed_rows(mb_ctx* ctx, const int32_t* ids, int M, const float* wte, int vocab,
-                      const AudioTables& audio, float* x);
+                      const AudioTables& audio, float* x, const int32_t* codes = nullptr,
+                      int assistant_id = 0);
 int launch_embed_local(mb_ctx* ctx, int step, int B, const float* wte, int assistant_id,
                        const AudioTables& audio, const int32_t* tokens, float* x);
 // With x non-null, text_decide also writes wte[assistant_id] to x[b] (step

@@ -387,14 +387,17 @@ int check_ids(mb_ctx* ctx, const int32_t* ids, int64_t rows) {
   return MB_OK;
 }
 
-// Global decode step on device buffers (rows17, pos, hidden all device).
+// Global decode step on device buffers (rows17, pos, hidden all device);
+// with rows17 null the rows are the frame rows of the codes in ctx->tokens.
 int decode_step(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t* pos, int64_t max_pos,
                 float* hidden) {
   int rc;
   Act a;
   if ((rc = activations(ctx, B, a))) return rc;
   const ModelW& m = ctx->model;
-  if ((rc = launch_embed_rows(ctx, rows17, B, m.wte, ctx->cfg.vocab, m.audio_emb, a.x))) return rc;
+  if ((rc = launch_embed_rows(ctx, rows17, B, m.wte, ctx->cfg.vocab, m.audio_emb, a.x,
+                              rows17 ? nullptr : ctx->tokens, ctx->assistant_id)))
+    return rc;
   for (int l = 0; l < ctx->cfg.n_layers; l++) {
     if ((rc = cancelled(ctx))) return rc;
     if ((rc = run_layer(ctx, m.layers[l], global_ring(ctx, l), B, 1, B, pos, nullptr, nullptr, false,
@@ -809,16 +812,16 @@ int mb_decode_step_dev(mb_ctx* ctx, int B, const int32_t* rows17, const int32_t*
 namespace mb {
 namespace {
 
-// One device-resident frame: local head on `hidden` -> frame rows, global
-// decode step of those rows at pos -> `hidden`, then the frame's codes and
-// flags to the outputs and pos += cont.
-int enqueue_frame(mb_ctx* ctx, int B, float* hidden, int32_t* pos, int32_t max_pos, int32_t* rows,
+// One device-resident frame: local head on `hidden` -> codes, global decode
+// step of their frame rows (embedded from the codes) at pos -> `hidden`,
+// then the frame's codes and flags to the outputs and pos += cont.
+int enqueue_frame(mb_ctx* ctx, int B, float* hidden, int32_t* pos, int32_t max_pos,
                   int32_t* frame_idx, int32_t* alive, int32_t* codes, int32_t* cont) {
   ctx->frame_alive = alive;
-  int rc = local_frame(ctx, B, hidden, nullptr, nullptr, rows);
+  int rc = local_frame(ctx, B, hidden, nullptr, nullptr, nullptr);
   ctx->frame_alive = nullptr;
   if (rc) return rc;
-  if ((rc = decode_step(ctx, B, rows, pos, max_pos, hidden))) return rc;
+  if ((rc = decode_step(ctx, B, nullptr, pos, max_pos, hidden))) return rc;
   return launch_frame_emit(ctx, ctx->tokens, ctx->cont, B, frame_idx, codes, cont, pos, alive);
 }
 
@@ -842,14 +845,13 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
   if ((rc = need_model(ctx))) return rc;
   if ((rc = cancelled(ctx))) return rc;
   int32_t* fidx = (int32_t*)scratch(ctx, "frame_idx", 4);
-  int32_t* rows = (int32_t*)scratch(ctx, "frame_rows", (size_t)B * ROW * 4);
   int32_t* alive = (int32_t*)scratch(ctx, "frame_alive", (size_t)B * 4);
-  if (!fidx || !rows || !alive) return fail(ctx, MB_ERR_NOMEM, "frame staging allocation failed");
+  if (!fidx || !alive) return fail(ctx, MB_ERR_NOMEM, "frame staging allocation failed");
   if ((rc = launch_fill_i32(ctx, fidx, 1, 0))) return rc;
   if ((rc = launch_fill_i32(ctx, alive, B, 1))) return rc;
   // Frame 0 runs eagerly: it sizes every scratch buffer the frame touches, so
   // nothing is allocated while the next frame is captured.
-  if ((rc = enqueue_frame(ctx, B, hidden, pos, max_pos, rows, fidx, alive, codes, cont))) return rc;
+  if ((rc = enqueue_frame(ctx, B, hidden, pos, max_pos, fidx, alive, codes, cont))) return rc;
   if (n_frames == 1) return MB_OK;
   const uint64_t key[8] = {(uint64_t)B, (uint64_t)max_pos, (uint64_t)(uintptr_t)hidden,
                            (uint64_t)(uintptr_t)pos, (uint64_t)(uintptr_t)codes,
@@ -865,7 +867,7 @@ int mb_decode_frames_dev(mb_ctx* ctx, int B, int n_frames, float* hidden, int32_
     const hipError_t eb = hipStreamBeginCapture(ctx->capture_stream, hipStreamCaptureModeThreadLocal);
     if (eb != hipSuccess) return hip_fail(ctx, eb, "hipStreamBeginCapture");
     ctx->stream = ctx->capture_stream;
-    rc = enqueue_frame(ctx, B, hidden, pos, max_pos, rows, fidx, alive, codes, cont);
+    rc = enqueue_frame(ctx, B, hidden, pos, max_pos, fidx, alive, codes, cont);
     hipGraph_t graph = nullptr;
     const hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
     ctx->stream = saved;
